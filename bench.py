@@ -1,0 +1,252 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention hot path; prints ONE JSON line.
+
+Headline (`value`): split-KV decode attention at BASELINE config 2 (MHA_Decode GQA,
+Llama-3-8B shape: B=16, 32 query / 8 KV heads, d=128, KV length 4096, fp16 cache,
+fp32 softmax/accumulate), as achieved HBM GB/s = algorithmic bytes / time, with the
+inputs resident in HBM.  One step = one call of the mha_decode_attn_f16_cuda operator,
+which is a single kernel launch (split-KV + fused LSE merge), so its event-timed average
+is that kernel's average duration (cross-checked by the rocprofv3 summary in profiles/).
+
+Also reported (`extra`): the full MHA_Decode op at config 2 (projections + append +
+attention + output projection), decode config 1 (FP32, GPT-2 small), config 4 (ragged
+long context), and fused prefill configs 3 (BERT-base) and 5 (causal GPT-2 medium) in
+TFLOP/s against the fp16 MFMA peak.  `cpu_baseline` times the CPU oracle (a C port of the
+reference fallback, single thread) on a bounded sample of the same decode workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "split-KV decode µs/step + HBM GB/s; fused MHA prefill TFLOP/s (fp16)"
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_op(cf, name, inputs, outputs, params, stream, steps, warmup, extra=()):
+    """Average ms per call over `steps` back-to-back calls on `stream`, timed by HIP
+    events in the library's C loop (operator_time), after `warmup` untimed calls."""
+    from cudaforge_amd.api import time_op as _t
+    return _t(name, inputs, outputs, params, stream, warmup, steps, extra_inputs=extra)
+
+
+def f16_normal(shape, seed, std=1.0):
+    import oracle as O
+    return O.to_f16(O.normal(shape, seed, 0.0, std))
+
+
+def bench_decode_core(cf, stream, steps, warmup):
+    B, H, H_kv, d, T = 16, 32, 8, 128, 4096
+    Q = cf.DeviceBuffer.from_numpy(f16_normal((B, H, d), 101))
+    K = cf.DeviceBuffer.from_numpy(f16_normal((B, T, H_kv, d), 102))
+    V = cf.DeviceBuffer.from_numpy(f16_normal((B, T, H_kv, d), 103))
+    O_ = cf.DeviceBuffer.empty((B, H, d), np.float16)
+    p = cf.MhaDecodeParams(B, H * d, H, H_kv, d, float(1 / np.sqrt(d)), T - 1, T)
+    ms = time_op(cf, "mha_decode_attn_f16_cuda", [Q, K, V], [O_], p, stream, steps, warmup)
+    kv_bytes = 2 * B * T * H_kv * d * 2
+    alg_bytes = kv_bytes + 2 * B * H * d * 2
+    return ms, alg_bytes, dict(B=B, H_q=H, H_kv=H_kv, d=d, kv_len=T)
+
+
+def bench_decode_full(cf, stream, steps, warmup, f16=True, B=16, H=32, H_kv=8, d=128, T=4096, seed=200):
+    D, kvd = H * d, H_kv * d
+    dt = np.float16 if f16 else np.float32
+
+    def mk(shape, s, std=1.0):
+        import oracle as O
+        a = O.normal(shape, seed + s, 0.0, std)
+        return cf.DeviceBuffer.from_numpy(O.to_f16(a) if f16 else a)
+
+    ins = [mk((B, 1, D), 1), mk((B, T, H_kv, d), 2), mk((B, T, H_kv, d), 3),
+           mk((D, D), 4, 0.02), cf.DeviceBuffer.from_numpy(np.zeros(D, dt)),
+           mk((D, kvd), 6, 0.02), cf.DeviceBuffer.from_numpy(np.zeros(kvd, dt)),
+           mk((D, kvd), 8, 0.02), cf.DeviceBuffer.from_numpy(np.zeros(kvd, dt)),
+           mk((D, D), 10, 0.02), cf.DeviceBuffer.from_numpy(np.zeros(D, dt))]
+    Y = cf.DeviceBuffer.empty((B, 1, D), dt)
+    p = cf.MhaDecodeParams(B, D, H, H_kv, d, float(1 / np.sqrt(d)), T - 1, T)
+    name = "mha_decode_f16_cuda" if f16 else "mha_decode_f32_cuda"
+    # In-place cache update (outputs alias the input caches), the decode-loop use.
+    ms = time_op(cf, name, ins, [Y, ins[1], ins[2]], p, stream, steps, warmup)
+    esz = 2 if f16 else 4
+    alg = (2 * B * T * kvd + (D * D * 2 + 2 * D * kvd) + 2 * D + 2 * kvd + 2 * B * D + 2 * B * kvd) * esz
+    return ms, alg
+
+
+def bench_decode_ragged(cf, stream, steps, warmup):
+    import oracle as O
+    B, H, H_kv, d, cap = 4, 32, 8, 128, 32768
+    lens = O.uniform_int(B, 404, 1024, cap) - 1        # cache_len_b; attended L_b = lens + 1
+    Q = cf.DeviceBuffer.from_numpy(f16_normal((B, H, d), 401))
+    K = cf.DeviceBuffer.from_numpy(f16_normal((B, cap, H_kv, d), 402))
+    V = cf.DeviceBuffer.from_numpy(f16_normal((B, cap, H_kv, d), 403))
+    L = cf.DeviceBuffer.from_numpy(lens.astype(np.int32))
+    O_ = cf.DeviceBuffer.empty((B, H, d), np.float16)
+    p = cf.MhaDecodeParams(B, H * d, H, H_kv, d, float(1 / np.sqrt(d)), -1, cap)
+    ms = time_op(cf, "mha_decode_attn_f16_cuda", [Q, K, V], [O_], p, stream, steps, warmup, extra=[L])
+    alg = int(4096 * int((lens + 1).sum()) + 2 * B * H * d * 2)
+    return ms, alg, [int(x) + 1 for x in lens]
+
+
+def bench_fused(cf, stream, steps, warmup, B, S, H, d, causal, seed):
+    D = H * d
+    mk = (lambda shape, s, std=1.0: cf.DeviceBuffer.from_numpy(f16_normal(shape, seed + s, std)))
+    zero = (lambda n: cf.DeviceBuffer.from_numpy(np.zeros(n, np.float16)))
+    ins = [mk((B, S, D), 1), None, mk((D, D), 2, 0.02), zero(D), mk((D, D), 3, 0.02), zero(D),
+           mk((D, D), 4, 0.02), zero(D), mk((D, D), 5, 0.02), zero(D)]
+    Y = cf.DeviceBuffer.empty((B, S, D), np.float16)
+    p = cf.MhaFusedParams(B, S, D, H, H, d, float(1 / np.sqrt(d)), False, causal)
+    ms = time_op(cf, "mha_fused_f16_cuda", ins, [Y], p, stream, steps, warmup)
+    proj = 2 * B * S * D * D * 4
+    pairs = B * H * (S * (S + 1) // 2 if causal else S * S)
+    flops = proj + 4 * pairs * d
+    return ms, flops
+
+
+def cpu_baseline_decode(budget_s: float):
+    """Oracle (C port of mha_decode.c's attention loop, single thread) on config-2 inputs,
+    on as many batch rows as fit the time budget; scaled to the full step."""
+    import oracle as O
+    B, H, H_kv, d, T = 16, 32, 8, 128, 4096
+    rows = 1
+    Q = O.round_f16(O.normal((rows, H, d), 101))
+    K = O.round_f16(O.normal((rows, T, H_kv, d), 102))
+    V = O.round_f16(O.normal((rows, T, H_kv, d), 103))
+    att = np.full(rows, T, np.int32)
+    scale = float(1 / np.sqrt(d))
+    t0 = O.now()
+    n = 0
+    while True:
+        O.decode_attn(Q, K, V, att, scale, H_kv)
+        n += 1
+        if O.now() - t0 >= budget_s:
+            break
+    per_row = (O.now() - t0) / n
+    step_s = per_row * B
+    alg_bytes = 2 * B * T * H_kv * d * 2 + 2 * B * H * d * 2
+    return {
+        "value": round(alg_bytes / step_s / 1e9, 3),
+        "unit": "GB/s",
+        "us_per_step": round(step_s * 1e6, 1),
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{n} x 1 of 16 batch rows of config 2 (32/8 heads, d=128, KV 4096), fp16 values as fp32, "
+                  f"scaled x16 to one step; oracle/oracle.c decode_attn, -O3, 1 thread "
+                  f"(host has {os.cpu_count()} logical CPUs)",
+    }
+
+
+def read_traffic(kernel_prefix: str):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if present."""
+    path = os.path.join(ROOT, "profiles", "decode_attn_fast_config2_traffic.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        with open(path) as f:
+            d = json.load(f)
+        return d.get("hbm_bytes_per_launch")
+    except Exception:
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU oracle timing")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only-core", action="store_true", help="time only the headline kernel (for profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one MI355X only; multi-GPU runs are out of scope "
+                                   "(--gpus must be 1)", "n_gpus": args.gpus}))
+        return 2
+
+    import cudaforge_amd as cf
+    cf.init_gpu(0)
+    caps = cf.device_caps(0)
+    log(f"device {caps.name.decode()} {caps.arch.decode()} CUs={caps.cu_count}")
+    stream = cf.Stream()
+    steps, warmup = args.steps, args.warmup
+
+    log("decode core, config 2")
+    ms, alg_bytes, cfg = bench_decode_core(cf, stream, steps, warmup)
+    gbs = alg_bytes / (ms * 1e-3) / 1e9
+    log(f"  {ms * 1e3:.2f} us/step  {gbs:.0f} GB/s")
+    extra = {}
+    if not args.only_core:
+        log("decode full op, config 2")
+        ms_f, alg_f = bench_decode_full(cf, stream, steps, warmup)
+        extra["decode_full_op_config2_f16"] = {"us_per_step": round(ms_f * 1e3, 2),
+                                               "GB_s": round(alg_f / (ms_f * 1e-3) / 1e9, 1),
+                                               "alg_bytes": alg_f}
+        log(f"  {ms_f * 1e3:.2f} us/step")
+        log("decode full op, config 1 (fp32)")
+        ms_1, alg_1 = bench_decode_full(cf, stream, steps, warmup, f16=False, B=1, H=12, H_kv=12, d=64, T=1024)
+        extra["decode_full_op_config1_f32"] = {"us_per_step": round(ms_1 * 1e3, 2),
+                                               "GB_s": round(alg_1 / (ms_1 * 1e-3) / 1e9, 1),
+                                               "alg_bytes": alg_1}
+        log("decode ragged, config 4")
+        ms_r, alg_r, lens = bench_decode_ragged(cf, stream, steps, warmup)
+        extra["decode_core_config4_ragged"] = {"us_per_step": round(ms_r * 1e3, 2),
+                                               "GB_s": round(alg_r / (ms_r * 1e-3) / 1e9, 1),
+                                               "alg_bytes": alg_r, "lengths": lens,
+                                               "hbm_frac": round(alg_r / (ms_r * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        for key, (B, S, H, d, causal, seed) in {
+                "prefill_config3_bert_base_f16": (8, 512, 12, 64, False, 300),
+                "prefill_config5_causal_gpt2_medium_f16": (4, 1024, 16, 64, True, 500)}.items():
+            log(key)
+            ms_p, fl = bench_fused(cf, stream, max(steps // 4, 10), max(warmup // 2, 3), B, S, H, d, causal, seed)
+            tf = fl / (ms_p * 1e-3) / 1e12
+            extra[key] = {"us_per_step": round(ms_p * 1e3, 2), "TFLOP_s": round(tf, 1), "alg_flop": fl,
+                          "mfma_frac": round(tf / FP16_PEAK_TFLOPS, 4)}
+            log(f"  {ms_p * 1e3:.1f} us/step {tf:.1f} TFLOP/s")
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline")
+        cpu = cpu_baseline_decode(args.cpu_budget)
+
+    out = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_step": round(ms * 1e3, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded N(0,1) fp16 Q/K/V; resident in HBM)",
+        "config": {"workload": "MHA_Decode GQA Llama-3-8B attention core (config 2): split-KV + LSE merge, "
+                               "one kernel per step", **cfg},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": read_traffic("decode_attn_fast"),
+                     "kernel": "decode_attn_fast<_Float16,128,4>", "alg_bytes_per_launch": alg_bytes},
+        "cpu_baseline": cpu,
+        "extra": extra,
+        "device": {"name": caps.name.decode(), "arch": caps.arch.decode(), "cu_count": caps.cu_count},
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

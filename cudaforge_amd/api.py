@@ -1,0 +1,249 @@
+"""ctypes helpers over the C-ABI: params structs, device buffers, streams, op calls."""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_bool, c_float, c_int, c_int64, c_void_p
+
+import numpy as np
+
+from ._native import GpuCaps, OperatorRegistryEntry, load_library
+
+
+class MhaDecodeParams(ctypes.Structure):
+    """mha_decode_params_t (include/mha_decode_int.h; reference mha_decode_int.h:6-15)."""
+
+    _fields_ = [
+        ("batch_size", c_int64),
+        ("hidden_size", c_int64),
+        ("num_heads", c_int64),
+        ("num_kv_heads", c_int64),
+        ("head_dim", c_int64),
+        ("scale", c_float),
+        ("cache_len", c_int64),
+        ("max_seq", c_int64),
+    ]
+
+
+class MhaFusedParams(ctypes.Structure):
+    """mha_fused_params_t (include/mha_fused_int.h; reference mha_fused_int.h:7-17)."""
+
+    _fields_ = [
+        ("batch_size", c_int64),
+        ("seq_len", c_int64),
+        ("hidden_size", c_int64),
+        ("num_heads", c_int64),
+        ("num_kv_heads", c_int64),
+        ("head_dim", c_int64),
+        ("scale", c_float),
+        ("has_residual", c_bool),
+        ("causal", c_bool),
+    ]
+
+
+class CausalMaskParams(ctypes.Structure):
+    _fields_ = [("seq_len", c_int64)]
+
+
+class TensorT(ctypes.Structure):
+    """tensor_t (include/platform.h; reference platform.h:36-44)."""
+
+    _fields_ = [
+        ("dtype", c_int),
+        ("ndim", c_int),
+        ("shape", c_int64 * 8),
+        ("strides", c_int64 * 8),
+        ("numel", c_int64),
+        ("data", c_void_p),
+        ("data_device", c_void_p),
+    ]
+
+
+OperatorRegistry = OperatorRegistryEntry
+
+DT_F32, DT_F16, DT_BF16, DT_I32 = 0, 1, 2, 3
+
+
+def gpu_available() -> bool:
+    return bool(load_library().gpu_available())
+
+
+def init_gpu(device: int = 0) -> None:
+    lib = load_library()
+    rc = lib.gpu_platform_init(device)
+    if rc != 0:
+        raise RuntimeError(f"gpu_platform_init({device}) failed: {rc} {lib.gpu_error_string(rc)!r}")
+
+
+def device_caps(device: int = 0) -> GpuCaps:
+    lib = load_library()
+    caps = GpuCaps()
+    rc = lib.gpu_get_gpu_caps(ctypes.byref(caps), device)
+    if rc != 0:
+        raise RuntimeError(f"gpu_get_gpu_caps failed: {rc}")
+    return caps
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        lib = load_library()
+        msg = lib.gpu_error_string(rc) if rc > 0 else b"invalid argument"
+        raise RuntimeError(f"{what} failed: rc={rc} ({msg.decode() if msg else ''})")
+
+
+class Stream:
+    """A HIP stream (default priority, non-blocking) owned by the Python object."""
+
+    def __init__(self, null: bool = False):
+        self.lib = load_library()
+        self.handle = c_void_p(None)
+        self.owned = not null
+        if not null:
+            _check(self.lib.gpu_stream_create(ctypes.byref(self.handle)), "gpu_stream_create")
+
+    def synchronize(self) -> None:
+        _check(self.lib.gpu_stream_synchronize(self.handle), "gpu_stream_synchronize")
+
+    def stream_t(self):
+        """A pointer to a stream_t holding this stream (stream_t is one void*)."""
+        self._st = (c_void_p * 1)(self.handle)
+        return ctypes.cast(self._st, c_void_p)
+
+    def close(self) -> None:
+        if self.owned and self.handle:
+            self.lib.gpu_stream_destroy(self.handle)
+            self.handle = c_void_p(None)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Event:
+    def __init__(self):
+        self.lib = load_library()
+        self.handle = c_void_p(None)
+        _check(self.lib.gpu_event_create(ctypes.byref(self.handle)), "gpu_event_create")
+
+    def record(self, stream: Stream | None = None) -> None:
+        _check(self.lib.gpu_event_record(self.handle, stream.handle if stream else None), "gpu_event_record")
+
+    def synchronize(self) -> None:
+        _check(self.lib.gpu_event_synchronize(self.handle), "gpu_event_synchronize")
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = c_float(0.0)
+        _check(self.lib.gpu_event_elapsed_ms(ctypes.byref(ms), self.handle, end.handle), "gpu_event_elapsed_ms")
+        return float(ms.value)
+
+    def __del__(self):
+        try:
+            if self.handle:
+                self.lib.gpu_event_destroy(self.handle)
+        except Exception:
+            pass
+
+
+class DeviceBuffer:
+    """Device memory from the platform allocator, with numpy upload/download."""
+
+    def __init__(self, nbytes: int, dtype=np.uint8, shape=None):
+        self.lib = load_library()
+        self.nbytes = int(nbytes)
+        self.dtype = np.dtype(dtype)
+        self.shape = tuple(shape) if shape is not None else (self.nbytes // self.dtype.itemsize,)
+        self.ptr = self.lib.gpu_device_alloc(max(self.nbytes, 1))
+        if not self.ptr:
+            raise MemoryError(f"gpu_device_alloc({self.nbytes}) failed")
+
+    @classmethod
+    def from_numpy(cls, arr: np.ndarray, stream: Stream | None = None) -> "DeviceBuffer":
+        arr = np.ascontiguousarray(arr)
+        buf = cls(arr.nbytes, arr.dtype, arr.shape)
+        buf.upload(arr, stream)
+        return buf
+
+    @classmethod
+    def empty(cls, shape, dtype) -> "DeviceBuffer":
+        dt = np.dtype(dtype)
+        n = int(np.prod(shape)) * dt.itemsize
+        return cls(n, dt, shape)
+
+    def upload(self, arr: np.ndarray, stream: Stream | None = None) -> None:
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes == self.nbytes, (arr.nbytes, self.nbytes)
+        _check(self.lib.gpu_memcpy_h2d(self.ptr, arr.ctypes.data, arr.nbytes, stream.handle if stream else None),
+               "gpu_memcpy_h2d")
+        # hipMemcpyAsync from pageable memory may return before the copy; make it safe to
+        # drop `arr` afterwards.
+        _check(self.lib.gpu_stream_synchronize(stream.handle if stream else None), "gpu_stream_synchronize")
+
+    def download(self, stream: Stream | None = None) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        _check(self.lib.gpu_memcpy_d2h(out.ctypes.data, self.ptr, self.nbytes, stream.handle if stream else None),
+               "gpu_memcpy_d2h")
+        return out
+
+    def fill_zero(self, stream: Stream | None = None) -> None:
+        _check(self.lib.gpu_memset(self.ptr, 0, self.nbytes, stream.handle if stream else None), "gpu_memset")
+
+    def free(self) -> None:
+        if self.ptr:
+            self.lib.gpu_device_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def _ptr(x):
+    if x is None:
+        return None
+    if isinstance(x, DeviceBuffer):
+        return x.ptr
+    if isinstance(x, np.ndarray):
+        return x.ctypes.data
+    return x
+
+
+def find_op(name: str):
+    lib = load_library()
+    entry = lib.operator_find(name.encode())
+    if not entry:
+        raise KeyError(f"operator {name!r} is not registered")
+    return entry.contents
+
+
+def time_op(name: str, inputs, outputs, params, stream: Stream | None, warmup: int, iters: int,
+            extra_inputs=()) -> float:
+    """Average milliseconds per call of a registered operator, timed by operator_time
+    (a C loop between HIP events on `stream`, so Python overhead is excluded)."""
+    lib = load_library()
+    ins = list(inputs) + list(extra_inputs)
+    in_arr = (c_void_p * max(len(ins), 1))(*[_ptr(x) for x in ins])
+    out_arr = (c_void_p * max(len(outputs), 1))(*[_ptr(x) for x in outputs])
+    ms = c_float(0.0)
+    st = stream.stream_t() if stream is not None else None
+    rc = lib.operator_time(name.encode(), ctypes.cast(in_arr, POINTER(c_void_p)),
+                           ctypes.cast(out_arr, POINTER(c_void_p)),
+                           ctypes.cast(ctypes.pointer(params), c_void_p), st, warmup, iters, ctypes.byref(ms))
+    if rc != 0:
+        raise RuntimeError(f"operator_time({name}) returned {rc}")
+    return ms.value / iters
+
+
+def call_op(name: str, inputs, outputs, params, stream: Stream | None = None, extra_inputs=()) -> int:
+    """Call a registered operator through its registry function pointer, exactly as the
+    reference tests do (operator_find(...)->func(inputs, outputs, params, stream))."""
+    entry = find_op(name)
+    ins = list(inputs) + list(extra_inputs)
+    in_arr = (c_void_p * max(len(ins), 1))(*[_ptr(x) for x in ins])
+    out_arr = (c_void_p * max(len(outputs), 1))(*[_ptr(x) for x in outputs])
+    st = stream.stream_t() if stream is not None else None
+    return entry.func(ctypes.cast(in_arr, POINTER(c_void_p)), ctypes.cast(out_arr, POINTER(c_void_p)),
+                      ctypes.cast(ctypes.pointer(params), c_void_p) if params is not None else None, st)

@@ -1,0 +1,405 @@
+/*
+ * graph.c — graph construction, topological build and name-based execution for the
+ * attention operators (src/application/engine/graph.c:17-220 and :670-1115 of the
+ * reference give the behaviour this follows).
+ *
+ * Execution contract kept from the reference:
+ *   - op lookup by name: "<base>_f16_cuda" when the node's first output is F16 (except
+ *     layout ops), else "<base>_cuda", else the CPU "<base>" (graph.c:836-884);
+ *     unresolved -> -2;
+ *   - input slots = node inputs then weights, outputs right after (graph.c:900-925);
+ *   - GPU ops get device pointers; outputs stay on the device until the end, when
+ *     graph outputs are copied back (lazy D2H, graph.c:1051-1083);
+ *   - an op's nonzero return aborts execution and is returned (graph.c:1019-1025).
+ * Changes: graph inputs are re-uploaded on every execution (the reference uploaded once,
+ * tensor.c:54, and reused stale data); KV-cache tensors are device-authoritative and
+ * uploaded once; a CPU op that writes a KV cache refreshes its device copy.  The MHA
+ * subgraph fusion pre-pass (graph.c:359-665) is not part of this build.
+ */
+#include "graph.h"
+#include "gpu_ops.h"
+#include "mha_decode_int.h"
+
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+inference_graph_t* graph_create(void) {
+    inference_graph_t* g = (inference_graph_t*)calloc(1, sizeof(inference_graph_t));
+    if (!g) return NULL;
+    g->kv_cache_K_tid = -1;
+    g->kv_cache_V_tid = -1;
+    return g;
+}
+
+int graph_add_tensor(inference_graph_t* g, tensor_t* t) {
+    if (!g || !t) return -1;
+    graph_tensor_t* p = (graph_tensor_t*)realloc(g->tensors, (size_t)(g->num_tensors + 1) * sizeof(graph_tensor_t));
+    if (!p) return -1;
+    g->tensors = p;
+    const int id = g->num_tensors++;
+    g->tensors[id].tensor = t;
+    g->tensors[id].producer = -1;
+    g->tensors[id].consumer = -1;
+    return id;
+}
+
+int graph_add_node(inference_graph_t* g, op_type_t type,
+                   int num_inputs, const int* input_tensors,
+                   int num_outputs, const int* output_tensors,
+                   int num_weights, tensor_t** weights,
+                   void* params, size_t params_size) {
+    if (!g || num_inputs < 0 || num_outputs < 0 || num_weights < 0) return -1;
+    if ((num_inputs > 0 && !input_tensors) || (num_outputs > 0 && !output_tensors)) return -1;
+    graph_node_t* p = (graph_node_t*)realloc(g->nodes, (size_t)(g->num_nodes + 1) * sizeof(graph_node_t));
+    if (!p) return -1;
+    g->nodes = p;
+    const int id = g->num_nodes++;
+    graph_node_t* n = &g->nodes[id];
+    memset(n, 0, sizeof(*n));
+    n->type = type;
+    n->num_inputs = num_inputs;
+    n->num_outputs = num_outputs;
+    n->num_weights = num_weights;
+    if (num_weights > 0 && weights) {
+        n->weights = (tensor_t**)malloc((size_t)num_weights * sizeof(tensor_t*));
+        if (!n->weights) return -1;
+        memcpy(n->weights, weights, (size_t)num_weights * sizeof(tensor_t*));
+    } else {
+        n->num_weights = 0;
+    }
+    if (params && params_size > 0) {
+        n->params = malloc(params_size);
+        if (!n->params) return -1;
+        memcpy(n->params, params, params_size);
+        n->params_size = params_size;
+    }
+    if (num_inputs > 0) {
+        n->input_tensors = (int*)malloc((size_t)num_inputs * sizeof(int));
+        if (!n->input_tensors) return -1;
+        memcpy(n->input_tensors, input_tensors, (size_t)num_inputs * sizeof(int));
+    }
+    if (num_outputs > 0) {
+        n->output_tensors = (int*)malloc((size_t)num_outputs * sizeof(int));
+        if (!n->output_tensors) return -1;
+        memcpy(n->output_tensors, output_tensors, (size_t)num_outputs * sizeof(int));
+    }
+    for (int i = 0; i < num_inputs; i++)
+        if (input_tensors[i] >= 0 && input_tensors[i] < g->num_tensors) g->tensors[input_tensors[i]].consumer = id;
+    for (int i = 0; i < num_outputs; i++) {
+        const int tid = output_tensors[i];
+        if (tid < 0 || tid >= g->num_tensors) continue;
+        /* A node that reads and writes the same tensor (in-place KV cache) is not its
+         * own producer for ordering purposes. */
+        int self = 0;
+        for (int j = 0; j < num_inputs; j++) if (input_tensors[j] == tid) self = 1;
+        if (!self) g->tensors[tid].producer = id;
+    }
+    return id;
+}
+
+static int append_id(int** arr, int* count, int value) {
+    int* p = (int*)realloc(*arr, (size_t)(*count + 1) * sizeof(int));
+    if (!p) return -1;
+    *arr = p;
+    p[(*count)++] = value;
+    return 0;
+}
+
+int graph_set_input(inference_graph_t* g, int node_id) {
+    if (!g || node_id < 0 || node_id >= g->num_nodes) return -1;
+    return append_id(&g->input_node_ids, &g->num_inputs, node_id);
+}
+
+int graph_set_output(inference_graph_t* g, int node_id) {
+    if (!g || node_id < 0 || node_id >= g->num_nodes) return -1;
+    return append_id(&g->output_node_ids, &g->num_outputs, node_id);
+}
+
+void graph_set_kv_cache(inference_graph_t* g, int K_tensor_id, int V_tensor_id) {
+    if (!g) return;
+    g->kv_cache_K_tid = K_tensor_id;
+    g->kv_cache_V_tid = V_tensor_id;
+}
+
+void graph_update_cache_len(inference_graph_t* g, int64_t new_cache_len) {
+    if (!g) return;
+    for (int i = 0; i < g->num_nodes; i++) {
+        graph_node_t* n = &g->nodes[i];
+        if (n->type == OP_MHA_DECODE && n->params && n->params_size >= sizeof(mha_decode_params_t))
+            ((mha_decode_params_t*)n->params)->cache_len = new_cache_len;
+    }
+}
+
+void graph_set_permanent_fusion(inference_graph_t* g, int enable) {
+    if (g) g->permanent_fusion = enable;
+}
+
+/* Kahn's algorithm (graph.c:158-220): a node depends on the producers of its inputs. */
+int graph_build(inference_graph_t* g) {
+    if (!g) return -1;
+    const int n = g->num_nodes;
+    int* indeg = (int*)calloc((size_t)(n > 0 ? n : 1), sizeof(int));
+    int* queue = (int*)malloc((size_t)(n > 0 ? n : 1) * sizeof(int));
+    int* order = (int*)malloc((size_t)(n > 0 ? n : 1) * sizeof(int));
+    if (!indeg || !queue || !order) { free(indeg); free(queue); free(order); return -1; }
+    for (int i = 0; i < n; i++)
+        for (int j = 0; j < g->nodes[i].num_inputs; j++) {
+            const int tid = g->nodes[i].input_tensors[j];
+            if (tid >= 0 && tid < g->num_tensors) {
+                const int prod = g->tensors[tid].producer;
+                if (prod >= 0 && prod != i) indeg[i]++;
+            }
+        }
+    int head = 0, tail = 0, done = 0;
+    for (int i = 0; i < n; i++) if (indeg[i] == 0) queue[tail++] = i;
+    while (head < tail) {
+        const int v = queue[head++];
+        order[done++] = v;
+        for (int k = 0; k < n; k++) {
+            if (k == v) continue;
+            for (int l = 0; l < g->nodes[k].num_inputs; l++) {
+                const int tid = g->nodes[k].input_tensors[l];
+                if (tid >= 0 && tid < g->num_tensors && g->tensors[tid].producer == v) {
+                    if (--indeg[k] == 0) queue[tail++] = k;
+                }
+            }
+        }
+    }
+    free(indeg);
+    free(queue);
+    if (done != n) { free(order); return -1; }   /* cycle */
+    free(g->topo_order);
+    g->topo_order = order;
+    return 0;
+}
+
+void graph_destroy(inference_graph_t* g) {
+    if (!g) return;
+    if (g->hip_graph) gpu_stream_destroy(g->hip_graph);
+    for (int i = 0; i < g->num_nodes; i++) {
+        free(g->nodes[i].input_tensors);
+        free(g->nodes[i].output_tensors);
+        free(g->nodes[i].weights);
+        free(g->nodes[i].params);
+    }
+    free(g->nodes);
+    for (int i = 0; i < g->num_tensors; i++) tensor_destroy(g->tensors[i].tensor);
+    free(g->tensors);
+    free(g->topo_order);
+    free(g->input_node_ids);
+    free(g->output_node_ids);
+    free(g);
+}
+
+/* Op type -> CPU base name (graph.c:254-294). */
+static const char* op_name(op_type_t type) {
+    switch (type) {
+        case OP_RELU: return "relu_f32";
+        case OP_SIGMOID: return "sigmoid_f32";
+        case OP_GELU: return "gelu_f32";
+        case OP_MATMUL: return "matmul_f32";
+        case OP_CONV2D: return "conv2d_f32";
+        case OP_MAXPOOL2D: return "maxpool2d_f32";
+        case OP_AVGPOOL2D: return "avgpool2d_f32";
+        case OP_BATCHNORM: return "batchnorm_f32";
+        case OP_ADD: return "add_f32";
+        case OP_RESHAPE: return "reshape_f32";
+        case OP_GLOBALAVGPOOL: return "globalavgpool_f32";
+        case OP_SOFTMAX: return "softmax_f32";
+        case OP_SILU: return "silu_f32";
+        case OP_MUL: return "mul_f32";
+        case OP_CONCAT: return "concat_f32";
+        case OP_RESIZE: return "resize_f32";
+        case OP_TRANSPOSE: return "transpose_f32";
+        case OP_SUB: return "sub_f32";
+        case OP_DIV: return "div_f32";
+        case OP_SLICE: return "slice_f32";
+        case OP_SPLIT: return "split_f32";
+        case OP_LAYERNORM: return "layernorm_f32";
+        case OP_GATHER: return "gather_f32";
+        case OP_SQUEEZE_UNSQUEEZE: return "squeeze_unsqueeze_f32";
+        case OP_EXP: return "exp_f32";
+        case OP_REDUCE: return "reduce_f32";
+        case OP_CAST: return "cast_f32";
+        case OP_ARGMAX: return "argmax_f32";
+        case OP_MHA_FUSED: return "mha_fused_f32";
+        case OP_MHA_DECODE: return "mha_decode_f32";
+        case OP_CAUSAL_MASK: return "causal_mask_f32";
+        case OP_ROPE: return "rope_f32";
+        case OP_PAD: return "pad_f32";
+        case OP_CLIP: return "clip_f32";
+        case OP_WHERE: return "where_f32";
+        case OP_TANH: return "tanh_f32";
+        default: return NULL;
+    }
+}
+
+const operator_registry_t* graph_resolve_op(const inference_graph_t* g, int node_id, bool use_cuda,
+                                            char* buf, size_t buf_len) {
+    if (!g || node_id < 0 || node_id >= g->num_nodes || !buf || buf_len < 8) return NULL;
+    const graph_node_t* n = &g->nodes[node_id];
+    const char* base = op_name(n->type);
+    buf[0] = '\0';
+    if (!base) return NULL;
+    int out_f16 = 0;
+    if (n->num_outputs > 0 && n->output_tensors && n->output_tensors[0] >= 0 &&
+        n->output_tensors[0] < g->num_tensors && g->tensors[n->output_tensors[0]].tensor)
+        out_f16 = g->tensors[n->output_tensors[0]].tensor->dtype == DATA_TYPE_F16;
+    const operator_registry_t* op = NULL;
+    const int layout_op = n->type == OP_CAST || n->type == OP_RESHAPE || n->type == OP_TRANSPOSE ||
+                          n->type == OP_SLICE || n->type == OP_SPLIT || n->type == OP_SQUEEZE_UNSQUEEZE;
+    if (out_f16 && !layout_op) {
+        const size_t bl = strlen(base);
+        char b16[64];
+        if (bl > 3 && strcmp(base + bl - 3, "f32") == 0) snprintf(b16, sizeof(b16), "%.*sf16", (int)(bl - 3), base);
+        else snprintf(b16, sizeof(b16), "%s", base);
+        snprintf(buf, buf_len, use_cuda ? "%s_cuda" : "%s", b16);
+        op = operator_find(buf);
+    }
+    if (!op) {
+        snprintf(buf, buf_len, use_cuda ? "%s_cuda" : "%s", base);
+        op = operator_find(buf);
+    }
+    if (!op && use_cuda) {
+        op = operator_find(base);
+        if (op) snprintf(buf, buf_len, "%s", base);
+    }
+    return op;
+}
+
+static size_t tensor_nbytes(const tensor_t* t) {
+    const data_type_info_t* info = data_type_get_info(t->dtype);
+    return info ? (size_t)t->numel * info->size : 0;
+}
+
+static int is_kv(const inference_graph_t* g, int tid) {
+    return tid >= 0 && (tid == g->kv_cache_K_tid || tid == g->kv_cache_V_tid);
+}
+
+int graph_execute(inference_graph_t* g, tensor_t* inputs[], tensor_t* outputs[], bool use_cuda) {
+    if (!g || !g->topo_order) return -1;
+    if (g->num_inputs > 0 && !inputs) return -1;
+    if (g->num_outputs > 0 && !outputs) return -1;
+
+    /* Graph inputs -> input-node tensors (host). */
+    for (int i = 0; i < g->num_inputs; i++) {
+        const graph_node_t* n = &g->nodes[g->input_node_ids[i]];
+        if (n->num_outputs <= 0 || !inputs[i]) continue;
+        const int tid = n->output_tensors[0];
+        if (tid < 0 || tid >= g->num_tensors) continue;
+        tensor_t* dst = g->tensors[tid].tensor;
+        if (dst->data != inputs[i]->data) {
+            if (inputs[i]->numel != dst->numel || inputs[i]->dtype != dst->dtype) return -1;
+            memcpy(dst->data, inputs[i]->data, tensor_nbytes(dst));
+        }
+    }
+
+    /* Tensors uploaded during this execution (so each external input moves once). */
+    unsigned char* fresh = (unsigned char*)calloc((size_t)(g->num_tensors > 0 ? g->num_tensors : 1), 1);
+    if (!fresh) return -1;
+    int ret = 0;
+    for (int oi = 0; oi < g->num_nodes && ret == 0; oi++) {
+        const int nid = g->topo_order[oi];
+        graph_node_t* n = &g->nodes[nid];
+        if (n->type == OP_INPUT || n->type == OP_OUTPUT) continue;
+        char name[64];
+        const operator_registry_t* op = graph_resolve_op(g, nid, use_cuda, name, sizeof(name));
+        if (!op) { ret = -2; break; }
+        const int on_gpu = use_cuda && strstr(name, "_cuda") != NULL;
+
+        const int in_slots = n->num_inputs + n->num_weights;
+        const int total = in_slots + n->num_outputs;
+        const void* local[32];
+        const void** slots = total <= 32 ? local : (const void**)malloc((size_t)total * sizeof(void*));
+        if (!slots) { ret = -1; break; }
+        void** outs = (void**)&slots[in_slots];
+
+        for (int i = 0; i < n->num_inputs && ret == 0; i++) {
+            const int tid = n->input_tensors[i];
+            slots[i] = NULL;
+            if (tid < 0 || tid >= g->num_tensors) continue;
+            tensor_t* t = g->tensors[tid].tensor;
+            if (on_gpu) {
+                if (is_kv(g, tid) || g->tensors[tid].producer >= 0) {
+                    if (tensor_copy_to_device(t) != 0) ret = -1;
+                } else if (!fresh[tid]) {
+                    if (tensor_upload(t) != 0) ret = -1;
+                    fresh[tid] = 1;
+                }
+                slots[i] = t->data_device;
+            } else {
+                if (t->data_device && g->tensors[tid].producer >= 0 && tensor_copy_to_host(t) != 0) ret = -1;
+                if (is_kv(g, tid) && t->data_device && tensor_copy_to_host(t) != 0) ret = -1;
+                slots[i] = t->data;
+            }
+        }
+        for (int w = 0; w < n->num_weights && ret == 0; w++) {
+            tensor_t* t = n->weights[w];
+            slots[n->num_inputs + w] = NULL;
+            if (!t) continue;
+            if (on_gpu) {
+                if (tensor_copy_to_device(t) != 0) ret = -1;
+                slots[n->num_inputs + w] = t->data_device;
+            } else {
+                slots[n->num_inputs + w] = t->data;
+            }
+        }
+        for (int i = 0; i < n->num_outputs && ret == 0; i++) {
+            const int tid = n->output_tensors[i];
+            outs[i] = NULL;
+            if (tid < 0 || tid >= g->num_tensors) continue;
+            tensor_t* t = g->tensors[tid].tensor;
+            if (on_gpu) {
+                if (!t->data_device) {
+                    t->data_device = gpu_device_alloc(tensor_nbytes(t));
+                    if (!t->data_device) ret = -1;
+                }
+                outs[i] = t->data_device;
+            } else {
+                outs[i] = t->data;
+            }
+        }
+        if (ret == 0) {
+            stream_t stream = {NULL};
+            ret = op->func(slots, outs, (const operator_params_t*)n->params, use_cuda ? &stream : NULL);
+        }
+        if (ret == 0 && use_cuda && !on_gpu) {
+            /* A CPU op wrote host data: device copies are stale.  KV caches stay
+             * device-authoritative, so refresh them; drop the others. */
+            for (int i = 0; i < n->num_outputs; i++) {
+                const int tid = n->output_tensors[i];
+                if (tid < 0 || tid >= g->num_tensors) continue;
+                tensor_t* t = g->tensors[tid].tensor;
+                if (!t->data_device) continue;
+                if (is_kv(g, tid)) {
+                    if (tensor_upload(t) != 0) ret = -1;
+                } else {
+                    gpu_device_free(t->data_device);
+                    t->data_device = NULL;
+                }
+            }
+        }
+        if (slots != local) free((void*)slots);
+    }
+    free(fresh);
+    if (ret != 0) return ret;
+
+    if (use_cuda) {
+        const int rc = gpu_stream_synchronize(NULL);
+        if (rc != 0) return rc;
+    }
+    for (int i = 0; i < g->num_outputs; i++) {
+        const graph_node_t* n = &g->nodes[g->output_node_ids[i]];
+        if (n->type != OP_OUTPUT || n->num_inputs <= 0) continue;
+        const int tid = n->input_tensors[0];
+        if (tid < 0 || tid >= g->num_tensors) continue;
+        tensor_t* src = g->tensors[tid].tensor;
+        if (use_cuda && src->data_device && tensor_copy_to_host(src) != 0) return -1;
+        if (outputs[i] && outputs[i]->data != src->data) {
+            if (outputs[i]->numel != src->numel || outputs[i]->dtype != src->dtype) return -1;
+            memcpy(outputs[i]->data, src->data, tensor_nbytes(src));
+        }
+    }
+    return 0;
+}

@@ -1,0 +1,146 @@
+/*
+ * kernels.h — C-ABI between the host operator code (C) and the HIP kernels (gfx950).
+ *
+ * Every launcher validates nothing beyond what the kernel's indexing needs; the
+ * operator layer (the csrc/operator C files) checks shapes and arguments first.  Launchers
+ * return 0 or a positive hipError_t value.  All pointers are device pointers.
+ */
+#ifndef CF_KERNELS_H_
+#define CF_KERNELS_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { CF_ELEM_F32 = 0, CF_ELEM_F16 = 1 };
+
+/* ---------------------------------------------------------------------------------
+ * Split-KV decode attention with a fused log-sum-exp combine.
+ *
+ * q: (B, H_q, d); k/v caches: (B, max_seq, H_kv, d); o: (B, H_q, d), all in `elem`.
+ * Sequence b attends positions 0 .. T_b-1 with T_b = seq_lens ? seq_lens[b] + 1
+ * : cache_len + 1.  Grid: n_split splits of `chunk` positions per (b, kv head); a
+ * split past T_b exits at once.  The last split to finish for a (b, kv head) merges
+ * the partial (max, sum, acc) tuples from `partials` and resets its counter.
+ * ------------------------------------------------------------------------------- */
+typedef struct {
+    const void*    q;
+    const void*    k;
+    const void*    v;
+    void*          o;
+    const int32_t* seq_lens;   /* device, NULL = uniform cache_len */
+    float*         partials;   /* workspace */
+    uint32_t*      counters;   /* workspace, zero on entry, left zero on exit */
+    int32_t        B, H_q, H_kv, d;
+    int32_t        max_seq, cache_len;
+    int32_t        chunk, n_split;
+    float          scale;
+    int32_t        elem;
+} cf_decode_attn_args_t;
+
+/* Positions one workgroup pass covers (chunk must be a multiple); 0 = generic kernel. */
+int32_t cf_decode_attn_chunk_quantum(int32_t elem, int32_t d, int32_t group);
+int32_t cf_decode_attn_chunk_max(int32_t elem, int32_t d, int32_t group);
+/* Workspace floats needed for the partials of a launch. */
+size_t  cf_decode_attn_partials_floats(int32_t B, int32_t H_q, int32_t H_kv, int32_t d,
+                                       int32_t n_split, int32_t elem);
+/* Counters needed (one per (b, kv head) or (b, q head)). */
+size_t  cf_decode_attn_counters(int32_t B, int32_t H_q, int32_t H_kv, int32_t d, int32_t elem);
+int     cf_launch_decode_attn(const cf_decode_attn_args_t* a, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * Skinny GEMM for decode projections: Y[m, n] = Σ_k X[m, k] W[k, n] + bias[n] for
+ * M <= 16 rows per tile (grid covers ceil(M/16) tiles), W row-major (K, N).
+ * Up to three column segments, each with its own W/bias and destination; segment s
+ * covers global columns [col0_s, col0_s + n_s) and writes element (m, j) to
+ *   out_s + m*ld_m_s + pos(m)*ld_pos_s + j,   pos(m) = pos_lens ? pos_lens[m] : pos_uniform.
+ * That places decode's K_new / V_new rows straight into the KV cache.
+ * K is split across `k_split` workgroups; the last one per column tile reduces the
+ * partials from the workspace, adds the bias and stores.
+ * ------------------------------------------------------------------------------- */
+#define CF_GEMV_MAX_SEGS 3
+typedef struct {
+    const void* w;
+    const void* bias;   /* may be NULL */
+    void*       out;
+    int64_t     n;
+    int64_t     ld_m;
+    int64_t     ld_pos;
+} cf_gemv_seg_t;
+
+typedef struct {
+    const void*    x;         /* (M, K) row-major */
+    int32_t        M, K;
+    int32_t        nseg;
+    cf_gemv_seg_t  seg[CF_GEMV_MAX_SEGS];
+    const int32_t* pos_lens;  /* device, may be NULL */
+    int64_t        pos_uniform;
+    int64_t        pos_limit; /* rows whose pos is outside [0, pos_limit) are not stored;
+                                 0 = no limit */
+    int32_t        k_split;   /* >= 1; K chunk = ceil(K / k_split) rounded to the k step */
+    float*         partials;  /* workspace */
+    uint32_t*      counters;  /* workspace, zero on entry, left zero on exit */
+    int32_t        elem;
+} cf_gemv_args_t;
+
+int32_t cf_gemv_col_tile(int32_t elem);
+int32_t cf_gemv_k_step(int32_t elem);
+size_t  cf_gemv_partials_floats(const cf_gemv_args_t* a);
+size_t  cf_gemv_counters(const cf_gemv_args_t* a);
+int     cf_launch_gemv(const cf_gemv_args_t* a, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * Prefill GEMM with fused epilogue: C = A·W + bias (+ residual), A (M, K) row-major,
+ * W (K, N) row-major.  Output layouts:
+ *   CF_GEMM_OUT_ROWMAJOR: out (M, N) row-major (+ residual (M, N) if non-NULL);
+ *   CF_GEMM_OUT_QKV:      columns split into Q | K | V, written head-major as
+ *                          q (B, H_q, S, d), k (B, H_kv, S, d), vt (B, H_kv, d, S)
+ *                          (V transposed so attention reads keys contiguously);
+ *                          M = B*S rows, W given as three segments.
+ * ------------------------------------------------------------------------------- */
+enum { CF_GEMM_OUT_ROWMAJOR = 0, CF_GEMM_OUT_QKV = 1 };
+
+typedef struct {
+    const void* a;           /* (M, K) */
+    int32_t     M, K;
+    int32_t     nseg;        /* 1 (row-major) or 3 (QKV) */
+    const void* w[3];
+    const void* bias[3];
+    int32_t     n[3];
+    int32_t     out_kind;
+    void*       out[3];      /* row-major: out[0]; QKV: q, k, vt */
+    const void* residual;    /* row-major only, may be NULL */
+    int32_t     B, S, H_q, H_kv, d;  /* QKV layout */
+    int32_t     elem;        /* element type of a, w, bias, out, residual */
+} cf_gemm_args_t;
+
+int cf_launch_gemm(const cf_gemm_args_t* a, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * Prefill attention (flash style, online softmax): q (B, H_q, S, d), k (B, H_kv, S, d),
+ * vt (B, H_kv, d, S) -> o (B, S, H_q, d) == (B*S, H_q*d) row-major.
+ * ------------------------------------------------------------------------------- */
+typedef struct {
+    const void* q;
+    const void* k;
+    const void* vt;
+    void*       o;
+    int32_t     B, S, H_q, H_kv, d;
+    float       scale;
+    int32_t     causal;
+    int32_t     elem;
+} cf_flash_args_t;
+
+int cf_launch_flash_attn(const cf_flash_args_t* a, void* stream);
+
+/* CausalMask (S, S) float on the device. */
+int cf_launch_causal_mask(float* mask, int64_t S, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CF_KERNELS_H_ */

@@ -1,0 +1,275 @@
+/*
+ * mha_decode_gpu.c — host side of the HIP MHA_Decode operators.
+ *
+ * Same contract as the reference decode op (src/operator/nn/mha_decode.c:11-125 for the
+ * semantics, mha_decode_cuda.cu:159-198 for the GPU entry and registration), built as
+ * three launches on the caller's stream:
+ *   1. projection GEMV: X_new·[WQ | WK | WV] + b; Q goes to the workspace, K_new/V_new
+ *      straight into row cache_len (or seq_lens[b]) of the output caches;
+ *   2. split-KV attention over positions 0..cache_len with the LSE merge;
+ *   3. output GEMV: O·WO + bO -> Y.
+ * Temporaries live in the persistent device workspace (no per-call allocation).
+ */
+#include "mha_ops.h"
+#include "gpu_ops.h"
+#include "op_common.h"
+#include "../kernels/kernels.h"
+
+#include <string.h>
+
+static int64_t g_chunk_override = 0;
+
+void mha_decode_set_split_chunk(int64_t chunk) { g_chunk_override = chunk > 0 ? chunk : 0; }
+
+typedef struct {
+    int64_t B, D, H, H_kv, d, max_seq, cache_len;
+    int ragged;
+} decode_shape_t;
+
+/* Validation shared by the op and the core entry (mha_decode.c:14-24, plus the GPU
+ * limits the launch grids need). */
+static int decode_shape(const mha_decode_params_t* p, decode_shape_t* s) {
+    if (!p) return -1;
+    s->B = p->batch_size;
+    s->D = p->hidden_size;
+    s->H = p->num_heads;
+    s->d = p->head_dim;
+    s->H_kv = p->num_kv_heads > 0 ? p->num_kv_heads : p->num_heads;
+    s->max_seq = p->max_seq;
+    s->cache_len = p->cache_len;
+    s->ragged = p->cache_len < 0;
+    if (s->B <= 0 || s->H <= 0 || s->d <= 0 || s->H_kv <= 0 || s->max_seq <= 0) return -1;
+    if (s->H % s->H_kv != 0) return -1;
+    if (!s->ragged && s->cache_len >= s->max_seq) return -1;
+    if (s->B > 65535 || s->H > 65535 || s->d > 1024 || s->max_seq > (1 << 30)) return -1;
+    return 0;
+}
+
+static void plan_split(int elem, const decode_shape_t* s, int64_t t_max, int64_t* chunk, int64_t* n_split) {
+    const int G = (int)(s->H / s->H_kv);
+    int64_t q = cf_decode_attn_chunk_quantum(elem, (int)s->d, G);
+    const int fast = q > 0;
+    if (!fast) q = 64;
+    int64_t cmax = cf_decode_attn_chunk_max(elem, (int)s->d, G);
+    cmax = cmax / q * q;
+    int64_t c;
+    if (g_chunk_override > 0) {
+        c = cf_ceil_div(g_chunk_override, q) * q;
+    } else {
+        const int64_t units = s->B * (fast ? s->H_kv : s->H);
+        const int64_t target = 4 * (int64_t)cf_cu_count();
+        int64_t n = cf_ceil_div(target, units);
+        const int64_t nmax = cf_ceil_div(t_max, q);
+        if (n > nmax) n = nmax;
+        if (n < 1) n = 1;
+        c = cf_ceil_div(cf_ceil_div(t_max, n), q) * q;
+    }
+    if (c > cmax) c = cmax;
+    if (c < q) c = q;
+    *chunk = c;
+    *n_split = cf_ceil_div(t_max, c);
+}
+
+int mha_decode_plan(const mha_decode_params_t* p, int elem_f16, int64_t* chunk, int64_t* n_split) {
+    decode_shape_t s;
+    if (!chunk || !n_split || decode_shape(p, &s) != 0) return -1;
+    const int64_t t_max = s.ragged ? s.max_seq : s.cache_len + 1;
+    plan_split(elem_f16 ? CF_ELEM_F16 : CF_ELEM_F32, &s, t_max, chunk, n_split);
+    return 0;
+}
+
+/* Fill the attention-core launch arguments; returns the workspace bytes it needs. */
+static size_t attn_args(int elem, const decode_shape_t* s, const int32_t* lens,
+                        cf_decode_attn_args_t* a) {
+    memset(a, 0, sizeof(*a));
+    const int64_t t_max = s->ragged ? s->max_seq : s->cache_len + 1;
+    int64_t chunk, n_split;
+    plan_split(elem, s, t_max, &chunk, &n_split);
+    a->seq_lens = lens;
+    a->B = (int32_t)s->B;
+    a->H_q = (int32_t)s->H;
+    a->H_kv = (int32_t)s->H_kv;
+    a->d = (int32_t)s->d;
+    a->max_seq = (int32_t)s->max_seq;
+    a->cache_len = s->ragged ? 0 : (int32_t)s->cache_len;
+    a->chunk = (int32_t)chunk;
+    a->n_split = (int32_t)n_split;
+    a->elem = elem;
+    return cf_decode_attn_partials_floats(a->B, a->H_q, a->H_kv, a->d, a->n_split, elem) * sizeof(float);
+}
+
+static int attn_core(int elem, const void* inputs[], void* outputs[],
+                     const operator_params_t* params, stream_t* stream) {
+    if (!params || !inputs || !outputs) return -1;
+    const mha_decode_params_t* p = (const mha_decode_params_t*)params;
+    decode_shape_t s;
+    if (decode_shape(p, &s) != 0) return -1;
+    for (int i = 0; i < 3; i++) if (!inputs[i]) return -1;
+    if (!outputs[0]) return -1;
+    const int32_t* lens = NULL;
+    if (s.ragged) {
+        lens = (const int32_t*)inputs[3];
+        if (!lens) return -1;
+    }
+    cf_decode_attn_args_t a;
+    const size_t part_bytes = attn_args(elem, &s, lens, &a);
+    if (cf_decode_attn_counters(a.B, a.H_q, a.H_kv, a.d, elem) * 4 > gpu_workspace_counter_bytes()) return -1;
+    char* ws = (char*)gpu_workspace_get(part_bytes);
+    if (!ws) return -1;
+    a.counters = (uint32_t*)ws;
+    a.partials = (float*)(ws + gpu_workspace_counter_bytes());
+    a.q = inputs[0];
+    a.k = inputs[1];
+    a.v = inputs[2];
+    a.o = outputs[0];
+    a.scale = p->scale;
+    return cf_launch_decode_attn(&a, cf_stream_of(stream));
+}
+
+int mha_decode_attn_f32_cuda(const void* inputs[], void* outputs[],
+                             const operator_params_t* params, stream_t* stream) {
+    return attn_core(CF_ELEM_F32, inputs, outputs, params, stream);
+}
+
+int mha_decode_attn_f16_cuda(const void* inputs[], void* outputs[],
+                             const operator_params_t* params, stream_t* stream) {
+    return attn_core(CF_ELEM_F16, inputs, outputs, params, stream);
+}
+
+static int gemv_k_split(int elem, int64_t K, int64_t col_tiles, int64_t m_tiles) {
+    const int64_t kstep = cf_gemv_k_step(elem);
+    const int64_t target = 2 * (int64_t)cf_cu_count();
+    int64_t ks = cf_ceil_div(target, col_tiles * m_tiles);
+    int64_t kmax = K / (4 * kstep);  /* keep >= 4 k steps (one per wave) per chunk */
+    if (ks > kmax) ks = kmax;
+    if (ks < 1) ks = 1;
+    /* every chunk non-empty */
+    while (ks > 1) {
+        const int64_t chunk = cf_ceil_div(cf_ceil_div(K, ks), kstep) * kstep;
+        if ((ks - 1) * chunk < K) break;
+        ks--;
+    }
+    return (int)ks;
+}
+
+static int decode_op(int elem, const void* inputs[], void* outputs[],
+                     const operator_params_t* params, stream_t* stream) {
+    if (!params || !inputs || !outputs) return -1;
+    for (int i = 0; i < MHA_DECODE_NUM_INPUTS; i++) if (!inputs[i]) return -1;
+    for (int i = 0; i < MHA_DECODE_NUM_OUTPUTS; i++) if (!outputs[i]) return -1;
+    const mha_decode_params_t* p = (const mha_decode_params_t*)params;
+    decode_shape_t s;
+    if (decode_shape(p, &s) != 0) return -1;
+    if (s.H * s.d != s.D) return -1;
+    const int32_t* lens = NULL;
+    if (s.ragged) {
+        lens = (const int32_t*)inputs[MHA_DECODE_SLOT_SEQLENS];
+        if (!lens) return -1;
+    }
+    const size_t esz = elem == CF_ELEM_F16 ? 2 : 4;
+    const int64_t kvd = s.H_kv * s.d;
+    void* st = cf_stream_of(stream);
+
+    /* Non-aliased output caches start as copies of the inputs (mha_decode.c:43-44). */
+    const size_t cache_bytes = (size_t)s.B * (size_t)s.max_seq * (size_t)kvd * esz;
+    int rc;
+    if (outputs[1] != inputs[1] && (rc = gpu_memcpy_d2d(outputs[1], inputs[1], cache_bytes, st)) != 0) return rc;
+    if (outputs[2] != inputs[2] && (rc = gpu_memcpy_d2d(outputs[2], inputs[2], cache_bytes, st)) != 0) return rc;
+
+    /* Plan all three launches, then carve one workspace. */
+    cf_gemv_args_t g1;
+    memset(&g1, 0, sizeof(g1));
+    g1.x = inputs[0];
+    g1.M = (int32_t)s.B;
+    g1.K = (int32_t)s.D;
+    g1.nseg = 3;
+    g1.seg[0] = (cf_gemv_seg_t){inputs[3], inputs[4], NULL, s.H * s.d, s.H * s.d, 0};
+    g1.seg[1] = (cf_gemv_seg_t){inputs[5], inputs[6], outputs[1], kvd, s.max_seq * kvd, kvd};
+    g1.seg[2] = (cf_gemv_seg_t){inputs[7], inputs[8], outputs[2], kvd, s.max_seq * kvd, kvd};
+    g1.pos_lens = lens;
+    g1.pos_uniform = s.ragged ? 0 : s.cache_len;
+    g1.pos_limit = s.max_seq;
+    g1.elem = elem;
+    const int64_t m_tiles = cf_ceil_div(s.B, 16);
+    const int64_t tile = cf_gemv_col_tile(elem);
+    const int64_t ct1 = cf_ceil_div(s.H * s.d, tile) + 2 * cf_ceil_div(kvd, tile);
+    g1.k_split = gemv_k_split(elem, s.D, ct1, m_tiles);
+
+    cf_decode_attn_args_t a;
+    const size_t attn_part = attn_args(elem, &s, lens, &a);
+
+    cf_gemv_args_t g2;
+    memset(&g2, 0, sizeof(g2));
+    g2.M = (int32_t)s.B;
+    g2.K = (int32_t)(s.H * s.d);
+    g2.nseg = 1;
+    g2.seg[0] = (cf_gemv_seg_t){inputs[9], inputs[10], outputs[0], s.D, s.D, 0};
+    g2.elem = elem;
+    g2.k_split = gemv_k_split(elem, s.H * s.d, cf_ceil_div(s.D, tile), m_tiles);
+
+    if (cf_gemv_counters(&g1) * 4 > gpu_workspace_counter_bytes() ||
+        cf_gemv_counters(&g2) * 4 > gpu_workspace_counter_bytes() ||
+        cf_decode_attn_counters(a.B, a.H_q, a.H_kv, a.d, elem) * 4 > gpu_workspace_counter_bytes())
+        return -1;
+
+    size_t cur = 0;
+    const size_t off_q = cf_ws_take(&cur, (size_t)s.B * s.H * s.d * esz);
+    const size_t off_o = cf_ws_take(&cur, (size_t)s.B * s.H * s.d * esz);
+    const size_t off_p1 = cf_ws_take(&cur, cf_gemv_partials_floats(&g1) * sizeof(float));
+    const size_t off_pa = cf_ws_take(&cur, attn_part);
+    const size_t off_p2 = cf_ws_take(&cur, cf_gemv_partials_floats(&g2) * sizeof(float));
+    char* ws = (char*)gpu_workspace_get(cur);
+    if (!ws) return -1;
+    char* data = ws + gpu_workspace_counter_bytes();
+    uint32_t* counters = (uint32_t*)ws;
+
+    g1.seg[0].out = data + off_q;
+    g1.partials = (float*)(data + off_p1);
+    g1.counters = counters;
+    if ((rc = cf_launch_gemv(&g1, st)) != 0) return rc;
+
+    a.q = data + off_q;
+    a.k = outputs[1];
+    a.v = outputs[2];
+    a.o = data + off_o;
+    a.scale = p->scale;
+    a.partials = (float*)(data + off_pa);
+    a.counters = counters;
+    if ((rc = cf_launch_decode_attn(&a, st)) != 0) return rc;
+
+    g2.x = data + off_o;
+    g2.partials = (float*)(data + off_p2);
+    g2.counters = counters;
+    return cf_launch_gemv(&g2, st);
+}
+
+int mha_decode_f32_cuda(const void* inputs[], void* outputs[],
+                        const operator_params_t* params, stream_t* stream) {
+    return decode_op(CF_ELEM_F32, inputs, outputs, params, stream);
+}
+
+int mha_decode_f16_cuda(const void* inputs[], void* outputs[],
+                        const operator_params_t* params, stream_t* stream) {
+    return decode_op(CF_ELEM_F16, inputs, outputs, params, stream);
+}
+
+/* Registrations (mha_decode_cuda.cu:192-198).  The attention-core entries are new. */
+int register_mha_decode_f32_cuda(void) {
+    static const operator_registry_t reg = {"mha_decode_f32_cuda", "f32", mha_decode_f32_cuda, 2, OP_FLAG_ALLOW_ALIAS};
+    return operator_register(&reg);
+}
+
+int register_mha_decode_f16_cuda(void) {
+    static const operator_registry_t reg = {"mha_decode_f16_cuda", "f16", mha_decode_f16_cuda, 1, OP_FLAG_ALLOW_ALIAS};
+    return operator_register(&reg);
+}
+
+int register_mha_decode_attn_f32_cuda(void) {
+    static const operator_registry_t reg = {"mha_decode_attn_f32_cuda", "f32", mha_decode_attn_f32_cuda, 1, OP_FLAG_NONE};
+    return operator_register(&reg);
+}
+
+int register_mha_decode_attn_f16_cuda(void) {
+    static const operator_registry_t reg = {"mha_decode_attn_f16_cuda", "f16", mha_decode_attn_f16_cuda, 1, OP_FLAG_NONE};
+    return operator_register(&reg);
+}

@@ -1,0 +1,123 @@
+/*
+ * mha_fused_gpu.c — host side of the HIP MHA_Fused operators.
+ *
+ * Contract of the reference fused op (src/operator/nn/mha_fused.c:7-31 for semantics,
+ * mha_fused_cuda.cu:938-1197 and mha_fused_f16_cuda.cu:209-252 for the GPU entries),
+ * executed as three launches on the caller's stream:
+ *   1. QKV GEMM: X·[WQ | WK | WV] + b, scattered head-major (V transposed);
+ *   2. attention with an online softmax (causal if params->causal);
+ *   3. output GEMM: merged·WO + bO (+ R when has_residual and R != NULL).
+ * Differences from the reference GPU op, by design: the FP32 entry computes in fp32 (the
+ * reference silently ran FP16 WMMA unless MHA_FORCE_FP32 was set, mha_fused_cuda.cu:982);
+ * causal and num_kv_heads are honoured at every S (the reference's S > 512 split path is
+ * wrong, mha_fused_cuda.cu:720,852,905-929); no per-call allocation.
+ */
+#include "mha_ops.h"
+#include "gpu_ops.h"
+#include "op_common.h"
+#include "../kernels/kernels.h"
+
+#include <string.h>
+
+static int fused_op(int elem, const void* inputs[], void* outputs[],
+                    const operator_params_t* params, stream_t* stream) {
+    if (!inputs || !inputs[0] || !outputs || !outputs[0] || !params) return -1;
+    if (!inputs[2] || !inputs[4] || !inputs[6] || !inputs[8]) return -1;
+    const mha_fused_params_t* p = (const mha_fused_params_t*)params;
+    const int64_t B = p->batch_size, S = p->seq_len, D = p->hidden_size;
+    const int64_t H = p->num_heads, d = p->head_dim;
+    const int64_t H_kv = p->num_kv_heads > 0 ? p->num_kv_heads : H;
+    if (B <= 0 || S <= 0 || D <= 0 || H <= 0 || d <= 0 || H % H_kv != 0 || H * d != D) return -1;
+    if (B > 65535 || H > 65535 || B * S > (1LL << 31) - 1 || D > (1 << 20)) return -1;
+    const size_t esz = elem == CF_ELEM_F16 ? 2 : 4;
+    const int64_t kvd = H_kv * d;
+    void* st = cf_stream_of(stream);
+
+    size_t cur = 0;
+    const size_t off_q = cf_ws_take(&cur, (size_t)(B * S * D) * esz);
+    const size_t off_k = cf_ws_take(&cur, (size_t)(B * S * kvd) * esz);
+    const size_t off_v = cf_ws_take(&cur, (size_t)(B * S * kvd) * esz);
+    const size_t off_o = cf_ws_take(&cur, (size_t)(B * S * D) * esz);
+    char* ws = (char*)gpu_workspace_get(cur);
+    if (!ws) return -1;
+    char* data = ws + gpu_workspace_counter_bytes();
+
+    cf_gemm_args_t g;
+    memset(&g, 0, sizeof(g));
+    g.a = inputs[0];
+    g.M = (int32_t)(B * S);
+    g.K = (int32_t)D;
+    g.nseg = 3;
+    g.w[0] = inputs[2]; g.bias[0] = inputs[3]; g.n[0] = (int32_t)D;
+    g.w[1] = inputs[4]; g.bias[1] = inputs[5]; g.n[1] = (int32_t)kvd;
+    g.w[2] = inputs[6]; g.bias[2] = inputs[7]; g.n[2] = (int32_t)kvd;
+    g.out_kind = CF_GEMM_OUT_QKV;
+    g.out[0] = data + off_q;
+    g.out[1] = data + off_k;
+    g.out[2] = data + off_v;
+    g.B = (int32_t)B; g.S = (int32_t)S; g.H_q = (int32_t)H; g.H_kv = (int32_t)H_kv; g.d = (int32_t)d;
+    g.elem = elem;
+    int rc = cf_launch_gemm(&g, st);
+    if (rc != 0) return rc;
+
+    cf_flash_args_t f;
+    memset(&f, 0, sizeof(f));
+    f.q = data + off_q;
+    f.k = data + off_k;
+    f.vt = data + off_v;
+    f.o = data + off_o;
+    f.B = (int32_t)B; f.S = (int32_t)S; f.H_q = (int32_t)H; f.H_kv = (int32_t)H_kv; f.d = (int32_t)d;
+    f.scale = p->scale;
+    f.causal = p->causal ? 1 : 0;
+    f.elem = elem;
+    if ((rc = cf_launch_flash_attn(&f, st)) != 0) return rc;
+
+    cf_gemm_args_t o;
+    memset(&o, 0, sizeof(o));
+    o.a = data + off_o;
+    o.M = (int32_t)(B * S);
+    o.K = (int32_t)D;
+    o.nseg = 1;
+    o.w[0] = inputs[8]; o.bias[0] = inputs[9]; o.n[0] = (int32_t)D;
+    o.out_kind = CF_GEMM_OUT_ROWMAJOR;
+    o.out[0] = outputs[0];
+    o.residual = (p->has_residual && inputs[1]) ? inputs[1] : NULL;
+    o.elem = elem;
+    return cf_launch_gemm(&o, st);
+}
+
+int mha_fused_f32_cuda(const void* inputs[], void* outputs[],
+                       const operator_params_t* params, stream_t* stream) {
+    return fused_op(CF_ELEM_F32, inputs, outputs, params, stream);
+}
+
+int mha_fused_f16_cuda(const void* inputs[], void* outputs[],
+                       const operator_params_t* params, stream_t* stream) {
+    return fused_op(CF_ELEM_F16, inputs, outputs, params, stream);
+}
+
+int causal_mask_f32_cuda(const void* inputs[], void* outputs[],
+                         const operator_params_t* params, stream_t* stream) {
+    (void)inputs;
+    if (!outputs || !outputs[0] || !params) return -1;
+    const causal_mask_params_t* p = (const causal_mask_params_t*)params;
+    if (p->seq_len <= 0) return -1;
+    return cf_launch_causal_mask((float*)outputs[0], p->seq_len, cf_stream_of(stream));
+}
+
+/* Registrations (mha_fused_cuda.cu:1191-1197, mha_fused_f16_cuda.cu:246-252,
+ * causal_mask_cuda.cu).  mha_fused_f16_cuda now declares "f16" I/O. */
+int register_mha_fused_f32_cuda(void) {
+    static const operator_registry_t reg = {"mha_fused_f32_cuda", "f32", mha_fused_f32_cuda, 6, OP_FLAG_NONE};
+    return operator_register(&reg);
+}
+
+int register_mha_fused_f16_cuda(void) {
+    static const operator_registry_t reg = {"mha_fused_f16_cuda", "f16", mha_fused_f16_cuda, 2, OP_FLAG_NONE};
+    return operator_register(&reg);
+}
+
+int register_causal_mask_f32_cuda(void) {
+    static const operator_registry_t reg = {"causal_mask_f32_cuda", "f32", causal_mask_f32_cuda, 1, OP_FLAG_NONE};
+    return operator_register(&reg);
+}

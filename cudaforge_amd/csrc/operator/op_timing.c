@@ -1,0 +1,27 @@
+/* op_timing.c — event-timed loop over a registered operator (see include/op_timing.h). */
+#include "op_timing.h"
+#include "gpu_ops.h"
+
+int operator_time(const char* name, const void* inputs[], void* outputs[],
+                  const operator_params_t* params, stream_t* stream,
+                  int warmup, int iters, float* ms_total) {
+    if (!name || !ms_total || iters <= 0 || warmup < 0) return -1;
+    const operator_registry_t* op = operator_find(name);
+    if (!op) return -2;
+    void* s = stream ? stream->cuda_stream : NULL;
+    int rc;
+    for (int i = 0; i < warmup; i++)
+        if ((rc = op->func(inputs, outputs, params, stream)) != 0) return rc;
+    if ((rc = gpu_stream_synchronize(s)) != 0) return rc;
+    gpu_event_t e0 = NULL, e1 = NULL;
+    if ((rc = gpu_event_create(&e0)) != 0) return rc;
+    if ((rc = gpu_event_create(&e1)) != 0) { gpu_event_destroy(e0); return rc; }
+    rc = gpu_event_record(e0, s);
+    for (int i = 0; i < iters && rc == 0; i++) rc = op->func(inputs, outputs, params, stream);
+    if (rc == 0) rc = gpu_event_record(e1, s);
+    if (rc == 0) rc = gpu_event_synchronize(e1);
+    if (rc == 0) rc = gpu_event_elapsed_ms(ms_total, e0, e1);
+    gpu_event_destroy(e0);
+    gpu_event_destroy(e1);
+    return rc;
+}

