@@ -57,9 +57,38 @@ def bench_decode_core(cf, stream, steps, warmup):
     O_ = cf.DeviceBuffer.empty((B, H, d), np.float16)
     p = cf.MhaDecodeParams(B, H * d, H, H_kv, d, float(1 / np.sqrt(d)), T - 1, T)
     ms = time_op(cf, "mha_decode_attn_f16_cuda", [Q, K, V], [O_], p, stream, steps, warmup)
+    ms_split, ms_merge = kernel_times(cf, [Q, K, V], [O_], p, stream, min(steps, 1000), warmup)
     kv_bytes = 2 * B * T * H_kv * d * 2
     alg_bytes = kv_bytes + 2 * B * H * d * 2
-    return ms, alg_bytes, dict(B=B, H_q=H, H_kv=H_kv, d=d, kv_len=T)
+    chunk, n_split = plan(cf, p)
+    return ms, ms_split, ms_merge, alg_bytes, dict(B=B, H_q=H, H_kv=H_kv, d=d, kv_len=T, chunk=chunk,
+                                                   n_split=n_split)
+
+
+def kernel_times(cf, inputs, outputs, params, stream, iters, warmup, f16=True):
+    """Mean duration of the split kernel and of the merge kernel (HIP events around
+    each launch, on the stream they run on)."""
+    import ctypes
+    from ctypes import POINTER, c_float, c_void_p
+    from cudaforge_amd.api import _ptr
+    lib = cf.load_library()
+    ins = (c_void_p * len(inputs))(*[_ptr(x) for x in inputs])
+    outs = (c_void_p * len(outputs))(*[_ptr(x) for x in outputs])
+    a, b = c_float(0), c_float(0)
+    rc = lib.mha_decode_attn_kernel_times(ctypes.cast(ins, POINTER(c_void_p)), ctypes.cast(outs, POINTER(c_void_p)),
+                                          ctypes.addressof(params), stream.stream_t(), 1 if f16 else 0, warmup,
+                                          iters, ctypes.byref(a), ctypes.byref(b))
+    if rc != 0:
+        raise RuntimeError(f"mha_decode_attn_kernel_times returned {rc}")
+    return a.value, b.value
+
+
+def plan(cf, params, f16=True):
+    import ctypes
+    lib = cf.load_library()
+    c, n = ctypes.c_int64(0), ctypes.c_int64(0)
+    lib.mha_decode_plan(ctypes.addressof(params), 1 if f16 else 0, ctypes.byref(c), ctypes.byref(n))
+    return int(c.value), int(n.value)
 
 
 def bench_decode_full(cf, stream, steps, warmup, f16=True, B=16, H=32, H_kv=8, d=128, T=4096, seed=200):
@@ -184,9 +213,11 @@ def main() -> int:
     steps, warmup = args.steps, args.warmup
 
     log("decode core, config 2")
-    ms, alg_bytes, cfg = bench_decode_core(cf, stream, steps, warmup)
+    ms, ms_split, ms_merge, alg_bytes, cfg = bench_decode_core(cf, stream, steps, warmup)
     gbs = alg_bytes / (ms * 1e-3) / 1e9
-    log(f"  {ms * 1e3:.2f} us/step  {gbs:.0f} GB/s")
+    gbs_split = alg_bytes / (ms_split * 1e-3) / 1e9
+    log(f"  {ms * 1e3:.2f} us/step  {gbs:.0f} GB/s; split kernel {ms_split * 1e3:.2f} us "
+        f"({gbs_split:.0f} GB/s), merge kernel {ms_merge * 1e3:.2f} us")
     extra = {}
     if not args.only_core:
         log("decode full op, config 2")
@@ -237,9 +268,10 @@ def main() -> int:
         "data": "synthetic (seeded N(0,1) fp16 Q/K/V; resident in HBM)",
         "config": {"workload": "MHA_Decode GQA Llama-3-8B attention core (config 2): split-KV + LSE merge, "
                                "one kernel per step", **cfg},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": read_traffic("decode_attn_fast"),
-                     "kernel": "decode_attn_fast<_Float16,128,4>", "alg_bytes_per_launch": alg_bytes},
+        "roofline": {"bound": "hbm", "achieved": round(gbs_split, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs_split / HBM_PEAK_GBS, 4), "traffic": read_traffic("split_f16"),
+                     "kernel": "split_f16<128,4> (decode_attn.hip)", "alg_bytes_per_launch": alg_bytes,
+                     "kernel_us": round(ms_split * 1e3, 2), "merge_kernel_us": round(ms_merge * 1e3, 2)},
         "cpu_baseline": cpu,
         "extra": extra,
         "device": {"name": caps.name.decode(), "arch": caps.arch.decode(), "cu_count": caps.cu_count},

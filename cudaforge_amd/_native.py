@@ -82,7 +82,6 @@ def _proto(lib):
         "gpu_event_synchronize": (c_int, [c_void_p]),
         "gpu_event_elapsed_ms": (c_int, [POINTER(c_float), c_void_p, c_void_p]),
         "gpu_workspace_get": (c_void_p, [c_size_t]),
-        "gpu_workspace_counter_bytes": (c_size_t, []),
         "gpu_workspace_size": (c_size_t, []),
         "gpu_workspace_release": (None, []),
         "gpu_inject_alloc_failures": (None, [c_int]),
@@ -94,6 +93,8 @@ def _proto(lib):
         "operator_register": (c_int, [c_void_p]),
         "operator_time": (c_int, [c_char_p, POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_void_p, c_int, c_int,
                                   POINTER(c_float)]),
+        "mha_decode_attn_kernel_times": (c_int, [POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_void_p, c_int,
+                                                 c_int, c_int, POINTER(c_float), POINTER(c_float)]),
         # decode planning knobs
         "mha_decode_set_split_chunk": (None, [c_int64]),
         "mha_decode_plan": (c_int, [c_void_p, c_int, POINTER(c_int64), POINTER(c_int64)]),

@@ -1,24 +1,29 @@
 // decode_attn.hip — split-KV single-token attention over a KV cache for gfx950.
 //
 // Replaces the reference's one-block-per-batch-row decode kernel
-// (src/operator/nn/mha_decode_cuda.cu:11-157) with a bandwidth-shaped design:
+// (src/operator/nn/mha_decode_cuda.cu:11-157).  Two launches:
 //
-//  * grid = (split, kv head, batch row); each workgroup streams one `chunk` of
-//    positions of one (b, kv head) and serves the whole GQA group of G query heads
-//    from a single read of each K and V row (kv head = h / G, mha_decode.c:77);
-//  * 16-byte loads per lane; a wave covers 64*16 B = RPW whole K rows per load and
-//    keeps kUnroll loads in flight;
-//  * inside a split the softmax is exact two-pass over LDS-resident scores: pass 1
-//    streams K and writes s = q·k·scale·log2(e), pass 2 streams V with p = 2^(s - m),
-//    so no running rescale is needed;
-//  * the partial (m, l, acc) of every split goes to the workspace; the last workgroup
-//    of a (b, kv head) — found with a device-scope counter — merges them with the
-//    log-sum-exp rule  O = Σ 2^(m_s - M)·acc_s / Σ 2^(m_s - M)·l_s  and resets the
-//    counter, so one launch produces the final output (mha_fused_cuda.cu:847-863 and
-//    :895-931 give the reference's split/merge formula).
-//
-// A generic kernel (one query head per workgroup, element-wise loops) covers head
-// sizes and group sizes the specialised kernel is not instantiated for.
+// 1. split kernel, grid = (split, kv head, batch row).  A workgroup streams one `chunk`
+//    of positions of one (b, kv head) and serves the whole GQA group of G query heads
+//    (kv head = h / G, mha_decode.c:77) from a single read of every K and V row.
+//    Inside a split the softmax is exact and two-pass over LDS-resident scores:
+//      pass 1 streams K and stores s = q·k · scale·log2(e) (and its max),
+//      pass 2 streams V with p = 2^(s - m)  -> partial (m, l = Σp, acc = Σ p·v).
+//    fp16 (d = 64/128): one wave per workgroup.  Q·K^T runs on the matrix cores as
+//      S^T(16 positions x 16 heads) = K(16 x 32 dims) · Q^T(32 dims x 16 heads) with
+//      v_mfma_f32_16x16x32_f16, so a lane ends up holding 4 positions of ONE head and
+//      no cross-lane reduction is needed; the K tile loads are double-buffered.  P·V is
+//      on the VALU: a lane owns 8 dims of one V row and accumulates all G heads.
+//    fp32 (d = 64/128): four waves, lanes own 4 dims of a row, dot products reduced
+//      across the row's lanes.
+//    Other head or group sizes: a generic kernel, one query head per workgroup.
+// 2. merge kernel, one workgroup per (b, kv head): the log-sum-exp combine
+//      O = Σ_s 2^(m_s - M)·acc_s / Σ_s 2^(m_s - M)·l_s
+//    (the reference's split/merge formula, mha_fused_cuda.cu:847-863 and :895-931,
+//    restated per (b, head) with the head index it lacked).  A sequence that fits in
+//    one split is finished by the split kernel and skipped here.
+// No fences or atomics: the kernel boundary orders the partials, which matters on
+// MI355X where each XCD has its own L2.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -27,155 +32,272 @@
 
 namespace {
 
-typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
-constexpr int kUnroll = 4;
-constexpr int kFastChunkMax = 1024;
+constexpr int kChunkMax = 4096;            // positions per split (LDS: chunk * G floats)
+constexpr int kF16Quantum = 32;            // fp16 split kernel: positions per double-block
+constexpr int kF32Threads = 256;
+constexpr int kF32Unroll = 4;
 constexpr int kGenericThreads = 128;
-constexpr int kGenericChunkMax = 4096;
-
-template <typename T> struct VecOf;
-template <> struct VecOf<_Float16> { using type = h8_t; static constexpr int n = 8; };
-template <> struct VecOf<float>    { using type = f4_t; static constexpr int n = 4; };
-
-__device__ __forceinline__ float dot_lane(const h8_t& a, const h8_t& b) {
-    float s = 0.0f;
-    s = __builtin_amdgcn_fdot2(h2_t{a[0], a[1]}, h2_t{b[0], b[1]}, s, false);
-    s = __builtin_amdgcn_fdot2(h2_t{a[2], a[3]}, h2_t{b[2], b[3]}, s, false);
-    s = __builtin_amdgcn_fdot2(h2_t{a[4], a[5]}, h2_t{b[4], b[5]}, s, false);
-    s = __builtin_amdgcn_fdot2(h2_t{a[6], a[7]}, h2_t{b[6], b[7]}, s, false);
-    return s;
-}
-
-__device__ __forceinline__ float dot_lane(const f4_t& a, const f4_t& b) {
-    float s = a[0] * b[0];
-    s = __builtin_fmaf(a[1], b[1], s);
-    s = __builtin_fmaf(a[2], b[2], s);
-    s = __builtin_fmaf(a[3], b[3], s);
-    return s;
-}
-
-template <int W>
-__device__ __forceinline__ float xor_sum(float v) {
-#pragma unroll
-    for (int m = 1; m < W; m <<= 1) v += __shfl_xor(v, m);
-    return v;
-}
+constexpr int kMergeThreads = 256;
 
 __device__ __forceinline__ float to_f(float x) { return x; }
 __device__ __forceinline__ float to_f(_Float16 x) { return (float)x; }
-template <typename T> __device__ __forceinline__ T from_f(float x);
-template <> __device__ __forceinline__ float from_f<float>(float x) { return x; }
-template <> __device__ __forceinline__ _Float16 from_f<_Float16>(float x) { return (_Float16)x; }
+template <typename T> __device__ __forceinline__ T from_f(float x) { return (T)x; }
 
-// Merge the partials of all splits of one unit (this workgroup is the last to finish).
-// part layout per split: [m (Gx)] [l (Gx)] [acc (Gx*D)], stride Gx*(D+2) floats.
-template <typename T>
-__device__ void merge_splits(const float* __restrict__ part, int nsplit, int Gx, int D,
-                             T* __restrict__ out, int out_head_stride) {
-    const int stride = Gx * (D + 2);
-    for (int idx = threadIdx.x; idx < Gx * D; idx += blockDim.x) {
-        const int g = idx / D, i = idx - g * D;
-        float mx = -INFINITY;
-        for (int s = 0; s < nsplit; s++) mx = fmaxf(mx, part[(size_t)s * stride + g]);
-        float num = 0.0f, den = 0.0f;
-        for (int s = 0; s < nsplit; s++) {
-            const float* ps = part + (size_t)s * stride;
-            const float w = exp2f(ps[g] - mx);
-            num = __builtin_fmaf(w, ps[2 * Gx + idx], num);
-            den = __builtin_fmaf(w, ps[Gx + g], den);
-        }
-        out[(size_t)g * out_head_stride + i] = from_f<T>(num / den);
-    }
+__device__ __forceinline__ int attended(const cf_decode_attn_args_t& a, int b) {
+    const int cl = a.seq_lens ? a.seq_lens[b] : a.cache_len;
+    return min(max(cl + 1, 1), a.max_seq);
 }
 
-// Publish this split's partial and report whether this workgroup is the last of its
-// unit.  Every thread fences its own stores before the counter moves (release); the
-// last workgroup fences again before reading the others' partials (acquire).
-__device__ bool publish_and_check_last(uint32_t* counter, int nsplit) {
-    __shared__ int s_last;
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t prev = atomicAdd(counter, 1u);
-        const int last = (prev == (uint32_t)(nsplit - 1));
-        if (last) atomicExch(counter, 0u);
-        s_last = last;
-    }
-    __syncthreads();
-    const bool last = s_last != 0;
-    if (last) __threadfence();
-    return last;
+// Partial record of one split: [m (Gx)] [l (Gx)] [acc (Gx*D)].
+__device__ __forceinline__ float* partial_at(const cf_decode_attn_args_t& a, int unit, int split, int Gx, int D) {
+    return a.partials + ((size_t)unit * a.n_split + split) * (size_t)(Gx * (D + 2));
 }
 
-template <typename T, int D, int G>
-__global__ __launch_bounds__(kThreads)
-void decode_attn_fast(cf_decode_attn_args_t a) {
-    using V = typename VecOf<T>::type;
-    constexpr int VEC = VecOf<T>::n;
-    constexpr int LPR = D / VEC;               // lanes per K/V row
-    constexpr int RPW = 64 / LPR;              // rows one wave load covers
-    constexpr int ROWS = kWaves * RPW;         // rows one workgroup load covers
-    constexpr int PIT = ROWS * kUnroll;        // positions per pass
-    static_assert(G <= LPR, "one writer lane per head");
+// ------------------------------------------------------------------ fp16 split ---
+template <int D, int G>
+__global__ __launch_bounds__(64)
+void split_f16(cf_decode_attn_args_t a) {
+    constexpr int KT = D / 32;          // 32-dim MFMA steps
+    constexpr int LPR = D / 8;          // lanes per V row (8 halves each)
+    constexpr int RPW = 64 / LPR;       // V rows per wave load
+    constexpr int VU = 4;               // V loads in flight per lane per step
+    extern __shared__ float sc[];       // [chunk][G]
 
-    extern __shared__ float smem[];
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-    const int T_b = min(max((a.seq_lens ? a.seq_lens[b] : a.cache_len) + 1, 1), a.max_seq);
+    const int T_b = attended(a, b);
     const int t0 = split * a.chunk;
     if (t0 >= T_b) return;
     const int t1 = min(t0 + a.chunk, T_b);
     const int npos = t1 - t0;
     const int nsplit_b = (T_b + a.chunk - 1) / a.chunk;
+    const int lane = threadIdx.x, lr = lane & 15, lq = lane >> 4;
 
+    const size_t row_stride = (size_t)a.H_kv * D;
+    const _Float16* __restrict__ kb = (const _Float16*)a.k + ((size_t)b * a.max_seq * a.H_kv + kvh) * D;
+    const _Float16* __restrict__ vb = (const _Float16*)a.v + ((size_t)b * a.max_seq * a.H_kv + kvh) * D;
+    const int h0 = kvh * G;
+
+    // B operand Q^T: lane (lr, lq) holds Q[head lr][32kt + 8lq .. +7]; heads >= G are 0.
+    h8_t qf[KT];
+#pragma unroll
+    for (int kt = 0; kt < KT; kt++)
+        qf[kt] = lr < G ? *(const h8_t*)((const _Float16*)a.q + ((size_t)b * a.H_q + h0 + lr) * D + 32 * kt + 8 * lq)
+                        : h8_t{};
+    const float qk_scale = a.scale * kLog2e;
+
+    // ---- pass 1: scores, 16 positions per MFMA block, two blocks in flight.
+    auto load_k = [&](int p0, h8_t (&kf)[KT]) {
+        const int pos = p0 + lr;
+#pragma unroll
+        for (int kt = 0; kt < KT; kt++)
+            kf[kt] = pos < t1 ? *(const h8_t*)(kb + (size_t)pos * row_stride + 32 * kt + 8 * lq) : h8_t{};
+    };
+    float mrun = -INFINITY;
+    auto score = [&](int p0, const h8_t (&kf)[KT]) {
+        f4_t s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kt = 0; kt < KT; kt++) s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[kt], qf[kt], s, 0, 0, 0);
+        if (lr < G) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int pos = p0 + 4 * lq + i;
+                if (pos < t1) {
+                    const float x = s[i] * qk_scale;
+                    sc[(pos - t0) * G + lr] = x;
+                    mrun = fmaxf(mrun, x);
+                }
+            }
+        }
+    };
+    h8_t ka[KT], kc[KT];
+    load_k(t0, ka);
+    for (int p0 = t0; p0 < t1; p0 += 32) {
+        load_k(p0 + 16, kc);
+        score(p0, ka);
+        if (p0 + 32 < t1) load_k(p0 + 32, ka);
+        if (p0 + 16 < t1) score(p0 + 16, kc);
+    }
+    // First V rows go out now, so their latency overlaps the softmax pass below.
+    const int r = lane / LPR, c = lane - (lane / LPR) * LPR;
+    const _Float16* __restrict__ vrow = vb + 8 * c;
+    auto load_v = [&](int p0, h8_t (&vv)[VU]) {
+#pragma unroll
+        for (int u = 0; u < VU; u++) {
+            const int pos = p0 + u * RPW + r;
+            vv[u] = pos < t1 ? *(const h8_t*)(vrow + (size_t)pos * row_stride) : h8_t{};
+        }
+    };
+    h8_t va[VU], vc[VU];
+    load_v(t0, va);
+    // Max per head: lanes with equal lr hold the same head.
+    mrun = fmaxf(mrun, __shfl_xor(mrun, 16));
+    mrun = fmaxf(mrun, __shfl_xor(mrun, 32));
+    float M[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) M[g] = __shfl(mrun, g);
+    __syncthreads();
+
+    // ---- probabilities and their sums (64 % G == 0, so a lane always sees one head).
+    float lsum = 0.0f;
+    {
+        const int gm = lane % G;
+        float mg = M[0];
+#pragma unroll
+        for (int g = 1; g < G; g++) if (gm == g) mg = M[g];
+        for (int i = lane; i < npos * G; i += 64) {
+            const float p = exp2f(sc[i] - mg);
+            sc[i] = p;
+            lsum += p;
+        }
+    }
+#pragma unroll
+    for (int off = G; off < 64; off <<= 1) lsum += __shfl_xor(lsum, off);
+    float L[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) L[g] = __shfl(lsum, g);
+    __syncthreads();
+
+    // ---- pass 2: acc[g][e] += p[g] * V[pos][8c + e], VU rows in flight per lane.
+    float acc[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[g][e] = 0.0f;
+    auto accum = [&](int p0, const h8_t (&vv)[VU]) {
+#pragma unroll
+        for (int u = 0; u < VU; u++) {
+            const int pos = p0 + u * RPW + r;
+            if (pos < t1) {
+                float p[G];
+#pragma unroll
+                for (int g = 0; g < G; g++) p[g] = sc[(pos - t0) * G + g];
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float ve = (float)vv[u][e];
+#pragma unroll
+                    for (int g = 0; g < G; g++) acc[g][e] = __builtin_fmaf(p[g], ve, acc[g][e]);
+                }
+            }
+        }
+    };
+    constexpr int VSTEP = VU * RPW;
+    for (int p0 = t0; p0 < t1; p0 += 2 * VSTEP) {
+        load_v(p0 + VSTEP, vc);
+        accum(p0, va);
+        if (p0 + 2 * VSTEP < t1) load_v(p0 + 2 * VSTEP, va);
+        if (p0 + VSTEP < t1) accum(p0 + VSTEP, vc);
+    }
+    // Rows of the wave -> row 0.
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            float v = acc[g][e];
+#pragma unroll
+            for (int off = LPR; off < 64; off <<= 1) v += __shfl_xor(v, off);
+            acc[g][e] = v;
+        }
+
+    if (nsplit_b == 1) {
+        if (r == 0) {
+            _Float16* out = (_Float16*)a.o + ((size_t)b * a.H_q + h0) * D + 8 * c;
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const float inv = 1.0f / L[g];
+                h8_t o;
+#pragma unroll
+                for (int e = 0; e < 8; e++) o[e] = (_Float16)(acc[g][e] * inv);
+                *(h8_t*)(out + (size_t)g * D) = o;
+            }
+        }
+        return;
+    }
+    float* part = partial_at(a, b * a.H_kv + kvh, split, G, D);
+    if (r == 0) {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            f4_t lo = {acc[g][0], acc[g][1], acc[g][2], acc[g][3]};
+            f4_t hi = {acc[g][4], acc[g][5], acc[g][6], acc[g][7]};
+            *(f4_t*)(part + 2 * G + g * D + 8 * c) = lo;
+            *(f4_t*)(part + 2 * G + g * D + 8 * c + 4) = hi;
+        }
+    }
+    if (lane < G) {
+        float m = M[0], l = L[0];
+#pragma unroll
+        for (int g = 1; g < G; g++) if (lane == g) { m = M[g]; l = L[g]; }
+        part[lane] = m;
+        part[G + lane] = l;
+    }
+}
+
+// ------------------------------------------------------------------ fp32 split ---
+template <int D, int G>
+__global__ __launch_bounds__(kF32Threads)
+void split_f32(cf_decode_attn_args_t a) {
+    constexpr int LPR = D / 4;                 // lanes per row (4 floats each)
+    constexpr int RPW = 64 / LPR;
+    constexpr int NW = kF32Threads / 64;
+    constexpr int ROWS = NW * RPW;
+    constexpr int PIT = ROWS * kF32Unroll;
+    static_assert(G <= LPR, "one writer lane per head");
+    extern __shared__ float smem[];
+
+    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int T_b = attended(a, b);
+    const int t0 = split * a.chunk;
+    if (t0 >= T_b) return;
+    const int t1 = min(t0 + a.chunk, T_b);
+    const int npos = t1 - t0;
+    const int nsplit_b = (T_b + a.chunk - 1) / a.chunk;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane / LPR, c = lane - r * LPR;
 
     const size_t row_stride = (size_t)a.H_kv * D;
-    const size_t unit_off = ((size_t)b * a.max_seq * a.H_kv + kvh) * D + (size_t)c * VEC;
-    const T* __restrict__ kbase = (const T*)a.k + unit_off;
-    const T* __restrict__ vbase = (const T*)a.v + unit_off;
+    const size_t unit_off = ((size_t)b * a.max_seq * a.H_kv + kvh) * D + (size_t)c * 4;
+    const float* __restrict__ kb = (const float*)a.k + unit_off;
+    const float* __restrict__ vb = (const float*)a.v + unit_off;
     const int h0 = kvh * G;
+    const int sc_floats = max(a.chunk * G, NW * G * D);
+    float* sc = smem;
+    float* red = smem + sc_floats;             // [2][NW][G]
 
-    const int sc_floats = max(a.chunk * G, kWaves * G * D);
-    float* sc = smem;                          // [npos][G] scores, later probabilities
-    float* red = smem + sc_floats;             // [2][kWaves][G]
-
-    V qv[G];
+    f4_t qv[G];
 #pragma unroll
-    for (int g = 0; g < G; g++)
-        qv[g] = *(const V*)((const T*)a.q + ((size_t)b * a.H_q + h0 + g) * D + (size_t)c * VEC);
+    for (int g = 0; g < G; g++) qv[g] = *(const f4_t*)((const float*)a.q + ((size_t)b * a.H_q + h0 + g) * D + c * 4);
     const float qk_scale = a.scale * kLog2e;
 
-    // Pass 1: scores.
     float mloc[G];
 #pragma unroll
     for (int g = 0; g < G; g++) mloc[g] = -INFINITY;
     for (int base = t0; base < t1; base += PIT) {
-        V kv[kUnroll];
-        int pos[kUnroll];
+        f4_t kv[kF32Unroll];
+        int pos[kF32Unroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) {
+        for (int u = 0; u < kF32Unroll; u++) {
             pos[u] = base + u * ROWS + wave * RPW + r;
-            if (pos[u] < t1) kv[u] = *(const V*)(kbase + (size_t)pos[u] * row_stride);
-            else kv[u] = V{};
+            kv[u] = pos[u] < t1 ? *(const f4_t*)(kb + (size_t)pos[u] * row_stride) : f4_t{};
         }
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) {
+        for (int u = 0; u < kF32Unroll; u++)
 #pragma unroll
             for (int g = 0; g < G; g++) {
-                const float s = xor_sum<LPR>(dot_lane(qv[g], kv[u])) * qk_scale;
+                float s = qv[g][0] * kv[u][0];
+                s = __builtin_fmaf(qv[g][1], kv[u][1], s);
+                s = __builtin_fmaf(qv[g][2], kv[u][2], s);
+                s = __builtin_fmaf(qv[g][3], kv[u][3], s);
+#pragma unroll
+                for (int m = 1; m < LPR; m <<= 1) s += __shfl_xor(s, m);
+                s *= qk_scale;
                 if (pos[u] < t1) {
                     if (c == g) sc[(pos[u] - t0) * G + g] = s;
                     mloc[g] = fmaxf(mloc[g], s);
                 }
             }
-        }
     }
 #pragma unroll
     for (int g = 0; g < G; g++) {
@@ -190,18 +312,16 @@ void decode_attn_fast(cf_decode_attn_args_t a) {
     for (int g = 0; g < G; g++) {
         float m = red[g];
 #pragma unroll
-        for (int w = 1; w < kWaves; w++) m = fmaxf(m, red[w * G + g]);
+        for (int w = 1; w < NW; w++) m = fmaxf(m, red[w * G + g]);
         M[g] = m;
     }
-
-    // Probabilities and their sum per head.
     float lsum = 0.0f;
     {
         const int gm = tid % G;
         float mg = M[0];
 #pragma unroll
         for (int g = 1; g < G; g++) if (gm == g) mg = M[g];
-        for (int i = tid; i < npos * G; i += kThreads) {
+        for (int i = tid; i < npos * G; i += kF32Threads) {
             const float p = exp2f(sc[i] - mg);
             sc[i] = p;
             lsum += p;
@@ -209,110 +329,92 @@ void decode_attn_fast(cf_decode_attn_args_t a) {
     }
 #pragma unroll
     for (int off = G; off < 64; off <<= 1) lsum += __shfl_xor(lsum, off);
-    if (lane < G) red[kWaves * G + wave * G + lane] = lsum;
+    if (lane < G) red[NW * G + wave * G + lane] = lsum;
     __syncthreads();
     float L[G];
 #pragma unroll
     for (int g = 0; g < G; g++) {
         float l = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kWaves; w++) l += red[kWaves * G + w * G + g];
+        for (int w = 0; w < NW; w++) l += red[NW * G + w * G + g];
         L[g] = l;
     }
-
-    // Pass 2: acc[g][:] += p[g] * V.
-    float acc[G][VEC];
+    float acc[G][4];
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
-        for (int e = 0; e < VEC; e++) acc[g][e] = 0.0f;
+        for (int e = 0; e < 4; e++) acc[g][e] = 0.0f;
     for (int base = t0; base < t1; base += PIT) {
-        V vv[kUnroll];
-        int pos[kUnroll];
+        f4_t vv[kF32Unroll];
+        int pos[kF32Unroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) {
+        for (int u = 0; u < kF32Unroll; u++) {
             pos[u] = base + u * ROWS + wave * RPW + r;
-            if (pos[u] < t1) vv[u] = *(const V*)(vbase + (size_t)pos[u] * row_stride);
-            else vv[u] = V{};
+            vv[u] = pos[u] < t1 ? *(const f4_t*)(vb + (size_t)pos[u] * row_stride) : f4_t{};
         }
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) {
+        for (int u = 0; u < kF32Unroll; u++)
             if (pos[u] < t1) {
-                const float* pp = sc + (pos[u] - t0) * G;
-                float p[G];
 #pragma unroll
-                for (int g = 0; g < G; g++) p[g] = pp[g];
+                for (int g = 0; g < G; g++) {
+                    const float p = sc[(pos[u] - t0) * G + g];
 #pragma unroll
-                for (int e = 0; e < VEC; e++) {
-                    const float ve = to_f(vv[u][e]);
-#pragma unroll
-                    for (int g = 0; g < G; g++) acc[g][e] = __builtin_fmaf(p[g], ve, acc[g][e]);
+                    for (int e = 0; e < 4; e++) acc[g][e] = __builtin_fmaf(p, vv[u][e], acc[g][e]);
                 }
             }
-        }
     }
-    // Rows of a wave -> row 0, then waves -> LDS.
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
-        for (int e = 0; e < VEC; e++) {
+        for (int e = 0; e < 4; e++) {
             float v = acc[g][e];
 #pragma unroll
             for (int off = LPR; off < 64; off <<= 1) v += __shfl_xor(v, off);
             acc[g][e] = v;
         }
-    __syncthreads();                           // everyone is done with sc
-    float* accbuf = smem;                      // [kWaves][G][D]
+    __syncthreads();
+    float* accbuf = smem;                      // [NW][G][D]
     if (r == 0) {
 #pragma unroll
         for (int g = 0; g < G; g++)
 #pragma unroll
-            for (int e = 0; e < VEC; e++) accbuf[(wave * G + g) * D + c * VEC + e] = acc[g][e];
+            for (int e = 0; e < 4; e++) accbuf[(wave * G + g) * D + c * 4 + e] = acc[g][e];
     }
     __syncthreads();
-
-    T* __restrict__ out = (T*)a.o + ((size_t)b * a.H_q + h0) * D;
-    if (nsplit_b == 1) {
-        for (int idx = tid; idx < G * D; idx += kThreads) {
-            float s = accbuf[idx];
+    float* part = nsplit_b == 1 ? nullptr : partial_at(a, b * a.H_kv + kvh, split, G, D);
+    float* out = (float*)a.o + ((size_t)b * a.H_q + h0) * D;
+    for (int idx = tid; idx < G * D; idx += kF32Threads) {
+        float s = accbuf[idx];
 #pragma unroll
-            for (int w = 1; w < kWaves; w++) s += accbuf[w * G * D + idx];
-            const int g = idx / D;
+        for (int w = 1; w < NW; w++) s += accbuf[w * G * D + idx];
+        const int g = idx / D;
+        if (part) {
+            part[2 * G + idx] = s;
+        } else {
             float l = L[0];
 #pragma unroll
             for (int gg = 1; gg < G; gg++) if (g == gg) l = L[gg];
-            out[idx] = from_f<T>(s / l);
+            out[idx] = s / l;
         }
-        return;
     }
-
-    const int unit = b * a.H_kv + kvh;
-    float* part = a.partials + ((size_t)unit * a.n_split + split) * (G * (D + 2));
-    for (int idx = tid; idx < G * D; idx += kThreads) {
-        float s = accbuf[idx];
-#pragma unroll
-        for (int w = 1; w < kWaves; w++) s += accbuf[w * G * D + idx];
-        part[2 * G + idx] = s;
-    }
-    if (tid < G) {
+    if (part && tid < G) {
         float m = M[0], l = L[0];
 #pragma unroll
         for (int g = 1; g < G; g++) if (tid == g) { m = M[g]; l = L[g]; }
         part[tid] = m;
         part[G + tid] = l;
     }
-    if (!publish_and_check_last(a.counters + unit, nsplit_b)) return;
-    merge_splits<T>(a.partials + (size_t)unit * a.n_split * (G * (D + 2)), nsplit_b, G, D, out, D);
 }
 
+// ---------------------------------------------------------------- generic split ---
 template <typename T>
 __global__ __launch_bounds__(kGenericThreads)
-void decode_attn_generic(cf_decode_attn_args_t a) {
+void split_generic(cf_decode_attn_args_t a) {
     extern __shared__ float smem[];
     const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int D = a.d;
     const int kvh = h / (a.H_q / a.H_kv);
-    const int T_b = min(max((a.seq_lens ? a.seq_lens[b] : a.cache_len) + 1, 1), a.max_seq);
+    const int T_b = attended(a, b);
     const int t0 = split * a.chunk;
     if (t0 >= T_b) return;
     const int t1 = min(t0 + a.chunk, T_b);
@@ -320,7 +422,6 @@ void decode_attn_generic(cf_decode_attn_args_t a) {
     const int nsplit_b = (T_b + a.chunk - 1) / a.chunk;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     constexpr int nw = kGenericThreads / 64;
-
     float* qs = smem;                 // [D]
     float* sc = smem + D;             // [chunk]
     float* red = sc + a.chunk;        // [2 * nw]
@@ -329,12 +430,10 @@ void decode_attn_generic(cf_decode_attn_args_t a) {
     const float qk_scale = a.scale * kLog2e;
     for (int i = tid; i < D; i += kGenericThreads) qs[i] = to_f(q[i]) * qk_scale;
     __syncthreads();
-
     const size_t row_stride = (size_t)a.H_kv * D;
     const size_t unit_off = ((size_t)b * a.max_seq * a.H_kv + kvh) * D;
     const T* __restrict__ kb = (const T*)a.k + unit_off;
     const T* __restrict__ vb = (const T*)a.v + unit_off;
-
     float mloc = -INFINITY;
     for (int t = t0 + tid; t < t1; t += kGenericThreads) {
         const T* kr = kb + (size_t)t * row_stride;
@@ -359,10 +458,8 @@ void decode_attn_generic(cf_decode_attn_args_t a) {
     __syncthreads();
     float L = 0.0f;
     for (int w = 0; w < nw; w++) L += red[nw + w];
-
     T* __restrict__ out = (T*)a.o + ((size_t)b * a.H_q + h) * D;
-    const int unit = b * a.H_q + h;
-    float* part = a.partials + ((size_t)unit * a.n_split + split) * (D + 2);
+    float* part = partial_at(a, b * a.H_q + h, split, 1, D);
     for (int i = tid; i < D; i += kGenericThreads) {
         float acc = 0.0f;
         const T* vc = vb + (size_t)t0 * row_stride + i;
@@ -370,10 +467,64 @@ void decode_attn_generic(cf_decode_attn_args_t a) {
         if (nsplit_b == 1) out[i] = from_f<T>(acc / L);
         else part[2 + i] = acc;
     }
-    if (nsplit_b == 1) return;
-    if (tid == 0) { part[0] = M; part[1] = L; }
-    if (!publish_and_check_last(a.counters + unit, nsplit_b)) return;
-    merge_splits<T>(a.partials + (size_t)unit * a.n_split * (D + 2), nsplit_b, 1, D, out, D);
+    if (nsplit_b > 1 && tid == 0) { part[0] = M; part[1] = L; }
+}
+
+// ------------------------------------------------------------------------ merge ---
+// One workgroup per (unit, head g): unit = (b, kv head) holding Gx heads, or (b, q head)
+// with Gx = 1.  blockIdx.x = unit * Gx + g.
+template <typename T>
+__global__ __launch_bounds__(kMergeThreads)
+void merge_kernel(cf_decode_attn_args_t a, int Gx, int units_per_b) {
+    extern __shared__ float w[];                   // [n_split] weights 2^(m_s - M)
+    __shared__ float s_red[kMergeThreads / 64][2];
+    const int unit = blockIdx.x / Gx, g = blockIdx.x - unit * Gx;
+    const int b = unit / units_per_b;
+    const int D = a.d;
+    const int T_b = attended(a, b);
+    const int nsplit = (T_b + a.chunk - 1) / a.chunk;
+    if (nsplit <= 1) return;                       // finished by the split kernel
+    const int stride = Gx * (D + 2);
+    const float* part = a.partials + (size_t)unit * a.n_split * stride;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+    // M = max_s m_s and den = Σ_s 2^(m_s - M) l_s, all splits read in parallel.
+    float m = -INFINITY;
+    for (int s = tid; s < nsplit; s += blockDim.x) m = fmaxf(m, part[(size_t)s * stride + g]);
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if (lane == 0) s_red[wave][0] = m;
+    __syncthreads();
+    m = s_red[0][0];
+    for (int i = 1; i < nw; i++) m = fmaxf(m, s_red[i][0]);
+    float den = 0.0f;
+    for (int s = tid; s < nsplit; s += blockDim.x) {
+        const float ws = exp2f(part[(size_t)s * stride + g] - m);
+        w[s] = ws;
+        den = __builtin_fmaf(ws, part[(size_t)s * stride + Gx + g], den);
+    }
+    for (int off = 32; off > 0; off >>= 1) den += __shfl_xor(den, off);
+    if (lane == 0) s_red[wave][1] = den;
+    __syncthreads();
+    den = 0.0f;
+    for (int i = 0; i < nw; i++) den += s_red[i][1];
+    const float inv = 1.0f / den;
+    T* out = (T*)a.o + ((size_t)unit * Gx + g) * D;
+    for (int i = tid; i < D; i += blockDim.x) {
+        const float* pa = part + 2 * Gx + g * D + i;
+        float n0 = 0.0f, n1 = 0.0f;
+        int s = 0;
+        for (; s + 8 <= nsplit; s += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = pa[(size_t)(s + j) * stride];
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) {
+                n0 = __builtin_fmaf(w[s + j], v[j], n0);
+                n1 = __builtin_fmaf(w[s + j + 1], v[j + 1], n1);
+            }
+        }
+        for (; s < nsplit; s++) n0 = __builtin_fmaf(w[s], pa[(size_t)s * stride], n0);
+        out[i] = from_f<T>((n0 + n1) * inv);
+    }
 }
 
 bool fast_supported(int elem, int d, int G) {
@@ -382,33 +533,39 @@ bool fast_supported(int elem, int d, int G) {
 }
 
 int quantum(int elem, int d) {
-    const int vec = elem == CF_ELEM_F16 ? 8 : 4;
-    const int lpr = d / vec;
-    return kWaves * (64 / lpr) * kUnroll;
+    if (elem == CF_ELEM_F16) return kF16Quantum;
+    return (kF32Threads / 64) * (64 / (d / 4)) * kF32Unroll;
 }
 
-template <typename T, int D, int G>
-hipError_t launch_fast(const cf_decode_attn_args_t& a, hipStream_t s) {
-    const int sc_floats = a.chunk * G > kWaves * G * D ? a.chunk * G : kWaves * G * D;
-    const size_t lds = (size_t)(sc_floats + 2 * kWaves * G) * sizeof(float);
+bool use_fast(const cf_decode_attn_args_t* a) {
+    const int G = a->H_q / a->H_kv;
+    const bool aligned = (((uintptr_t)a->q | (uintptr_t)a->k | (uintptr_t)a->v | (uintptr_t)a->o) % 16) == 0;
+    return aligned && fast_supported(a->elem, a->d, G);
+}
+
+template <int D, int G>
+hipError_t launch_split_fast(const cf_decode_attn_args_t& a, hipStream_t s) {
     dim3 grid((unsigned)a.n_split, (unsigned)a.H_kv, (unsigned)a.B);
-    hipLaunchKernelGGL((decode_attn_fast<T, D, G>), grid, dim3(kThreads), lds, s, a);
+    if (a.elem == CF_ELEM_F16) {
+        const size_t lds = (size_t)a.chunk * G * sizeof(float);
+        hipLaunchKernelGGL((split_f16<D, G>), grid, dim3(64), lds, s, a);
+    } else {
+        const int NW = kF32Threads / 64;
+        const int sc_floats = a.chunk * G > NW * G * D ? a.chunk * G : NW * G * D;
+        const size_t lds = (size_t)(sc_floats + 2 * NW * G) * sizeof(float);
+        hipLaunchKernelGGL((split_f32<D, G>), grid, dim3(kF32Threads), lds, s, a);
+    }
     return hipGetLastError();
 }
 
-template <typename T, int D>
-hipError_t launch_fast_g(const cf_decode_attn_args_t& a, int G, hipStream_t s) {
+template <int D>
+hipError_t launch_split_g(const cf_decode_attn_args_t& a, int G, hipStream_t s) {
     switch (G) {
-        case 1: return launch_fast<T, D, 1>(a, s);
-        case 2: return launch_fast<T, D, 2>(a, s);
-        case 4: return launch_fast<T, D, 4>(a, s);
-        default: return launch_fast<T, D, 8>(a, s);
+        case 1: return launch_split_fast<D, 1>(a, s);
+        case 2: return launch_split_fast<D, 2>(a, s);
+        case 4: return launch_split_fast<D, 4>(a, s);
+        default: return launch_split_fast<D, 8>(a, s);
     }
-}
-
-template <typename T>
-hipError_t launch_fast_dg(const cf_decode_attn_args_t& a, int G, hipStream_t s) {
-    return a.d == 64 ? launch_fast_g<T, 64>(a, G, s) : launch_fast_g<T, 128>(a, G, s);
 }
 
 }  // namespace
@@ -418,40 +575,56 @@ extern "C" int32_t cf_decode_attn_chunk_quantum(int32_t elem, int32_t d, int32_t
 }
 
 extern "C" int32_t cf_decode_attn_chunk_max(int32_t elem, int32_t d, int32_t group) {
-    return fast_supported(elem, d, group) ? kFastChunkMax : kGenericChunkMax;
+    (void)elem; (void)d; (void)group;
+    return kChunkMax;
 }
 
 extern "C" size_t cf_decode_attn_partials_floats(int32_t B, int32_t H_q, int32_t H_kv, int32_t d,
                                                  int32_t n_split, int32_t elem) {
-    const int G = H_q / H_kv;
-    if (fast_supported(elem, d, G)) return (size_t)B * H_kv * n_split * G * (d + 2);
+    // (b, kv head) units with G heads each, or (b, q head) units: the same total.
+    (void)H_kv; (void)elem;
     return (size_t)B * H_q * n_split * (d + 2);
 }
 
-extern "C" size_t cf_decode_attn_counters(int32_t B, int32_t H_q, int32_t H_kv, int32_t d, int32_t elem) {
-    // Worst case over both kernels (the launcher may pick the generic one for
-    // unaligned pointers): one counter per (b, query head).
-    (void)H_kv; (void)d; (void)elem;
-    return (size_t)B * H_q;
-}
-
-extern "C" int cf_launch_decode_attn(const cf_decode_attn_args_t* a, void* stream) {
+extern "C" int cf_launch_decode_attn_split(const cf_decode_attn_args_t* a, void* stream) {
     hipStream_t s = (hipStream_t)stream;
-    const int G = a->H_q / a->H_kv;
-    // The specialised kernel issues 16-byte loads of Q, K and V rows.
-    const bool aligned = (((uintptr_t)a->q | (uintptr_t)a->k | (uintptr_t)a->v) % 16) == 0;
+    if (a->chunk <= 0 || a->chunk > kChunkMax || a->n_split <= 0) return (int)hipErrorInvalidValue;
     hipError_t err;
-    if (aligned && fast_supported(a->elem, a->d, G)) {
-        err = a->elem == CF_ELEM_F16 ? launch_fast_dg<_Float16>(*a, G, s)
-                                     : launch_fast_dg<float>(*a, G, s);
+    if (use_fast(a)) {
+        const int G = a->H_q / a->H_kv;
+        err = a->d == 64 ? launch_split_g<64>(*a, G, s) : launch_split_g<128>(*a, G, s);
     } else {
         const size_t lds = (size_t)(a->d + a->chunk + 8) * sizeof(float);
         dim3 grid((unsigned)a->n_split, (unsigned)a->H_q, (unsigned)a->B);
         if (a->elem == CF_ELEM_F16)
-            hipLaunchKernelGGL(decode_attn_generic<_Float16>, grid, dim3(kGenericThreads), lds, s, *a);
+            hipLaunchKernelGGL(split_generic<_Float16>, grid, dim3(kGenericThreads), lds, s, *a);
         else
-            hipLaunchKernelGGL(decode_attn_generic<float>, grid, dim3(kGenericThreads), lds, s, *a);
+            hipLaunchKernelGGL(split_generic<float>, grid, dim3(kGenericThreads), lds, s, *a);
         err = hipGetLastError();
     }
     return (int)err;
+}
+
+extern "C" int cf_launch_decode_attn_merge(const cf_decode_attn_args_t* a, void* stream) {
+    if (a->n_split <= 1) return 0;
+    hipStream_t s = (hipStream_t)stream;
+    const bool fast = use_fast(a);
+    const int Gx = fast ? a->H_q / a->H_kv : 1;
+    const int units_per_b = fast ? a->H_kv : a->H_q;
+    const size_t lds = (size_t)a->n_split * sizeof(float);
+    // One thread per output element of a head (rounded up to whole waves, at most 256).
+    int threads = (a->d + 63) / 64 * 64;
+    if (threads > kMergeThreads) threads = kMergeThreads;
+    dim3 grid((unsigned)(a->B * units_per_b * Gx));
+    if (a->elem == CF_ELEM_F16)
+        hipLaunchKernelGGL(merge_kernel<_Float16>, grid, dim3(threads), lds, s, *a, Gx, units_per_b);
+    else
+        hipLaunchKernelGGL(merge_kernel<float>, grid, dim3(threads), lds, s, *a, Gx, units_per_b);
+    return (int)hipGetLastError();
+}
+
+extern "C" int cf_launch_decode_attn(const cf_decode_attn_args_t* a, void* stream) {
+    int rc = cf_launch_decode_attn_split(a, stream);
+    if (rc != 0) return rc;
+    return cf_launch_decode_attn_merge(a, stream);
 }

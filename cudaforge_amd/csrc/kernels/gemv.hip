@@ -124,18 +124,35 @@ __device__ __forceinline__ void kstep<float>(const cf_gemv_args_t& a, const floa
     }
 }
 
+// Store one finished output element (bias added) of segment `seg`, segment-local column n.
+template <typename T>
+__device__ __forceinline__ void store_out(const cf_gemv_args_t& a, const cf_gemv_seg_t& sg, int m, int n, float v) {
+    const T* __restrict__ bias = (const T*)sg.bias;
+    if (bias) v += to_f(bias[n]);
+    const int64_t pos = a.pos_lens ? (int64_t)a.pos_lens[m] : a.pos_uniform;
+    if (a.pos_limit == 0 || (pos >= 0 && pos < a.pos_limit))
+        ((T*)sg.out)[(size_t)m * sg.ld_m + (size_t)pos * sg.ld_pos + n] = from_f<T>(v);
+}
+
+__device__ __forceinline__ int seg_of(const cf_gemv_args_t& a, const Tiles& t, int tile) {
+    int seg = 0;
+#pragma unroll
+    for (int s = 1; s < CF_GEMV_MAX_SEGS; s++)
+        if (s < a.nseg && tile >= t.start[s]) seg = s;
+    return seg;
+}
+
+// Split-K partial kernel.  With one K chunk it applies the epilogue itself; otherwise
+// it writes fp32 partials [k_split][Mp][ncols] (ncols = 128 * column tiles) for
+// gemv_reduce.
 template <typename T>
 __global__ __launch_bounds__(kThreads)
 void gemv_kernel(cf_gemv_args_t a, Tiles t) {
     constexpr int KSTEP = Cfg<T>::KSTEP;
     __shared__ float red[kWaves * kTileVals];  // 32 KB
-    __shared__ int s_last;
 
     const int tile = blockIdx.x, ks = blockIdx.y, mt = blockIdx.z;
-    int seg = 0;
-#pragma unroll
-    for (int s = 1; s < CF_GEMV_MAX_SEGS; s++)
-        if (s < a.nseg && tile >= t.start[s]) seg = s;
+    const int seg = seg_of(a, t, tile);
     const cf_gemv_seg_t& sg = a.seg[seg];
     const int N = (int)sg.n;
     const int nb = (tile - t.start[seg]) * kColTile;
@@ -159,60 +176,43 @@ void gemv_kernel(cf_gemv_args_t a, Tiles t) {
 #pragma unroll
         for (int i = 0; i < 4; i++) red[wave * kTileVals + (c * 4 + i) * 64 + l] = acc[c][i];
     __syncthreads();
-    float vals[kTileVals / kThreads];
+    const int ncols = t.start[a.nseg] * kColTile;
+    const int Mp = gridDim.z * kMTile;
 #pragma unroll
     for (int j = 0; j < kTileVals / kThreads; j++) {
         const int idx = tid + j * kThreads;
         float s = red[idx];
 #pragma unroll
         for (int w = 1; w < kWaves; w++) s += red[w * kTileVals + idx];
-        vals[j] = s;
-    }
-
-    const int ntiles = t.start[a.nseg];
-    const int unit = mt * ntiles + tile;
-    if (a.k_split > 1) {
-        float* part = a.partials + ((size_t)unit * a.k_split + ks) * kTileVals;
-#pragma unroll
-        for (int j = 0; j < kTileVals / kThreads; j++) part[tid + j * kThreads] = vals[j];
-        __threadfence();
-        __syncthreads();
-        if (tid == 0) {
-            const uint32_t prev = atomicAdd(a.counters + unit, 1u);
-            const int last = prev == (uint32_t)(a.k_split - 1);
-            if (last) atomicExch(a.counters + unit, 0u);
-            s_last = last;
-        }
-        __syncthreads();
-        if (!s_last) return;
-        __threadfence();
-        const float* base = a.partials + (size_t)unit * a.k_split * kTileVals;
-#pragma unroll
-        for (int j = 0; j < kTileVals / kThreads; j++) {
-            const int idx = tid + j * kThreads;
-            float s = 0.0f;
-            for (int kk = 0; kk < a.k_split; kk++) s += base[(size_t)kk * kTileVals + idx];
-            vals[j] = s;
-        }
-    }
-
-    // Epilogue: bias and scatter.
-    const T* __restrict__ bias = (const T*)sg.bias;
-    T* __restrict__ out = (T*)sg.out;
-#pragma unroll
-    for (int j = 0; j < kTileVals / kThreads; j++) {
-        const int idx = tid + j * kThreads;
         const int li = idx & 63, ci = idx >> 6;
-        const int c = ci >> 2, i = ci & 3;
-        const int n = nb + tile_col<T>(c, i, li);
+        const int lc = tile_col<T>(ci >> 2, ci & 3, li);
         const int mm = mt * kMTile + (li & 15);
-        if (n < N && mm < a.M) {
-            float v = vals[j];
-            if (bias) v += to_f(bias[n]);
-            const int64_t pos = a.pos_lens ? (int64_t)a.pos_lens[mm] : a.pos_uniform;
-            if (a.pos_limit == 0 || (pos >= 0 && pos < a.pos_limit))
-                out[(size_t)mm * sg.ld_m + (size_t)pos * sg.ld_pos + n] = from_f<T>(v);
+        if (a.k_split > 1) {
+            a.partials[((size_t)ks * Mp + mm) * ncols + (size_t)tile * kColTile + lc] = s;
+        } else if (nb + lc < N && mm < a.M) {
+            store_out<T>(a, sg, mm, nb + lc, s);
         }
+    }
+}
+
+// Sums the K-chunk partials of every output element and applies the epilogue.
+template <typename T>
+__global__ __launch_bounds__(256)
+void gemv_reduce(cf_gemv_args_t a, Tiles t) {
+    const int ncols = t.start[a.nseg] * kColTile;
+    const int Mp = (a.M + kMTile - 1) / kMTile * kMTile;
+    const size_t total = (size_t)a.M * ncols;
+    const size_t plane = (size_t)Mp * ncols;
+    for (size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (size_t)gridDim.x * 256) {
+        const int m = (int)(idx / ncols), col = (int)(idx - (size_t)m * ncols);
+        const int tile = col / kColTile;
+        const int seg = seg_of(a, t, tile);
+        const int n = (tile - t.start[seg]) * kColTile + (col - tile * kColTile);
+        if (n >= a.seg[seg].n) continue;
+        const float* p = a.partials + (size_t)m * ncols + col;
+        float s = 0.0f;
+        for (int kk = 0; kk < a.k_split; kk++) s += p[kk * plane];
+        store_out<T>(a, a.seg[seg], m, n, s);
     }
 }
 
@@ -230,11 +230,9 @@ Tiles make_tiles(const cf_gemv_args_t* a) {
     int chunk = (a->K + ks - 1) / ks;
     chunk = (chunk + kstep - 1) / kstep * kstep;
     t.k_chunk = chunk;
-    const size_t esz = a->elem == CF_ELEM_F16 ? 2 : 4;
     int ok = (a->K % vec == 0) && (((uintptr_t)a->x) % 16 == 0);
     for (int s = 0; s < a->nseg; s++)
         ok = ok && (a->seg[s].n % vec == 0) && (((uintptr_t)a->seg[s].w) % 16 == 0);
-    (void)esz;
     t.vec_ok = ok;
     return t;
 }
@@ -246,27 +244,35 @@ extern "C" int32_t cf_gemv_k_step(int32_t elem) {
     return elem == CF_ELEM_F16 ? Cfg<_Float16>::KSTEP : Cfg<float>::KSTEP;
 }
 
-extern "C" size_t cf_gemv_counters(const cf_gemv_args_t* a) {
-    const Tiles t = make_tiles(a);
-    return (size_t)t.start[a->nseg] * (size_t)((a->M + kMTile - 1) / kMTile);
-}
-
 extern "C" size_t cf_gemv_partials_floats(const cf_gemv_args_t* a) {
     if (a->k_split <= 1) return 0;
-    return cf_gemv_counters(a) * (size_t)a->k_split * kTileVals;
+    const Tiles t = make_tiles(a);
+    const size_t Mp = (size_t)((a->M + kMTile - 1) / kMTile) * kMTile;
+    return (size_t)a->k_split * Mp * (size_t)t.start[a->nseg] * kColTile;
 }
 
 extern "C" int cf_launch_gemv(const cf_gemv_args_t* a, void* stream) {
     const Tiles t = make_tiles(a);
-    // Every K chunk must be non-empty for the counter to reach k_split.
+    // Every K chunk must be non-empty (each writes its full partial plane).
     const int ks = a->k_split > 0 ? a->k_split : 1;
     if ((ks - 1) * t.k_chunk >= a->K) return (int)hipErrorInvalidValue;
     cf_gemv_args_t args = *a;
     args.k_split = ks;
-    dim3 grid((unsigned)t.start[a->nseg], (unsigned)ks, (unsigned)((a->M + kMTile - 1) / kMTile));
+    hipStream_t s = (hipStream_t)stream;
+    const int m_tiles = (a->M + kMTile - 1) / kMTile;
+    dim3 grid((unsigned)t.start[a->nseg], (unsigned)ks, (unsigned)m_tiles);
     if (a->elem == CF_ELEM_F16)
-        hipLaunchKernelGGL(gemv_kernel<_Float16>, grid, dim3(kThreads), 0, (hipStream_t)stream, args, t);
+        hipLaunchKernelGGL(gemv_kernel<_Float16>, grid, dim3(kThreads), 0, s, args, t);
     else
-        hipLaunchKernelGGL(gemv_kernel<float>, grid, dim3(kThreads), 0, (hipStream_t)stream, args, t);
+        hipLaunchKernelGGL(gemv_kernel<float>, grid, dim3(kThreads), 0, s, args, t);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || ks == 1) return (int)e;
+    const size_t total = (size_t)a->M * t.start[a->nseg] * kColTile;
+    size_t blocks = (total + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    if (a->elem == CF_ELEM_F16)
+        hipLaunchKernelGGL(gemv_reduce<_Float16>, dim3((unsigned)blocks), dim3(256), 0, s, args, t);
+    else
+        hipLaunchKernelGGL(gemv_reduce<float>, dim3((unsigned)blocks), dim3(256), 0, s, args, t);
     return (int)hipGetLastError();
 }

@@ -22,9 +22,10 @@ enum { CF_ELEM_F32 = 0, CF_ELEM_F16 = 1 };
  *
  * q: (B, H_q, d); k/v caches: (B, max_seq, H_kv, d); o: (B, H_q, d), all in `elem`.
  * Sequence b attends positions 0 .. T_b-1 with T_b = seq_lens ? seq_lens[b] + 1
- * : cache_len + 1.  Grid: n_split splits of `chunk` positions per (b, kv head); a
- * split past T_b exits at once.  The last split to finish for a (b, kv head) merges
- * the partial (max, sum, acc) tuples from `partials` and resets its counter.
+ * : cache_len + 1.  The split kernel covers n_split splits of `chunk` positions per
+ * (b, kv head) (a split past T_b exits at once) and writes partial (max, sum, acc)
+ * tuples to `partials`; the merge kernel combines them.  A sequence with one split is
+ * written directly by the split kernel.
  * ------------------------------------------------------------------------------- */
 typedef struct {
     const void*    q;
@@ -33,7 +34,6 @@ typedef struct {
     void*          o;
     const int32_t* seq_lens;   /* device, NULL = uniform cache_len */
     float*         partials;   /* workspace */
-    uint32_t*      counters;   /* workspace, zero on entry, left zero on exit */
     int32_t        B, H_q, H_kv, d;
     int32_t        max_seq, cache_len;
     int32_t        chunk, n_split;
@@ -47,9 +47,9 @@ int32_t cf_decode_attn_chunk_max(int32_t elem, int32_t d, int32_t group);
 /* Workspace floats needed for the partials of a launch. */
 size_t  cf_decode_attn_partials_floats(int32_t B, int32_t H_q, int32_t H_kv, int32_t d,
                                        int32_t n_split, int32_t elem);
-/* Counters needed (one per (b, kv head) or (b, q head)). */
-size_t  cf_decode_attn_counters(int32_t B, int32_t H_q, int32_t H_kv, int32_t d, int32_t elem);
-int     cf_launch_decode_attn(const cf_decode_attn_args_t* a, void* stream);
+int     cf_launch_decode_attn_split(const cf_decode_attn_args_t* a, void* stream);
+int     cf_launch_decode_attn_merge(const cf_decode_attn_args_t* a, void* stream);
+int     cf_launch_decode_attn(const cf_decode_attn_args_t* a, void* stream);  /* split + merge */
 
 /* ---------------------------------------------------------------------------------
  * Skinny GEMM for decode projections: Y[m, n] = Σ_k X[m, k] W[k, n] + bias[n] for
@@ -58,8 +58,8 @@ int     cf_launch_decode_attn(const cf_decode_attn_args_t* a, void* stream);
  * covers global columns [col0_s, col0_s + n_s) and writes element (m, j) to
  *   out_s + m*ld_m_s + pos(m)*ld_pos_s + j,   pos(m) = pos_lens ? pos_lens[m] : pos_uniform.
  * That places decode's K_new / V_new rows straight into the KV cache.
- * K is split across `k_split` workgroups; the last one per column tile reduces the
- * partials from the workspace, adds the bias and stores.
+ * K is split across `k_split` workgroups writing fp32 partials to the workspace; a
+ * second kernel sums them, adds the bias and stores (k_split = 1: one kernel).
  * ------------------------------------------------------------------------------- */
 #define CF_GEMV_MAX_SEGS 3
 typedef struct {
@@ -82,14 +82,12 @@ typedef struct {
                                  0 = no limit */
     int32_t        k_split;   /* >= 1; K chunk = ceil(K / k_split) rounded to the k step */
     float*         partials;  /* workspace */
-    uint32_t*      counters;  /* workspace, zero on entry, left zero on exit */
     int32_t        elem;
 } cf_gemv_args_t;
 
 int32_t cf_gemv_col_tile(int32_t elem);
 int32_t cf_gemv_k_step(int32_t elem);
 size_t  cf_gemv_partials_floats(const cf_gemv_args_t* a);
-size_t  cf_gemv_counters(const cf_gemv_args_t* a);
 int     cf_launch_gemv(const cf_gemv_args_t* a, void* stream);
 
 /* ---------------------------------------------------------------------------------

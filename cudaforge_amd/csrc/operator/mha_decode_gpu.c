@@ -15,7 +15,10 @@
 #include "op_common.h"
 #include "../kernels/kernels.h"
 
+#include <stdlib.h>
 #include <string.h>
+
+#include "op_timing.h"
 
 static int64_t g_chunk_override = 0;
 
@@ -56,8 +59,11 @@ static void plan_split(int elem, const decode_shape_t* s, int64_t t_max, int64_t
     if (g_chunk_override > 0) {
         c = cf_ceil_div(g_chunk_override, q) * q;
     } else {
+        /* Enough workgroups to keep every CU's memory pipeline full: the fp16 kernel
+         * is one wave per workgroup, so it wants ~16 per CU; the others are 2-4 waves. */
         const int64_t units = s->B * (fast ? s->H_kv : s->H);
-        const int64_t target = 4 * (int64_t)cf_cu_count();
+        const int64_t per_cu = (fast && elem == CF_ELEM_F16) ? 8 : 4;
+        const int64_t target = per_cu * (int64_t)cf_cu_count();
         int64_t n = cf_ceil_div(target, units);
         const int64_t nmax = cf_ceil_div(t_max, q);
         if (n > nmax) n = nmax;
@@ -66,6 +72,8 @@ static void plan_split(int elem, const decode_shape_t* s, int64_t t_max, int64_t
     }
     if (c > cmax) c = cmax;
     if (c < q) c = q;
+    /* The merge kernel keeps 2 floats per (split, head) in LDS: at most 1024 splits. */
+    if (cf_ceil_div(t_max, c) > 1024) c = cf_ceil_div(cf_ceil_div(t_max, 1024), q) * q;
     *chunk = c;
     *n_split = cf_ceil_div(t_max, c);
 }
@@ -98,8 +106,8 @@ static size_t attn_args(int elem, const decode_shape_t* s, const int32_t* lens,
     return cf_decode_attn_partials_floats(a->B, a->H_q, a->H_kv, a->d, a->n_split, elem) * sizeof(float);
 }
 
-static int attn_core(int elem, const void* inputs[], void* outputs[],
-                     const operator_params_t* params, stream_t* stream) {
+static int attn_prepare(int elem, const void* inputs[], void* outputs[],
+                        const operator_params_t* params, cf_decode_attn_args_t* a) {
     if (!params || !inputs || !outputs) return -1;
     const mha_decode_params_t* p = (const mha_decode_params_t*)params;
     decode_shape_t s;
@@ -111,18 +119,59 @@ static int attn_core(int elem, const void* inputs[], void* outputs[],
         lens = (const int32_t*)inputs[3];
         if (!lens) return -1;
     }
-    cf_decode_attn_args_t a;
-    const size_t part_bytes = attn_args(elem, &s, lens, &a);
-    if (cf_decode_attn_counters(a.B, a.H_q, a.H_kv, a.d, elem) * 4 > gpu_workspace_counter_bytes()) return -1;
+    const size_t part_bytes = attn_args(elem, &s, lens, a);
     char* ws = (char*)gpu_workspace_get(part_bytes);
     if (!ws) return -1;
-    a.counters = (uint32_t*)ws;
-    a.partials = (float*)(ws + gpu_workspace_counter_bytes());
-    a.q = inputs[0];
-    a.k = inputs[1];
-    a.v = inputs[2];
-    a.o = outputs[0];
-    a.scale = p->scale;
+    a->partials = (float*)ws;
+    a->q = inputs[0];
+    a->k = inputs[1];
+    a->v = inputs[2];
+    a->o = outputs[0];
+    a->scale = p->scale;
+    return 0;
+}
+
+int mha_decode_attn_kernel_times(const void* inputs[], void* outputs[], const operator_params_t* params,
+                                 stream_t* stream, int elem_f16, int warmup, int iters,
+                                 float* ms_split, float* ms_merge) {
+    if (!ms_split || !ms_merge || iters <= 0 || iters > 4096 || warmup < 0) return -1;
+    cf_decode_attn_args_t a;
+    int rc = attn_prepare(elem_f16 ? CF_ELEM_F16 : CF_ELEM_F32, inputs, outputs, params, &a);
+    if (rc != 0) return rc;
+    void* st = cf_stream_of(stream);
+    for (int i = 0; i < warmup; i++)
+        if ((rc = cf_launch_decode_attn(&a, st)) != 0) return rc;
+    gpu_event_t* ev = (gpu_event_t*)calloc((size_t)(3 * iters), sizeof(gpu_event_t));
+    if (!ev) return -1;
+    for (int i = 0; i < 3 * iters && rc == 0; i++) rc = gpu_event_create(&ev[i]);
+    for (int i = 0; i < iters && rc == 0; i++) {
+        rc = gpu_event_record(ev[3 * i], st);
+        if (rc == 0) rc = cf_launch_decode_attn_split(&a, st);
+        if (rc == 0) rc = gpu_event_record(ev[3 * i + 1], st);
+        if (rc == 0) rc = cf_launch_decode_attn_merge(&a, st);
+        if (rc == 0) rc = gpu_event_record(ev[3 * i + 2], st);
+    }
+    if (rc == 0) rc = gpu_event_synchronize(ev[3 * iters - 1]);
+    double s_sum = 0.0, m_sum = 0.0;
+    for (int i = 0; i < iters && rc == 0; i++) {
+        float t1 = 0.0f, t2 = 0.0f;
+        rc = gpu_event_elapsed_ms(&t1, ev[3 * i], ev[3 * i + 1]);
+        if (rc == 0) rc = gpu_event_elapsed_ms(&t2, ev[3 * i + 1], ev[3 * i + 2]);
+        s_sum += t1;
+        m_sum += t2;
+    }
+    for (int i = 0; i < 3 * iters; i++) if (ev[i]) gpu_event_destroy(ev[i]);
+    free(ev);
+    *ms_split = (float)(s_sum / iters);
+    *ms_merge = (float)(m_sum / iters);
+    return rc;
+}
+
+static int attn_core(int elem, const void* inputs[], void* outputs[],
+                     const operator_params_t* params, stream_t* stream) {
+    cf_decode_attn_args_t a;
+    const int rc = attn_prepare(elem, inputs, outputs, params, &a);
+    if (rc != 0) return rc;
     return cf_launch_decode_attn(&a, cf_stream_of(stream));
 }
 
@@ -207,25 +256,17 @@ static int decode_op(int elem, const void* inputs[], void* outputs[],
     g2.elem = elem;
     g2.k_split = gemv_k_split(elem, s.H * s.d, cf_ceil_div(s.D, tile), m_tiles);
 
-    if (cf_gemv_counters(&g1) * 4 > gpu_workspace_counter_bytes() ||
-        cf_gemv_counters(&g2) * 4 > gpu_workspace_counter_bytes() ||
-        cf_decode_attn_counters(a.B, a.H_q, a.H_kv, a.d, elem) * 4 > gpu_workspace_counter_bytes())
-        return -1;
-
     size_t cur = 0;
     const size_t off_q = cf_ws_take(&cur, (size_t)s.B * s.H * s.d * esz);
     const size_t off_o = cf_ws_take(&cur, (size_t)s.B * s.H * s.d * esz);
     const size_t off_p1 = cf_ws_take(&cur, cf_gemv_partials_floats(&g1) * sizeof(float));
     const size_t off_pa = cf_ws_take(&cur, attn_part);
     const size_t off_p2 = cf_ws_take(&cur, cf_gemv_partials_floats(&g2) * sizeof(float));
-    char* ws = (char*)gpu_workspace_get(cur);
-    if (!ws) return -1;
-    char* data = ws + gpu_workspace_counter_bytes();
-    uint32_t* counters = (uint32_t*)ws;
+    char* data = (char*)gpu_workspace_get(cur);
+    if (!data) return -1;
 
     g1.seg[0].out = data + off_q;
     g1.partials = (float*)(data + off_p1);
-    g1.counters = counters;
     if ((rc = cf_launch_gemv(&g1, st)) != 0) return rc;
 
     a.q = data + off_q;
@@ -234,12 +275,10 @@ static int decode_op(int elem, const void* inputs[], void* outputs[],
     a.o = data + off_o;
     a.scale = p->scale;
     a.partials = (float*)(data + off_pa);
-    a.counters = counters;
     if ((rc = cf_launch_decode_attn(&a, st)) != 0) return rc;
 
     g2.x = data + off_o;
     g2.partials = (float*)(data + off_p2);
-    g2.counters = counters;
     return cf_launch_gemv(&g2, st);
 }
 

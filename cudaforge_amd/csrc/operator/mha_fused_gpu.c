@@ -38,9 +38,8 @@ static int fused_op(int elem, const void* inputs[], void* outputs[],
     const size_t off_k = cf_ws_take(&cur, (size_t)(B * S * kvd) * esz);
     const size_t off_v = cf_ws_take(&cur, (size_t)(B * S * kvd) * esz);
     const size_t off_o = cf_ws_take(&cur, (size_t)(B * S * D) * esz);
-    char* ws = (char*)gpu_workspace_get(cur);
-    if (!ws) return -1;
-    char* data = ws + gpu_workspace_counter_bytes();
+    char* data = (char*)gpu_workspace_get(cur);
+    if (!data) return -1;
 
     cf_gemm_args_t g;
     memset(&g, 0, sizeof(g));

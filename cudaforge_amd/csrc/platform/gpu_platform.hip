@@ -14,7 +14,6 @@
 namespace {
 
 constexpr int kMaxDevices = 16;
-constexpr size_t kCounterBytes = 256 * 1024;  // 65536 split-reduction counters
 
 struct Workspace {
     void*  base = nullptr;
@@ -196,13 +195,11 @@ int gpu_event_elapsed_ms(float* ms, gpu_event_t start, gpu_event_t stop) {
     return rc(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
 }
 
-size_t gpu_workspace_counter_bytes(void) { return kCounterBytes; }
-
 void* gpu_workspace_get(size_t bytes) {
     const int dev = current_device();
     if (dev < 0 || dev >= kMaxDevices) return nullptr;
     Workspace& ws = g_ws[dev];
-    const size_t need = kCounterBytes + ((bytes + 255) / 256) * 256;
+    const size_t need = ((bytes + 255) / 256) * 256;
     if (ws.base && ws.bytes >= need) return ws.base;
     // Grow: in-flight kernels may still use the old buffer.
     if (ws.base) {
@@ -214,10 +211,6 @@ void* gpu_workspace_get(size_t bytes) {
     size_t grow = need < (size_t)64 << 20 ? (size_t)64 << 20 : need + need / 4;
     void* p = gpu_device_alloc(grow);
     if (!p) return nullptr;
-    if (hipMemset(p, 0, kCounterBytes) != hipSuccess) {
-        (void)hipFree(p);
-        return nullptr;
-    }
     ws.base = p;
     ws.bytes = grow;
     return p;

@@ -98,14 +98,12 @@ int   gpu_event_record(gpu_event_t ev, gpu_stream_t stream);
 int   gpu_event_synchronize(gpu_event_t ev);
 int   gpu_event_elapsed_ms(float* ms, gpu_event_t start, gpu_event_t stop);
 
-/* Persistent workspace of the current device.  Returns a device buffer of at least
- * `bytes` bytes, 256-byte aligned, whose first `gpu_workspace_counter_bytes()` bytes
- * are split-reduction counters that the kernels leave at zero after every call.
- * The buffer grows (one synchronous reallocation) when a larger size is requested and
- * is otherwise reused; calls that share it must be ordered on one stream.
- * Returns NULL on allocation failure. */
+/* Persistent scratch of the current device for split partials and projections.
+ * Returns a 256-byte aligned device buffer of at least `bytes` bytes.  The buffer grows
+ * (one synchronous reallocation, never during a launch sequence) when a larger size is
+ * requested and is otherwise reused: operators that share it must be ordered on one
+ * stream.  Returns NULL on allocation failure. */
 void*  gpu_workspace_get(size_t bytes);
-size_t gpu_workspace_counter_bytes(void);
 size_t gpu_workspace_size(void);
 void   gpu_workspace_release(void);
 

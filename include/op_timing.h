@@ -24,6 +24,14 @@ int operator_time(const char* name, const void* inputs[], void* outputs[],
                   const operator_params_t* params, stream_t* stream,
                   int warmup, int iters, float* ms_total);
 
+/* The decode attention core (mha_decode_attn_{f16,f32}_cuda, same arguments) run
+ * `iters` times (<= 4096) after `warmup` calls, with HIP events recorded around its
+ * split kernel and its merge kernel separately; stores the mean duration of each (ms).
+ * elem_f16 selects the fp16 (1) or fp32 (0) entry. */
+int mha_decode_attn_kernel_times(const void* inputs[], void* outputs[], const operator_params_t* params,
+                                 stream_t* stream, int elem_f16, int warmup, int iters,
+                                 float* ms_split, float* ms_merge);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,345 @@
+"""CPU tests of the C-ABI boundary and the host logic (no GPU work is launched).
+
+- every function declared in include/*.h is exported by libcudaforge_amd.so;
+- struct layouts match the reference interface sizes;
+- the registry holds exactly the HIP operators, under the reference's names;
+- argument validation returns -1 before touching the device (mha_decode.c:14-16,
+  mha_fused_cuda.cu:940-941 error contract);
+- the graph: topological build, cycle detection, the reference's name-resolution rule
+  (graph.c:836-884), and execution through graph_execute / inference_session_run with the
+  oracle registered as the CPU ops (the reference's CPU-vs-reference graph tests,
+  tests/test_bert_mha.c:167-306, in a CPU-only process).
+"""
+
+import ctypes
+import os
+import re
+import subprocess
+from ctypes import POINTER, c_int, c_int64, c_void_p
+
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import DecodeCase, FusedCase
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INCLUDE = os.path.join(ROOT, "include")
+
+OP_MHA_FUSED, OP_MHA_DECODE, OP_CAUSAL_MASK, OP_RELU, OP_INPUT, OP_OUTPUT = 28, 29, 30, 0, 36, 37
+DT_F32, DT_F16 = 0, 1
+
+
+def declared_functions():
+    names = set()
+    for fn in sorted(os.listdir(INCLUDE)):
+        if not fn.endswith(".h"):
+            continue
+        src = open(os.path.join(INCLUDE, fn)).read()
+        src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+        src = re.sub(r"//[^\n]*", "", src)
+        src = re.sub(r"^\s*#[^\n]*", "", src, flags=re.M)
+        depth, stmt = 0, ""
+        for ch in src:
+            if ch == "{":
+                depth += 1
+                stmt = ""
+                continue
+            if ch == "}":
+                depth -= 1
+                stmt = ""
+                continue
+            if depth > 0 and not stmt.lstrip().startswith("extern"):
+                # inside extern "C" { ... } blocks depth is 1: treat that as top level
+                pass
+            stmt += ch
+            if ch == ";":
+                s = " ".join(stmt.split())
+                stmt = ""
+                if s.startswith("typedef") or "(" not in s or "(*" in s:
+                    continue
+                m = re.match(r"^(?:extern\s+)?[\w\s\*]+?\b(\w+)\s*\(", s)
+                if m:
+                    names.add(m.group(1))
+    return names
+
+
+def test_every_declared_symbol_is_exported(native):
+    names = declared_functions()
+    assert len(names) > 60
+    out = subprocess.run(["nm", "-D", "--defined-only", native._name], capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = sorted(n for n in names if n not in exported)
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_struct_layouts(native):
+    import cudaforge_amd as cf
+    assert ctypes.sizeof(cf.MhaDecodeParams) == 64       # mha_decode_int.h:6-15
+    assert ctypes.sizeof(cf.MhaFusedParams) == 56        # mha_fused_int.h:7-17
+    assert ctypes.sizeof(cf.TensorT) == 160              # platform.h:36-44
+    assert ctypes.sizeof(cf.OperatorRegistry) == 40      # operator.h:34-40
+
+
+def test_registry_names(native):
+    names = {native.operator_at(i).contents.name.decode() for i in range(native.operator_count())}
+    hip = {"mha_decode_f32_cuda", "mha_decode_f16_cuda", "mha_decode_attn_f32_cuda", "mha_decode_attn_f16_cuda",
+           "mha_fused_f32_cuda", "mha_fused_f16_cuda", "causal_mask_f32_cuda"}
+    assert hip <= names
+    assert native.operator_init_all() == 0              # idempotent
+    assert native.operator_count() == len(names)
+    assert not native.operator_find(b"mha_fused_f32_nonexistent")
+    e = native.operator_find(b"mha_fused_f16_cuda").contents
+    assert e.data_type == b"f16"
+
+
+def _slots(vals):
+    return (c_void_p * len(vals))(*vals)
+
+
+DUMMY = ctypes.create_string_buffer(64)
+DP = ctypes.addressof(DUMMY)
+
+
+@pytest.mark.parametrize("mutate,expect", [
+    (lambda p, ins: None, None),
+    (lambda p, ins: ins.__setitem__(4, None), -1),            # NULL bias (mha_decode.c:15)
+    (lambda p, ins: setattr(p, "num_kv_heads", 3), -1),       # 4 % 3 != 0
+    (lambda p, ins: setattr(p, "hidden_size", 100), -1),      # H*d != D
+    (lambda p, ins: setattr(p, "cache_len", 8), -1),          # cache_len >= max_seq
+    (lambda p, ins: setattr(p, "batch_size", 0), -1),
+    (lambda p, ins: setattr(p, "head_dim", 0), -1),
+])
+def test_decode_argument_validation(native, mutate, expect):
+    import cudaforge_amd as cf
+    p = cf.MhaDecodeParams(1, 32, 4, 2, 8, 0.35, 0, 8)
+    ins = [DP] * 11
+    mutate(p, ins)
+    if expect is None:
+        return      # the valid case is exercised on the GPU
+    for name in ("mha_decode_f32_cuda", "mha_decode_f16_cuda"):
+        rc = native[name](_slots(ins), _slots([DP] * 3), ctypes.byref(p), None) if False else \
+            getattr(native, name)(ctypes.cast(_slots(ins), POINTER(c_void_p)),
+                                  ctypes.cast(_slots([DP] * 3), POINTER(c_void_p)), ctypes.addressof(p), None)
+        assert rc == expect
+
+
+def test_decode_null_params_and_ragged_without_lengths(native):
+    import cudaforge_amd as cf
+    f = native.mha_decode_f32_cuda
+    ins = ctypes.cast(_slots([DP] * 11 + [None]), POINTER(c_void_p))
+    outs = ctypes.cast(_slots([DP] * 3), POINTER(c_void_p))
+    assert f(ins, outs, None, None) == -1
+    p = cf.MhaDecodeParams(1, 32, 4, 2, 8, 0.35, -1, 8)    # ragged, slot 11 NULL
+    assert f(ins, outs, ctypes.addressof(p), None) == -1
+    g = native.mha_decode_attn_f16_cuda
+    assert g(ctypes.cast(_slots([DP, DP, DP, None]), POINTER(c_void_p)),
+             ctypes.cast(_slots([DP]), POINTER(c_void_p)), ctypes.addressof(p), None) == -1
+
+
+def test_fused_argument_validation(native):
+    import cudaforge_amd as cf
+    f = native.mha_fused_f16_cuda
+    good = [DP] * 10
+    outs = ctypes.cast(_slots([DP]), POINTER(c_void_p))
+    p = cf.MhaFusedParams(1, 4, 16, 2, 2, 8, 0.35, False, False)
+    bad = list(good)
+    bad[0] = None
+    assert f(ctypes.cast(_slots(bad), POINTER(c_void_p)), outs, ctypes.addressof(p), None) == -1
+    assert f(ctypes.cast(_slots(good), POINTER(c_void_p)), ctypes.cast(_slots([None]), POINTER(c_void_p)),
+             ctypes.addressof(p), None) == -1
+    assert f(ctypes.cast(_slots(good), POINTER(c_void_p)), outs, None, None) == -1
+    p.hidden_size = 15
+    assert f(ctypes.cast(_slots(good), POINTER(c_void_p)), outs, ctypes.addressof(p), None) == -1
+    p.hidden_size, p.num_kv_heads = 16, 3
+    assert native.mha_fused_f32_cuda(ctypes.cast(_slots(good), POINTER(c_void_p)), outs, ctypes.addressof(p),
+                                     None) == -1
+
+
+# ----------------------------------------------------------------------- graph ---
+
+class Graph:
+    """Small wrapper over the graph C-ABI; tensors are owned by the graph once added."""
+
+    def __init__(self, lib):
+        self.lib = lib
+        self.g = lib.graph_create()
+        assert self.g
+
+    def tensor(self, arr, dtype=DT_F32):
+        arr = np.ascontiguousarray(arr)
+        shape = (c_int64 * max(arr.ndim, 1))(*arr.shape)
+        t = self.lib.tensor_create(dtype, arr.ndim, shape)
+        assert t
+        tt = ctypes.cast(t, POINTER(__import__("cudaforge_amd").TensorT)).contents
+        ctypes.memmove(tt.data, arr.ctypes.data, arr.nbytes)
+        return t, self.lib.graph_add_tensor(self.g, t)
+
+    def node(self, op, ins, outs, weights=(), params=None):
+        ia = (c_int * max(len(ins), 1))(*ins)
+        oa = (c_int * max(len(outs), 1))(*outs)
+        wa = (c_void_p * max(len(weights), 1))(*weights)
+        pp = ctypes.addressof(params) if params is not None else None
+        ps = ctypes.sizeof(params) if params is not None else 0
+        return self.lib.graph_add_node(self.g, op, len(ins), ia, len(outs), oa, len(weights), wa, pp, ps)
+
+    def read(self, t, shape, dtype=np.float32):
+        import cudaforge_amd as cf
+        tt = ctypes.cast(t, POINTER(cf.TensorT)).contents
+        out = np.empty(shape, dtype)
+        ctypes.memmove(out.ctypes.data, tt.data, out.nbytes)
+        return out
+
+    def destroy(self):
+        self.lib.graph_destroy(self.g)
+
+
+_cpu_regs = []
+
+
+@pytest.fixture(scope="module")
+def cpu_ops(native):
+    """Register the oracle as the CPU ops mha_fused_f32 / mha_decode_f32 / causal_mask_f32
+    (the reference's CPU registrations, operator_registry.def:35-37)."""
+    import cudaforge_amd as cf
+    from cudaforge_amd._native import OP_FUNC
+    for name, fn in (("mha_fused_f32", "oracle_op_mha_fused_f32"), ("mha_decode_f32", "oracle_op_mha_decode_f32"),
+                     ("causal_mask_f32", "oracle_op_causal_mask_f32")):
+        if native.operator_find(name.encode()):
+            continue
+        entry = cf.OperatorRegistry(name.encode(), b"f32", OP_FUNC(O.cpu_op_pointer(fn)), 1, 0)
+        _cpu_regs.append(entry)
+        assert native.operator_register(ctypes.addressof(entry)) == 0
+    return native
+
+
+def test_graph_topological_order_and_cycle(native):
+    g = Graph(native)
+    _, a = g.tensor(np.zeros(4, np.float32))
+    _, b = g.tensor(np.zeros(4, np.float32))
+    _, c = g.tensor(np.zeros(4, np.float32))
+    n2 = g.node(OP_RELU, [b], [c])
+    n1 = g.node(OP_RELU, [a], [b])
+    assert native.graph_build(g.g) == 0
+    gs = ctypes.cast(g.g, POINTER(c_int * 8)).contents   # first field num_nodes
+    assert gs[0] == 2
+    order_ptr = ctypes.cast(g.g + 24, POINTER(POINTER(c_int))).contents   # topo_order
+    assert [order_ptr[0], order_ptr[1]] == [n1, n2]
+    g.destroy()
+    g = Graph(native)
+    _, a = g.tensor(np.zeros(4, np.float32))
+    _, b = g.tensor(np.zeros(4, np.float32))
+    g.node(OP_RELU, [a], [b])
+    g.node(OP_RELU, [b], [a])
+    assert native.graph_build(g.g) == -1
+    g.destroy()
+
+
+def build_fused_graph(lib, c: FusedCase, f16_out=False):
+    g = Graph(lib)
+    tX, iX = g.tensor(c.X)
+    tR, iR = g.tensor(c.R if c.R is not None else np.zeros_like(c.X))
+    tY, iY = g.tensor(np.zeros_like(c.X), DT_F16 if f16_out else DT_F32)
+    ws = [g.tensor(w)[0] for w in (c.WQ, c.bQ, c.WK, c.bK, c.WV, c.bV, c.WO, c.bO)]
+    p = O.fused_params(c.B, c.S, c.D, c.H, c.H_kv, c.d, c.residual, c.causal)
+    nid = g.node(OP_MHA_FUSED, [iX, iR], [iY], ws, p)
+    g.lib.graph_set_input(g.g, g.node(OP_INPUT, [], [iX]))
+    g.lib.graph_set_output(g.g, g.node(OP_OUTPUT, [iY], []))
+    assert lib.graph_build(g.g) == 0
+    return g, nid, tX, tY
+
+
+def test_graph_name_resolution(cpu_ops):
+    lib = cpu_ops
+    c = FusedCase(1, 4, 2, 2, 8, fill="lcg", residual=True)
+    buf = ctypes.create_string_buffer(64)
+    g, nid, _, _ = build_fused_graph(lib, c)
+    assert lib.graph_resolve_op(g.g, nid, True, buf, 64) and buf.value == b"mha_fused_f32_cuda"
+    assert lib.graph_resolve_op(g.g, nid, False, buf, 64) and buf.value == b"mha_fused_f32"
+    g.destroy()
+    g, nid, _, _ = build_fused_graph(lib, c, f16_out=True)
+    assert lib.graph_resolve_op(g.g, nid, True, buf, 64) and buf.value == b"mha_fused_f16_cuda"
+    g.destroy()
+
+
+def test_graph_execute_cpu_matches_oracle(cpu_ops):
+    """tests/test_bert_mha.c:167-306: one MHA_Fused node, INPUT/OUTPUT wrappers, CPU run."""
+    lib = cpu_ops
+    c = FusedCase(1, 4, 2, 2, 8, fill="lcg", residual=True)
+    g, nid, tX, tY = build_fused_graph(lib, c)
+    ins = (c_void_p * 1)(tX)
+    outs = (c_void_p * 1)(tY)
+    assert lib.graph_execute(g.g, ins, outs, False) == 0
+    got = g.read(tY, c.X.shape)
+    assert np.array_equal(got, c.oracle())
+    # session wrapper (inference_engine.c:31-37)
+    s = lib.inference_session_from_graph(g.g, 1, 1)
+    assert s and lib.inference_session_num_inputs(s) == 1
+    assert lib.inference_session_run(s, ins, outs, 0) == 0
+    assert np.array_equal(g.read(tY, c.X.shape), c.oracle())
+    lib.inference_session_destroy(s)       # owns and destroys the graph
+
+
+def test_graph_decode_kv_cache_steps_cpu(cpu_ops):
+    """OP_MHA_DECODE with in-place caches and graph_update_cache_len over two steps."""
+    lib = cpu_ops
+    c = DecodeCase(1, 4, 2, 8, 8, cache_len=0, seed=4, wstd=0.3)
+    g = Graph(lib)
+    tX, iX = g.tensor(c.X)
+    tK, iK = g.tensor(c.Kc)
+    tV, iV = g.tensor(c.Vc)
+    tY, iY = g.tensor(np.zeros_like(c.X))
+    ws = [g.tensor(w)[0] for w in (c.WQ, c.bQ, c.WK, c.bK, c.WV, c.bV, c.WO, c.bO)]
+    p = O.decode_params(1, c.D, c.H, c.H_kv, c.d, 0, c.max_seq)
+    g.node(OP_MHA_DECODE, [iX, iK, iV], [iY, iK, iV], ws, p)
+    lib.graph_set_input(g.g, g.node(OP_INPUT, [], [iX]))
+    lib.graph_set_output(g.g, g.node(OP_OUTPUT, [iY], []))
+    lib.graph_set_kv_cache(g.g, iK, iV)
+    assert lib.graph_build(g.g) == 0
+    want = c.oracle()
+    ins, outs = (c_void_p * 1)(tX), (c_void_p * 1)(tY)
+    assert lib.graph_execute(g.g, ins, outs, False) == 0
+    assert np.array_equal(g.read(tY, c.X.shape), want[0])
+    assert np.array_equal(g.read(tK, c.Kc.shape), want[1])
+    # step 2
+    c2 = DecodeCase(1, 4, 2, 8, 8, cache_len=1, seed=4, wstd=0.3)
+    c2.Kc, c2.Vc = want[1], want[2]
+    c2.X = O.normal(c.X.shape, 77)
+    ctypes.memmove(ctypes.cast(tX, POINTER(__import__("cudaforge_amd").TensorT)).contents.data,
+                   c2.X.ctypes.data, c2.X.nbytes)
+    lib.graph_update_cache_len(g.g, 1)
+    assert lib.graph_execute(g.g, ins, outs, False) == 0
+    want2 = c2.oracle()
+    assert np.array_equal(g.read(tY, c.X.shape), want2[0])
+    assert np.array_equal(g.read(tV, c.Vc.shape), want2[2])
+    g.destroy()
+
+
+def test_graph_unresolved_op_returns_minus_two(native):
+    g = Graph(native)
+    _, a = g.tensor(np.zeros(4, np.float32))
+    _, b = g.tensor(np.zeros(4, np.float32))
+    g.node(OP_RELU, [a], [b])
+    assert native.graph_build(g.g) == 0
+    assert native.graph_execute(g.g, None, None, False) == -2
+    g.destroy()
+
+
+def test_session_load_reports_missing_onnx(native):
+    assert not native.inference_session_load(b"model.onnx")
+
+
+def test_tensor_api(native):
+    import cudaforge_amd as cf
+    shape = (c_int64 * 3)(2, 3, 4)
+    t = native.tensor_create(DT_F16, 3, shape)
+    tt = ctypes.cast(t, POINTER(cf.TensorT)).contents
+    assert tt.numel == 24 and list(tt.strides[:3]) == [12, 4, 1] and tt.data and not tt.data_device
+    u = native.tensor_create(DT_F16, 3, shape)
+    assert native.tensor_allclose(t, u, 0.0, 0.0)
+    ctypes.cast(ctypes.cast(tt.data, c_void_p), POINTER(ctypes.c_uint16))[5] = 0x3C00   # 1.0
+    assert not native.tensor_allclose(t, u, 1e-3, 1e-3)
+    assert native.tensor_copy_to_host(t) == 0            # no device mirror: no-op
+    native.tensor_destroy(t)
+    native.tensor_destroy(u)
+    assert not native.tensor_create(DT_F32, 9, shape)
