@@ -17,7 +17,7 @@
 //    fp32 (d = 64/128): four waves, lanes own 4 dims of a row, dot products reduced
 //      across the row's lanes.
 //    Other head or group sizes: a generic kernel, one query head per workgroup.
-// 2. merge kernel, one workgroup per (b, kv head): the log-sum-exp combine
+// 2. merge kernel, one thread per output element: the log-sum-exp combine
 //      O = Σ_s 2^(m_s - M)·acc_s / Σ_s 2^(m_s - M)·l_s
 //    (the reference's split/merge formula, mha_fused_cuda.cu:847-863 and :895-931,
 //    restated per (b, head) with the head index it lacked).  A sequence that fits in
@@ -471,60 +471,55 @@ void split_generic(cf_decode_attn_args_t a) {
 }
 
 // ------------------------------------------------------------------------ merge ---
-// One workgroup per (unit, head g): unit = (b, kv head) holding Gx heads, or (b, q head)
-// with Gx = 1.  blockIdx.x = unit * Gx + g.
+// One thread per output element (unit, head g, dim i); unit = (b, kv head) holding Gx
+// heads, or (b, q head) with Gx = 1.  Each thread streams its splits 16 at a time with
+// all loads of a group in flight together and folds them into a running
+// (M, num, den) with the log-sum-exp rescale, so there is no LDS and no barrier.
 template <typename T>
 __global__ __launch_bounds__(kMergeThreads)
 void merge_kernel(cf_decode_attn_args_t a, int Gx, int units_per_b) {
-    extern __shared__ float w[];                   // [n_split] weights 2^(m_s - M)
-    __shared__ float s_red[kMergeThreads / 64][2];
-    const int unit = blockIdx.x / Gx, g = blockIdx.x - unit * Gx;
-    const int b = unit / units_per_b;
     const int D = a.d;
+    const size_t idx = (size_t)blockIdx.x * kMergeThreads + threadIdx.x;
+    const size_t total = (size_t)a.B * units_per_b * Gx * D;
+    if (idx >= total) return;
+    const int i = (int)(idx % D);
+    const size_t ug = idx / D;
+    const int g = (int)(ug % Gx);
+    const int unit = (int)(ug / Gx);
+    const int b = unit / units_per_b;
     const int T_b = attended(a, b);
     const int nsplit = (T_b + a.chunk - 1) / a.chunk;
     if (nsplit <= 1) return;                       // finished by the split kernel
     const int stride = Gx * (D + 2);
     const float* part = a.partials + (size_t)unit * a.n_split * stride;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
-    // M = max_s m_s and den = Σ_s 2^(m_s - M) l_s, all splits read in parallel.
-    float m = -INFINITY;
-    for (int s = tid; s < nsplit; s += blockDim.x) m = fmaxf(m, part[(size_t)s * stride + g]);
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    if (lane == 0) s_red[wave][0] = m;
-    __syncthreads();
-    m = s_red[0][0];
-    for (int i = 1; i < nw; i++) m = fmaxf(m, s_red[i][0]);
-    float den = 0.0f;
-    for (int s = tid; s < nsplit; s += blockDim.x) {
-        const float ws = exp2f(part[(size_t)s * stride + g] - m);
-        w[s] = ws;
-        den = __builtin_fmaf(ws, part[(size_t)s * stride + Gx + g], den);
-    }
-    for (int off = 32; off > 0; off >>= 1) den += __shfl_xor(den, off);
-    if (lane == 0) s_red[wave][1] = den;
-    __syncthreads();
-    den = 0.0f;
-    for (int i = 0; i < nw; i++) den += s_red[i][1];
-    const float inv = 1.0f / den;
-    T* out = (T*)a.o + ((size_t)unit * Gx + g) * D;
-    for (int i = tid; i < D; i += blockDim.x) {
-        const float* pa = part + 2 * Gx + g * D + i;
-        float n0 = 0.0f, n1 = 0.0f;
-        int s = 0;
-        for (; s + 8 <= nsplit; s += 8) {
-            float v[8];
+    constexpr int NB = 16;
+    float M = -INFINITY, num = 0.0f, den = 0.0f;
+    for (int s0 = 0; s0 < nsplit; s0 += NB) {
+        float mv[NB], lv[NB], av[NB];
 #pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = pa[(size_t)(s + j) * stride];
-#pragma unroll
-            for (int j = 0; j < 8; j += 2) {
-                n0 = __builtin_fmaf(w[s + j], v[j], n0);
-                n1 = __builtin_fmaf(w[s + j + 1], v[j + 1], n1);
-            }
+        for (int j = 0; j < NB; j++) {
+            const float* ps = part + (size_t)(s0 + j) * stride;
+            const bool ok = s0 + j < nsplit;
+            mv[j] = ok ? ps[g] : -INFINITY;
+            lv[j] = ok ? ps[Gx + g] : 0.0f;
+            av[j] = ok ? ps[2 * Gx + g * D + i] : 0.0f;
         }
-        for (; s < nsplit; s++) n0 = __builtin_fmaf(w[s], pa[(size_t)s * stride], n0);
-        out[i] = from_f<T>((n0 + n1) * inv);
+        float mc = mv[0];
+#pragma unroll
+        for (int j = 1; j < NB; j++) mc = fmaxf(mc, mv[j]);
+        const float m_new = fmaxf(M, mc);
+        const float rescale = exp2f(M - m_new);    // 0 on the first group (M = -inf)
+        num *= rescale;
+        den *= rescale;
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            const float w = exp2f(mv[j] - m_new);  // 0 for padding entries
+            num = __builtin_fmaf(w, av[j], num);
+            den = __builtin_fmaf(w, lv[j], den);
+        }
+        M = m_new;
     }
+    ((T*)a.o)[idx] = from_f<T>(num / den);
 }
 
 bool fast_supported(int elem, int d, int G) {
@@ -611,15 +606,12 @@ extern "C" int cf_launch_decode_attn_merge(const cf_decode_attn_args_t* a, void*
     const bool fast = use_fast(a);
     const int Gx = fast ? a->H_q / a->H_kv : 1;
     const int units_per_b = fast ? a->H_kv : a->H_q;
-    const size_t lds = (size_t)a->n_split * sizeof(float);
-    // One thread per output element of a head (rounded up to whole waves, at most 256).
-    int threads = (a->d + 63) / 64 * 64;
-    if (threads > kMergeThreads) threads = kMergeThreads;
-    dim3 grid((unsigned)(a->B * units_per_b * Gx));
+    const size_t total = (size_t)a->B * units_per_b * Gx * a->d;
+    dim3 grid((unsigned)((total + kMergeThreads - 1) / kMergeThreads));
     if (a->elem == CF_ELEM_F16)
-        hipLaunchKernelGGL(merge_kernel<_Float16>, grid, dim3(threads), lds, s, *a, Gx, units_per_b);
+        hipLaunchKernelGGL(merge_kernel<_Float16>, grid, dim3(kMergeThreads), 0, s, *a, Gx, units_per_b);
     else
-        hipLaunchKernelGGL(merge_kernel<float>, grid, dim3(threads), lds, s, *a, Gx, units_per_b);
+        hipLaunchKernelGGL(merge_kernel<float>, grid, dim3(kMergeThreads), 0, s, *a, Gx, units_per_b);
     return (int)hipGetLastError();
 }
 

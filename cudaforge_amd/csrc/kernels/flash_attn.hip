@@ -7,15 +7,18 @@
 // kv head = h / (H_q/H_kv) (mha_decode.c:77).  The reference CPU semantics it must match
 // are mha_fused.c:98-131 (two-pass softmax); the online form changes only rounding.
 //
-// fp16 path (d = 64 or 128): a workgroup owns 64 queries (4 waves x 16).  Key blocks of
-// 64 are staged in LDS (K as [key][dim], V^T as [dim][key]).  Each wave computes
-// S^T = K·Q^T with v_mfma_f32_16x16x32_f16, so a lane holds 16 scores of ONE query and
-// the row max / row sum are lane-local plus a 4-lane exchange.  The probabilities are
-// converted to fp16 in registers and fed straight back as the B operand of
+// fp16 path (d = 64 or 128): a workgroup owns 128 queries, 32 per wave (two 16-query
+// column blocks, so every K and V^T fragment read from LDS feeds two MFMAs).  Key blocks
+// of 64 are staged in LDS (K as [key][dim], V^T as [dim][key]) through a two-stage ring
+// whose next block is loaded into registers while the current one is used.  Each wave
+// computes S^T = K·Q^T with v_mfma_f32_16x16x32_f16, so a lane holds 16 scores of ONE
+// query per column block: the row max and row sum are lane-local plus a 4-lane exchange.
+// The probabilities are converted to fp16 in registers and fed back as the B operand of
 // O^T += V^T·P^T; the key order inside each 32-key MFMA step is permuted so that the
-// registers a lane already holds are exactly its B operand (V^T reads follow the same
-// permutation).  No score or probability ever goes through LDS.
-// Causal workgroups are issued heaviest-first.
+// registers a lane already holds are exactly its B operand (the V^T reads follow the
+// same permutation).  No score or probability goes through LDS.  Masks are evaluated
+// only on blocks that cross the sequence end or the causal diagonal; causal workgroups
+// are issued heaviest-first.
 //
 // Generic path (fp32, or other head sizes): one thread per query, online softmax in
 // fp32 with Q and the accumulator in LDS.
@@ -32,19 +35,21 @@ typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kQB = 64;      // queries per workgroup
+constexpr int kQB = 128;     // queries per workgroup (32 per wave)
 constexpr int kKB = 64;      // keys per block
 constexpr int kThreads = 256;
 
 template <int D>
-__global__ __launch_bounds__(kThreads)
+__global__ __launch_bounds__(kThreads, 2)
 void flash_f16(cf_flash_args_t a) {
     constexpr int LDK = D + 8;        // halves per K row in LDS
     constexpr int LDV = kKB + 8;      // halves per V^T row in LDS
     constexpr int KT = D / 32;        // 32-dim steps of S^T
     constexpr int UT = D / 16;        // 16-dim tiles of O^T
-    __shared__ __attribute__((aligned(16))) _Float16 Ks[kKB * LDK];
-    __shared__ __attribute__((aligned(16))) _Float16 Vs[D * LDV];
+    constexpr int K_ST = kKB * LDK, V_ST = D * LDV;
+    constexpr int KCH = kKB * D / 8 / kThreads;   // 16-byte K chunks per thread per block
+    constexpr int VCH = D * kKB / 8 / kThreads;   // 16-byte V^T chunks per thread per block
+    __shared__ __attribute__((aligned(16))) _Float16 smem[2 * (K_ST + V_ST)];
 
     const int nqb = gridDim.x;
     const int qb = a.causal ? (nqb - 1 - (int)blockIdx.x) : (int)blockIdx.x;
@@ -54,34 +59,43 @@ void flash_f16(cf_flash_args_t a) {
     const int q0 = qb * kQB;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 15, lq = lane >> 4;
-    const int query = q0 + wave * 16 + lr;
+    const int qw = q0 + 32 * wave;                 // first query of this wave
 
     const _Float16* __restrict__ qp = (const _Float16*)a.q + (((size_t)b * a.H_q + h) * S) * D;
     const _Float16* __restrict__ kp = (const _Float16*)a.k + (((size_t)b * a.H_kv + kvh) * S) * D;
     const _Float16* __restrict__ vp = (const _Float16*)a.vt + (((size_t)b * a.H_kv + kvh) * D) * (size_t)S;
 
-    h8_t qf[KT];
+    int query[2];
+    h8_t qf[2][KT];
 #pragma unroll
-    for (int kt = 0; kt < KT; kt++)
-        qf[kt] = query < S ? *(const h8_t*)(qp + (size_t)query * D + 32 * kt + 8 * lq) : h8_t{};
+    for (int j = 0; j < 2; j++) {
+        query[j] = qw + 16 * j + lr;
+#pragma unroll
+        for (int kt = 0; kt < KT; kt++)
+            qf[j][kt] = query[j] < S ? *(const h8_t*)(qp + (size_t)query[j] * D + 32 * kt + 8 * lq) : h8_t{};
+    }
 
     const float c = a.scale * kLog2e;
-    float m_run = -INFINITY, l_run = 0.0f;
-    f4_t acc[UT];
+    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.0f, 0.0f};
+    f4_t acc[2][UT];
 #pragma unroll
-    for (int u = 0; u < UT; u++) acc[u] = f4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int u = 0; u < UT; u++) acc[j][u] = f4_t{0.f, 0.f, 0.f, 0.f};
 
     const int k_end = a.causal ? min(S, q0 + kQB) : S;
     const bool v_vec = (S % 8) == 0;
-    for (int k0 = 0; k0 < k_end; k0 += kKB) {
-        // Stage K [key][dim] and V^T [dim][key].
-        for (int ch = tid; ch < kKB * D / 8; ch += kThreads) {
+    h8_t rk[KCH], rv[VCH];
+    auto load_block = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < KCH; i++) {
+            const int ch = tid + i * kThreads;
             const int r = ch / (D / 8), cc = (ch % (D / 8)) * 8;
-            h8_t v{};
-            if (k0 + r < S) v = *(const h8_t*)(kp + (size_t)(k0 + r) * D + cc);
-            *(h8_t*)&Ks[r * LDK + cc] = v;
+            rk[i] = k0 + r < S ? *(const h8_t*)(kp + (size_t)(k0 + r) * D + cc) : h8_t{};
         }
-        for (int ch = tid; ch < D * (kKB / 8); ch += kThreads) {
+#pragma unroll
+        for (int i = 0; i < VCH; i++) {
+            const int ch = tid + i * kThreads;
             const int dm = ch / (kKB / 8), kc = (ch % (kKB / 8)) * 8;
             const _Float16* src = vp + (size_t)dm * S + k0 + kc;
             h8_t v{};
@@ -90,75 +104,113 @@ void flash_f16(cf_flash_args_t a) {
 #pragma unroll
                 for (int e = 0; e < 8; e++) if (k0 + kc + e < S) v[e] = src[e];
             }
-            *(h8_t*)&Vs[dm * LDV + kc] = v;
+            rv[i] = v;
         }
-        __syncthreads();
+    };
+    auto store_block = [&](int stage) {
+        _Float16* Ks = smem + stage * (K_ST + V_ST);
+        _Float16* Vs = Ks + K_ST;
+#pragma unroll
+        for (int i = 0; i < KCH; i++) {
+            const int ch = tid + i * kThreads;
+            *(h8_t*)&Ks[(ch / (D / 8)) * LDK + (ch % (D / 8)) * 8] = rk[i];
+        }
+#pragma unroll
+        for (int i = 0; i < VCH; i++) {
+            const int ch = tid + i * kThreads;
+            *(h8_t*)&Vs[(ch / (kKB / 8)) * LDV + (ch % (kKB / 8)) * 8] = rv[i];
+        }
+    };
 
-        // S^T tiles: st[t][i] = score(key k0 + 16t + 4*lq + i, query).
-        f4_t st[4];
+    const int nblk = (k_end + kKB - 1) / kKB;
+    load_block(0);
+    store_block(0);
+    __syncthreads();
+    for (int bi = 0; bi < nblk; bi++) {
+        const int k0 = bi * kKB;
+        if (bi + 1 < nblk) load_block(k0 + kKB);
+        const _Float16* Ks = smem + (bi & 1) * (K_ST + V_ST);
+        const _Float16* Vs = Ks + K_ST;
+
+        // S^T tiles: st[j][t][i] = score(key k0 + 16t + 4*lq + i, query[j]).
+        f4_t st[2][4];
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            st[t] = f4_t{0.f, 0.f, 0.f, 0.f};
+            st[0][t] = f4_t{0.f, 0.f, 0.f, 0.f};
+            st[1][t] = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kt = 0; kt < KT; kt++) {
                 const h8_t kf = *(const h8_t*)&Ks[(16 * t + lr) * LDK + 32 * kt + 8 * lq];
-                st[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[kt], st[t], 0, 0, 0);
+                st[0][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[0][kt], st[0][t], 0, 0, 0);
+                st[1][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[1][kt], st[1][t], 0, 0, 0);
             }
         }
-        float mloc = -INFINITY;
+        const bool edge = (k0 + kKB > S) || (a.causal && k0 + kKB - 1 > qw);
+        h8_t pf[2][2];
 #pragma unroll
-        for (int t = 0; t < 4; t++)
+        for (int j = 0; j < 2; j++) {
+            if (edge) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int key = k0 + 16 * t + 4 * lq + i;
-                float x = st[t][i] * c;
-                if (key >= S || (a.causal && key > query)) x = -INFINITY;
-                st[t][i] = x;
-                mloc = fmaxf(mloc, x);
+                for (int t = 0; t < 4; t++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int key = k0 + 16 * t + 4 * lq + i;
+                        if (key >= S || (a.causal && key > query[j])) st[j][t][i] = -INFINITY;
+                    }
             }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-        const float m_new = fmaxf(m_run, mloc);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = exp2f(m_run - m_use);
-        m_run = m_new;
-        float psum = 0.0f;
-        h8_t pf[2];
+            float mloc = fmaxf(fmaxf(st[j][0][0], st[j][0][1]), fmaxf(st[j][0][2], st[j][0][3]));
 #pragma unroll
-        for (int t = 0; t < 4; t++)
+            for (int t = 1; t < 4; t++)
+                mloc = fmaxf(mloc, fmaxf(fmaxf(st[j][t][0], st[j][t][1]), fmaxf(st[j][t][2], st[j][t][3])));
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+            // Scores are raw dot products; the scale folds into the exponent: p = 2^(s*c - m*c).
+            const float m_new = fmaxf(m_run[j], mloc * c);
+            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+            const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_use);
+            m_run[j] = m_new;
+            float psum = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float p = exp2f(st[t][i] - m_use);
-                psum += p;
-                pf[t >> 1][(t & 1) * 4 + i] = (_Float16)p;
-            }
-        l_run = l_run * alpha + psum;
+            for (int t = 0; t < 4; t++)
 #pragma unroll
-        for (int u = 0; u < UT; u++) acc[u] *= alpha;
-        // O^T[16u + 4*lq + i][query] += Σ_keys V^T · P^T, key k-slot e of lane group lq
-        // in step j is key 32j + 16*(e/4) + 4*lq + (e%4).
+                for (int i = 0; i < 4; i++) {
+                    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(st[j][t][i], c, -m_use));
+                    psum += p;
+                    pf[j][t >> 1][(t & 1) * 4 + i] = (_Float16)p;
+                }
+            l_run[j] = l_run[j] * alpha + psum;
+#pragma unroll
+            for (int u = 0; u < UT; u++) acc[j][u] *= alpha;
+        }
+        // O^T[16u + 4*lq + i][query] += V^T · P^T; in 32-key step s, k-slot e of lane group
+        // lq is key 32s + 16*(e/4) + 4*lq + (e%4).
 #pragma unroll
         for (int u = 0; u < UT; u++)
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const _Float16* vr = &Vs[(16 * u + lr) * LDV + 32 * j + 4 * lq];
+            for (int s = 0; s < 2; s++) {
+                const _Float16* vr = &Vs[(16 * u + lr) * LDV + 32 * s + 4 * lq];
                 const h4_t lo = *(const h4_t*)vr;
                 const h4_t hi = *(const h4_t*)(vr + 16);
                 const h8_t vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[j], acc[u], 0, 0, 0);
+                acc[0][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[0][s], acc[0][u], 0, 0, 0);
+                acc[1][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[1][s], acc[1][u], 0, 0, 0);
             }
+        if (bi + 1 < nblk) store_block((bi + 1) & 1);
         __syncthreads();
     }
-    float l_tot = l_run + __shfl_xor(l_run, 16);
-    l_tot += __shfl_xor(l_tot, 32);
-    if (query < S) {
-        const float inv = 1.0f / l_tot;
-        _Float16* op = (_Float16*)a.o + (((size_t)b * S + query) * a.H_q + h) * D;
 #pragma unroll
-        for (int u = 0; u < UT; u++) {
-            const h4_t ov = {(_Float16)(acc[u][0] * inv), (_Float16)(acc[u][1] * inv),
-                             (_Float16)(acc[u][2] * inv), (_Float16)(acc[u][3] * inv)};
-            *(h4_t*)(op + 16 * u + 4 * lq) = ov;
+    for (int j = 0; j < 2; j++) {
+        float l_tot = l_run[j] + __shfl_xor(l_run[j], 16);
+        l_tot += __shfl_xor(l_tot, 32);
+        if (query[j] < S) {
+            const float inv = 1.0f / l_tot;
+            _Float16* op = (_Float16*)a.o + (((size_t)b * S + query[j]) * a.H_q + h) * D;
+#pragma unroll
+            for (int u = 0; u < UT; u++) {
+                const h4_t ov = {(_Float16)(acc[j][u][0] * inv), (_Float16)(acc[j][u][1] * inv),
+                                 (_Float16)(acc[j][u][2] * inv), (_Float16)(acc[j][u][3] * inv)};
+                *(h4_t*)(op + 16 * u + 4 * lq) = ov;
+            }
         }
     }
 }
@@ -222,7 +274,8 @@ extern "C" int cf_launch_flash_attn(const cf_flash_args_t* a, void* stream) {
     hipStream_t s = (hipStream_t)stream;
     if (a->S <= 0 || a->d <= 0 || a->H_kv <= 0 || a->H_q % a->H_kv != 0) return (int)hipErrorInvalidValue;
     const bool aligned = ((uintptr_t)a->q | (uintptr_t)a->k | (uintptr_t)a->vt | (uintptr_t)a->o) % 16 == 0;
-    if (a->elem == CF_ELEM_F16 && aligned && (a->d == 64 || a->d == 128)) {
+    // The fast kernel takes the row max of raw scores and scales it, valid for scale > 0.
+    if (a->elem == CF_ELEM_F16 && aligned && (a->d == 64 || a->d == 128) && a->scale > 0.0f) {
         dim3 grid((unsigned)((a->S + kQB - 1) / kQB), (unsigned)a->H_q, (unsigned)a->B);
         if (a->d == 64) hipLaunchKernelGGL(flash_f16<64>, grid, dim3(kThreads), 0, s, *a);
         else hipLaunchKernelGGL(flash_f16<128>, grid, dim3(kThreads), 0, s, *a);
@@ -236,4 +289,3 @@ extern "C" int cf_launch_flash_attn(const cf_flash_args_t* a, void* stream) {
     else hipLaunchKernelGGL(flash_generic<float>, grid, dim3(nt), lds, s, *a);
     return (int)hipGetLastError();
 }
-

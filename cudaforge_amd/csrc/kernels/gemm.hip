@@ -7,11 +7,15 @@
 // transposed, vt (B,H_kv,d,S), so attention reads keys contiguously for P·V.
 //
 // fp16: 128x128x64 workgroup tile, 4 waves as 2x2, each wave 64x64 = 4x4 tiles of
-//       v_mfma_f32_16x16x32_f16.  The W tile is transposed to [n][k] while it is
-//       staged in LDS (8x4 register blocks -> 16-byte LDS rows), so every MFMA operand
-//       is one ds_read_b128.
-// fp32: same tiling with v_mfma_f32_16x16x4_f32, both tiles staged k-major so each
-//       operand is one conflict-free ds_read_b32.
+//       v_mfma_f32_16x16x32_f16.  Both tiles are staged in LDS in their natural global
+//       layout (A as [m][k], W as [k][n]) through a two-stage ring: the next k-tile's
+//       16-byte global loads are in flight while the current one is multiplied, and
+//       there is one barrier per k-tile.  The MFMA B operand needs 8 consecutive k of
+//       one column per lane; it comes from W[k][n] with two ds_read_b64_tr_b16
+//       (gfx950 LDS transpose reads): in each 16-lane group, lane j addresses
+//       W[kb + j/4][nb + 4(j%4)] and lane i receives W[kb..kb+3][nb + i].
+// fp32: 128x128x16 tile with v_mfma_f32_16x16x4_f32, both tiles staged k-major so each
+//       operand is one conflict-free ds_read_b32 (the FP32 operator's parity path).
 // Tile edges are zero-filled on load and masked on store.
 
 #include <hip/hip_runtime.h>
@@ -24,6 +28,8 @@ namespace {
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 lds_h4_t;
+#define CF_LDS __attribute__((address_space(3)))
 
 constexpr int kThreads = 256;
 constexpr int BM = 128, BN = 128;
@@ -39,26 +45,6 @@ __device__ __forceinline__ float to_f(float x) { return x; }
 __device__ __forceinline__ float to_f(_Float16 x) { return (float)x; }
 template <typename T> __device__ __forceinline__ T from_f(float x) { return (T)x; }
 
-// Store one accumulator element of output column n (segment-local), row m.
-template <typename T>
-__device__ __forceinline__ void store_out(const cf_gemm_args_t& a, int seg, int m, int n, float v) {
-    const T* bias = (const T*)a.bias[seg];
-    if (bias) v += to_f(bias[n]);
-    if (a.out_kind == CF_GEMM_OUT_ROWMAJOR) {
-        const size_t idx = (size_t)m * a.n[0] + n;
-        if (a.residual) v += to_f(((const T*)a.residual)[idx]);
-        ((T*)a.out[0])[idx] = from_f<T>(v);
-        return;
-    }
-    const int b = m / a.S, s = m - b * a.S;
-    const int h = n / a.d, i = n - h * a.d;
-    const int H = seg == 0 ? a.H_q : a.H_kv;
-    size_t idx;
-    if (seg < 2) idx = (((size_t)b * H + h) * a.S + s) * a.d + i;
-    else idx = (((size_t)b * H + h) * a.d + i) * a.S + s;
-    ((T*)a.out[seg])[idx] = from_f<T>(v);
-}
-
 __device__ __forceinline__ int find_seg(const cf_gemm_args_t& a, const Tiling& t, int tile_n) {
     int seg = 0;
     if (a.nseg > 1 && tile_n >= t.seg_start[1]) seg = 1;
@@ -66,14 +52,71 @@ __device__ __forceinline__ int find_seg(const cf_gemm_args_t& a, const Tiling& t
     return seg;
 }
 
+// Destination offsets split as row part + column part:
+//   row-major:          m*N + n
+//   q, k (B,H,S,d):     (b*H*S + s)*d      + (n/d)*S*d + n%d
+//   vt   (B,H,d,S):     b*H*d*S + s        + n*S
+__device__ __forceinline__ size_t row_part(const cf_gemm_args_t& a, int seg, int m) {
+    if (a.out_kind == CF_GEMM_OUT_ROWMAJOR) return (size_t)m * a.n[0];
+    const int b = m / a.S, s = m - b * a.S;
+    const int H = seg == 0 ? a.H_q : a.H_kv;
+    if (seg < 2) return ((size_t)b * H * a.S + s) * a.d;
+    return (size_t)b * H * a.d * a.S + s;
+}
+
+__device__ __forceinline__ size_t col_part(const cf_gemm_args_t& a, int seg, int n) {
+    if (a.out_kind == CF_GEMM_OUT_ROWMAJOR) return (size_t)n;
+    if (seg < 2) {
+        const int h = n / a.d;
+        return (size_t)h * a.S * a.d + (n - h * a.d);
+    }
+    return (size_t)n * a.S;
+}
+
+// Store the accumulators of a wave tile: acc[i][j][e] is C[m0 + 16i + 4*lq + e][n0 + 16j + lr].
+template <typename T>
+__device__ __forceinline__ void store_tile(const cf_gemm_args_t& a, int seg, int N, int m0, int n0,
+                                           int lr, int lq, const f4_t (&acc)[4][4]) {
+    const T* __restrict__ bias = (const T*)a.bias[seg];
+    const T* __restrict__ res = a.out_kind == CF_GEMM_OUT_ROWMAJOR ? (const T*)a.residual : nullptr;
+    T* __restrict__ out = (T*)a.out[seg];
+    size_t cp[4];
+    float bv[4];
+    bool nok[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int n = n0 + 16 * j + lr;
+        nok[j] = n < N;
+        cp[j] = nok[j] ? col_part(a, seg, n) : 0;
+        bv[j] = (bias && nok[j]) ? to_f(bias[n]) : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int m = m0 + 16 * i + 4 * lq + e;
+            if (m >= a.M) continue;
+            const size_t rp = row_part(a, seg, m);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (!nok[j]) continue;
+                float v = acc[i][j][e] + bv[j];
+                if (res) v += to_f(res[rp + cp[j]]);
+                out[rp + cp[j]] = from_f<T>(v);
+            }
+        }
+}
+
 // ------------------------------------------------------------------------- fp16 ---
 constexpr int BK16 = 64;
-constexpr int LDA16 = BK16 + 8;   // halves per LDS row (pad keeps 16-byte rows off one bank set)
+constexpr int LDA16 = BK16 + 8;   // halves per A row in LDS
+constexpr int LDW16 = BN + 8;     // halves per W row in LDS
+constexpr int A_STAGE = BM * LDA16;
+constexpr int W_STAGE = BK16 * LDW16;
 
-__global__ __launch_bounds__(kThreads)
+__global__ __launch_bounds__(kThreads, 2)
 void gemm_f16(cf_gemm_args_t a, Tiling t) {
-    __shared__ __attribute__((aligned(16))) _Float16 As[BM * LDA16];
-    __shared__ __attribute__((aligned(16))) _Float16 Bs[BN * LDA16];
+    __shared__ __attribute__((aligned(16))) _Float16 smem[2 * (A_STAGE + W_STAGE)];
 
     const int tile_m = blockIdx.x % t.n_tiles_m;
     const int tile_n = blockIdx.x / t.n_tiles_m;
@@ -90,19 +133,14 @@ void gemm_f16(cf_gemm_args_t a, Tiling t) {
     const bool a_vec = t.a_vec != 0;
     const bool w_vec = t.w_vec[seg] != 0;
 
-    f4_t acc[4][4];
+    // Global -> register staging: A chunk c = tid + 256*i is row c>>3, k (c&7)*8;
+    // W chunk c is row (k) c>>4, column (c&15)*8.
+    h8_t ra[4], rw[4];
+    auto load_tiles = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
-
-    for (int k0 = 0; k0 < a.K; k0 += BK16) {
-        // A tile: 128 rows x 64 halves = 1024 chunks of 8; 4 per thread.
-#pragma unroll
-        for (int it = 0; it < 4; it++) {
-            const int ch = tid + it * kThreads;
-            const int r = ch >> 3, kc = (ch & 7) * 8;
-            const int gm = m0 + r, gk = k0 + kc;
+        for (int i = 0; i < 4; i++) {
+            const int ch = tid + i * kThreads;
+            const int gm = m0 + (ch >> 3), gk = k0 + (ch & 7) * 8;
             h8_t v{};
             if (gm < a.M) {
                 const _Float16* src = A + (size_t)gm * a.K + gk;
@@ -112,62 +150,73 @@ void gemm_f16(cf_gemm_args_t a, Tiling t) {
                     for (int e = 0; e < 8; e++) if (gk + e < a.K) v[e] = src[e];
                 }
             }
-            *(h8_t*)&As[r * LDA16 + kc] = v;
+            ra[i] = v;
         }
-        // W tile: 64 k x 128 n.  Thread owns an 8(k) x 4(n) block, 256 blocks.
-        {
-            const int kb = (tid & 7) * 8;       // k offset of the block
-            const int nb = (tid >> 3) * 4;      // n offset of the block
-            h4_t rows[8];
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int gk = k0 + kb + j, gn = n0 + nb;
-                h4_t v{};
-                if (gk < a.K) {
-                    const _Float16* src = W + (size_t)gk * N + gn;
-                    if (w_vec && gn + 4 <= N) v = *(const h4_t*)src;
-                    else {
+        for (int i = 0; i < 4; i++) {
+            const int ch = tid + i * kThreads;
+            const int gk = k0 + (ch >> 4), gn = n0 + (ch & 15) * 8;
+            h8_t v{};
+            if (gk < a.K) {
+                const _Float16* src = W + (size_t)gk * N + gn;
+                if (w_vec && gn + 8 <= N) v = *(const h8_t*)src;
+                else {
 #pragma unroll
-                        for (int e = 0; e < 4; e++) if (gn + e < N) v[e] = src[e];
-                    }
+                    for (int e = 0; e < 8; e++) if (gn + e < N) v[e] = src[e];
                 }
-                rows[j] = v;
             }
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                h8_t col;
-#pragma unroll
-                for (int j = 0; j < 8; j++) col[j] = rows[j][c];
-                *(h8_t*)&Bs[(nb + c) * LDA16 + kb] = col;
-            }
+            rw[i] = v;
         }
-        __syncthreads();
+    };
+    auto store_tiles = [&](int stage) {
+        _Float16* As = smem + stage * (A_STAGE + W_STAGE);
+        _Float16* Ws = As + A_STAGE;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int ch = tid + i * kThreads;
+            *(h8_t*)&As[(ch >> 3) * LDA16 + (ch & 7) * 8] = ra[i];
+            *(h8_t*)&Ws[(ch >> 4) * LDW16 + (ch & 15) * 8] = rw[i];
+        }
+    };
+
+    f4_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+    const int nk = (a.K + BK16 - 1) / BK16;
+    load_tiles(0);
+    store_tiles(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+        const int stage = kt & 1;
+        if (kt + 1 < nk) load_tiles((kt + 1) * BK16);
+        const _Float16* As = smem + stage * (A_STAGE + W_STAGE);
+        const _Float16* Ws = As + A_STAGE;
 #pragma unroll
         for (int kk = 0; kk < BK16; kk += 32) {
             h8_t af[4], bf[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) af[i] = *(const h8_t*)&As[(wm + 16 * i + lr) * LDA16 + kk + 8 * lq];
 #pragma unroll
-            for (int j = 0; j < 4; j++) bf[j] = *(const h8_t*)&Bs[(wn + 16 * j + lr) * LDA16 + kk + 8 * lq];
+            for (int j = 0; j < 4; j++) {
+                const _Float16* p = &Ws[(kk + 8 * lq + (lr >> 2)) * LDW16 + wn + 16 * j + 4 * (lr & 3)];
+                const lds_h4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((CF_LDS lds_h4_t*)p);
+                const lds_h4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((CF_LDS lds_h4_t*)(p + 4 * LDW16));
+                const h4_t l4 = __builtin_bit_cast(h4_t, lo), h4 = __builtin_bit_cast(h4_t, hi);
+                bf[j] = h8_t{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+            }
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
                 for (int j = 0; j < 4; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
+        if (kt + 1 < nk) store_tiles(stage ^ 1);
         __syncthreads();
     }
-    // acc[i][j][e]: row = wm + 16i + 4*lq + e, col = wn + 16j + lr  (A rows = m, B rows = n)
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int m = m0 + wm + 16 * i + 4 * lq + e;
-                const int n = n0 + wn + 16 * j + lr;
-                if (m < a.M && n < N) store_out<_Float16>(a, seg, m, n, acc[i][j][e]);
-            }
+    store_tile<_Float16>(a, seg, N, m0 + wm, n0 + wn, lr, lq, acc);
 }
 
 // ------------------------------------------------------------------------- fp32 ---
@@ -252,16 +301,7 @@ void gemm_f32(cf_gemm_args_t a, Tiling t) {
         }
         __syncthreads();
     }
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int m = m0 + wm + 16 * i + 4 * lq + e;
-                const int n = n0 + wn + 16 * j + lr;
-                if (m < a.M && n < N) store_out<float>(a, seg, m, n, acc[i][j][e]);
-            }
+    store_tile<float>(a, seg, N, m0 + wm, n0 + wn, lr, lq, acc);
 }
 
 }  // namespace
@@ -276,11 +316,11 @@ extern "C" int cf_launch_gemm(const cf_gemm_args_t* a, void* stream) {
         acc += (a->n[s] + BN - 1) / BN;
     }
     for (int s = a->nseg; s < 4; s++) t.seg_start[s] = acc;
-    // fp16 A is read 8 halves at a time and W 4 at a time; fp32 reads 4 floats.
-    const int avec = a->elem == CF_ELEM_F16 ? 8 : 4;
-    t.a_vec = (a->K % avec == 0) && ((uintptr_t)a->a % 16 == 0);
+    // fp16 reads 8 halves at a time from A and W; fp32 reads 4 floats.
+    const int vec = a->elem == CF_ELEM_F16 ? 8 : 4;
+    t.a_vec = (a->K % vec == 0) && ((uintptr_t)a->a % 16 == 0);
     for (int s = 0; s < a->nseg; s++)
-        t.w_vec[s] = (a->n[s] % 4 == 0) && ((uintptr_t)a->w[s] % 16 == 0);
+        t.w_vec[s] = (a->n[s] % vec == 0) && ((uintptr_t)a->w[s] % 16 == 0);
     const long long blocks = (long long)acc * t.n_tiles_m;
     if (blocks <= 0 || blocks > 0x7fffffffLL) return (int)hipErrorInvalidValue;
     dim3 grid((unsigned)blocks);

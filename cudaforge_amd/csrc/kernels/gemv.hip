@@ -210,9 +210,18 @@ void gemv_reduce(cf_gemv_args_t a, Tiles t) {
         const int n = (tile - t.start[seg]) * kColTile + (col - tile * kColTile);
         if (n >= a.seg[seg].n) continue;
         const float* p = a.partials + (size_t)m * ncols + col;
-        float s = 0.0f;
-        for (int kk = 0; kk < a.k_split; kk++) s += p[kk * plane];
-        store_out<T>(a, a.seg[seg], m, n, s);
+        // Eight independent loads in flight per round trip.
+        float s0 = 0.0f, s1 = 0.0f;
+        int kk = 0;
+        for (; kk + 8 <= a.k_split; kk += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = p[(size_t)(kk + j) * plane];
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) { s0 += v[j]; s1 += v[j + 1]; }
+        }
+        for (; kk < a.k_split; kk++) s0 += p[(size_t)kk * plane];
+        store_out<T>(a, a.seg[seg], m, n, s0 + s1);
     }
 }
 
