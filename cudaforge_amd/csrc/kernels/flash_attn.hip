@@ -51,9 +51,17 @@ void flash_f16(cf_flash_args_t a) {
     constexpr int VCH = D * kKB / 8 / kThreads;   // 16-byte V^T chunks per thread per block
     __shared__ __attribute__((aligned(16))) _Float16 smem[2 * (K_ST + V_ST)];
 
-    const int nqb = gridDim.x;
-    const int qb = a.causal ? (nqb - 1 - (int)blockIdx.x) : (int)blockIdx.x;
-    const int h = blockIdx.y, b = blockIdx.z;
+    // XCD-aware order: workgroup id w runs on XCD w % 8.  Ids are laid out as
+    // ((group * nqb + qb) * 8 + r) with head-batch index hb = group * 8 + r, so every
+    // query block of one (b, h) lands on the same XCD and shares its K/V in that L2.
+    const int nqb = (a.S + kQB - 1) / kQB;
+    const int HB = a.B * a.H_q;
+    const int w = blockIdx.x, r8 = w & 7, rest = w >> 3;
+    const int qi = rest % nqb, grp = rest / nqb;
+    const int hb = grp * 8 + r8;
+    if (hb >= HB) return;                          // padding of the last group of 8
+    const int qb = a.causal ? (nqb - 1 - qi) : qi;
+    const int h = hb % a.H_q, b = hb / a.H_q;
     const int S = a.S;
     const int kvh = h / (a.H_q / a.H_kv);
     const int q0 = qb * kQB;
@@ -276,7 +284,10 @@ extern "C" int cf_launch_flash_attn(const cf_flash_args_t* a, void* stream) {
     const bool aligned = ((uintptr_t)a->q | (uintptr_t)a->k | (uintptr_t)a->vt | (uintptr_t)a->o) % 16 == 0;
     // The fast kernel takes the row max of raw scores and scales it, valid for scale > 0.
     if (a->elem == CF_ELEM_F16 && aligned && (a->d == 64 || a->d == 128) && a->scale > 0.0f) {
-        dim3 grid((unsigned)((a->S + kQB - 1) / kQB), (unsigned)a->H_q, (unsigned)a->B);
+        const long long nqb = (a->S + kQB - 1) / kQB;
+        const long long groups = ((long long)a->B * a->H_q + 7) / 8;
+        if (groups * nqb * 8 > 0x7fffffffLL) return (int)hipErrorInvalidValue;
+        dim3 grid((unsigned)(groups * nqb * 8));
         if (a->d == 64) hipLaunchKernelGGL(flash_f16<64>, grid, dim3(kThreads), 0, s, *a);
         else hipLaunchKernelGGL(flash_f16<128>, grid, dim3(kThreads), 0, s, *a);
         return (int)hipGetLastError();

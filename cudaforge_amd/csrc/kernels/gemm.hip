@@ -6,14 +6,16 @@
 // head-major buffers for the attention kernel: q (B,H_q,S,d), k (B,H_kv,S,d) and V
 // transposed, vt (B,H_kv,d,S), so attention reads keys contiguously for P·V.
 //
-// fp16: 128x128x64 workgroup tile, 4 waves as 2x2, each wave 64x64 = 4x4 tiles of
-//       v_mfma_f32_16x16x32_f16.  Both tiles are staged in LDS in their natural global
-//       layout (A as [m][k], W as [k][n]) through a two-stage ring: the next k-tile's
-//       16-byte global loads are in flight while the current one is multiplied, and
-//       there is one barrier per k-tile.  The MFMA B operand needs 8 consecutive k of
-//       one column per lane; it comes from W[k][n] with two ds_read_b64_tr_b16
+// fp16: 128x128 workgroup tile, 4 waves as 2x2, each wave 64x64 = 4x4 tiles of
+//       v_mfma_f32_16x16x32_f16.  Both operands are staged in LDS in their natural
+//       global layout (A as [m][k], W as [k][n]).  The MFMA B operand needs 8 consecutive
+//       k of one column per lane; it comes from W[k][n] with two ds_read_b64_tr_b16
 //       (gfx950 LDS transpose reads): in each 16-lane group, lane j addresses
 //       W[kb + j/4][nb + 4(j%4)] and lane i receives W[kb..kb+3][nb + i].
+//       Full tiles use a 4-stage ring filled by global_load_lds_dwordx4 (three k-tiles in
+//       flight, no VGPR staging); edge shapes use a 2-stage register-staged kernel.
+//       The output tile goes through LDS so stores are 16 bytes along the destination's
+//       contiguous direction.
 // fp32: 128x128x16 tile with v_mfma_f32_16x16x4_f32, both tiles staged k-major so each
 //       operand is one conflict-free ds_read_b32 (the FP32 operator's parity path).
 // Tile edges are zero-filled on load and masked on store.
@@ -39,11 +41,34 @@ struct Tiling {
     int seg_start[4];   // first column tile of each segment
     int a_vec;          // A rows may be read with vector loads (alignment and K)
     int w_vec[3];       // W rows of segment s may be read with vector loads
+    int epi_vec;        // fp16 epilogue may use 8-element stores (alignment and shape)
 };
 
 __device__ __forceinline__ float to_f(float x) { return x; }
 __device__ __forceinline__ float to_f(_Float16 x) { return (float)x; }
 template <typename T> __device__ __forceinline__ T from_f(float x) { return (T)x; }
+
+// XCD-aware tile order.  Workgroup ids are dealt round-robin to MI355X's 8 XCDs, each
+// with its own L2, so workgroup b runs on XCD b % 8.  XCD x receives a contiguous range
+// of the tile order, and inside it tiles go column-major over groups of kGroupM tile
+// rows: the workgroups an XCD runs together share A row tiles and W column tiles in
+// that XCD's L2 instead of fetching them from MALL/HBM once per workgroup.
+constexpr int kXcds = 8;
+constexpr int kGroupM = 4;
+
+__device__ __forceinline__ void tile_of_block(int blk, int tiles_m, int tiles_n, int& tm, int& tn) {
+    const int T = tiles_m * tiles_n;
+    const int x = blk % kXcds, j = blk / kXcds;
+    const int base = T / kXcds, rem = T % kXcds;
+    const int t = x * base + min(x, rem) + j;      // position in the tile order
+    const int per_group = kGroupM * tiles_n;
+    const int g = t / per_group;
+    const int first_m = g * kGroupM;
+    const int gm = min(tiles_m - first_m, kGroupM);
+    const int r = t - g * per_group;
+    tm = first_m + r % gm;
+    tn = r / gm;
+}
 
 __device__ __forceinline__ int find_seg(const cf_gemm_args_t& a, const Tiling& t, int tile_n) {
     int seg = 0;
@@ -108,6 +133,75 @@ __device__ __forceinline__ void store_tile(const cf_gemm_args_t& a, int seg, int
 }
 
 // ------------------------------------------------------------------------- fp16 ---
+// Epilogue shared by both fp16 kernels: the C tile goes through LDS in fp32, 64 rows at a
+// time, so bias and residual are added before the single rounding to fp16, and stores
+// are 16 bytes along the destination's contiguous direction (n for row-major / q / k,
+// s for v^T).  `Cs` must hold 64 x (BN + 4) floats and be free (after a barrier).
+constexpr int LDCF = BN + 4;
+__device__ __forceinline__ void epilogue_f16(const cf_gemm_args_t& a, int seg, int N, int m0, int n0, int wm,
+                                             int wn, int lr, int lq, int tid, const f4_t (&acc)[4][4],
+                                             float* Cs) {
+    const _Float16* __restrict__ bias = (const _Float16*)a.bias[seg];
+    _Float16* __restrict__ out = (_Float16*)a.out[seg];
+    const _Float16* __restrict__ res = a.out_kind == CF_GEMM_OUT_ROWMAJOR ? (const _Float16*)a.residual : nullptr;
+    const bool along_n = a.out_kind == CF_GEMM_OUT_ROWMAJOR || seg < 2;
+    for (int half = 0; half < 2; half++) {
+        if (wm == 64 * half) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int nl = wn + 16 * j + lr;
+                const float bv = (bias && n0 + nl < N) ? (float)bias[n0 + nl] : 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) Cs[(16 * i + 4 * lq + e) * LDCF + nl] = acc[i][j][e] + bv;
+            }
+        }
+        __syncthreads();
+        const int mh = m0 + 64 * half;
+#pragma unroll
+        for (int it = 0; it < (64 * BN / 8) / kThreads; it++) {
+            const int ch = tid + it * kThreads;
+            h8_t v;
+            if (along_n) {
+                const int r = ch >> 4, c8 = (ch & 15) * 8;
+                const int m = mh + r, n = n0 + c8;
+                if (m >= a.M || n >= N) continue;
+                const size_t off = row_part(a, seg, m) + col_part(a, seg, n);
+                const f4_t lo = *(const f4_t*)&Cs[r * LDCF + c8], hi = *(const f4_t*)&Cs[r * LDCF + c8 + 4];
+                float f[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                if (res) {
+                    const h8_t rv = *(const h8_t*)(res + off);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) f[e] += (float)rv[e];
+                }
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] = (_Float16)f[e];
+                *(h8_t*)(out + off) = v;
+            } else {
+                const int col = ch & (BN - 1), r8 = (ch / BN) * 8;
+                const int m = mh + r8, n = n0 + col;
+                if (m >= a.M || n >= N) continue;
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] = (_Float16)Cs[(r8 + e) * LDCF + col];
+                *(h8_t*)(out + row_part(a, seg, m) + col_part(a, seg, n)) = v;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// MFMA B operand (8 consecutive k of one column) from a W tile stored [k][n] in LDS:
+// two ds_read_b64_tr_b16.  p points at W[kb + lr/4][nb + 4*(lr%4)] of the caller's
+// lane; the second read is 4 rows further.
+__device__ __forceinline__ h8_t b_frag_tr(const _Float16* p, const _Float16* p4) {
+    const lds_h4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((CF_LDS lds_h4_t*)p);
+    const lds_h4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((CF_LDS lds_h4_t*)p4);
+    const h4_t l4 = __builtin_bit_cast(h4_t, lo), h4 = __builtin_bit_cast(h4_t, hi);
+    return h8_t{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+}
+
+// ---- general kernel: any shape; registers stage the next k-tile (zero-filled edges).
 constexpr int BK16 = 64;
 constexpr int LDA16 = BK16 + 8;   // halves per A row in LDS
 constexpr int LDW16 = BN + 8;     // halves per W row in LDS
@@ -118,8 +212,8 @@ __global__ __launch_bounds__(kThreads, 2)
 void gemm_f16(cf_gemm_args_t a, Tiling t) {
     __shared__ __attribute__((aligned(16))) _Float16 smem[2 * (A_STAGE + W_STAGE)];
 
-    const int tile_m = blockIdx.x % t.n_tiles_m;
-    const int tile_n = blockIdx.x / t.n_tiles_m;
+    int tile_m, tile_n;
+    tile_of_block(blockIdx.x, t.n_tiles_m, t.seg_start[3], tile_m, tile_n);
     const int seg = find_seg(a, t, tile_n);
     const int N = a.n[seg];
     const int m0 = tile_m * BM;
@@ -133,8 +227,7 @@ void gemm_f16(cf_gemm_args_t a, Tiling t) {
     const bool a_vec = t.a_vec != 0;
     const bool w_vec = t.w_vec[seg] != 0;
 
-    // Global -> register staging: A chunk c = tid + 256*i is row c>>3, k (c&7)*8;
-    // W chunk c is row (k) c>>4, column (c&15)*8.
+    // A chunk c = tid + 256*i is row c>>3, k (c&7)*8; W chunk c is row (k) c>>4, column (c&15)*8.
     h8_t ra[4], rw[4];
     auto load_tiles = [&](int k0) {
 #pragma unroll
@@ -202,10 +295,7 @@ void gemm_f16(cf_gemm_args_t a, Tiling t) {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const _Float16* p = &Ws[(kk + 8 * lq + (lr >> 2)) * LDW16 + wn + 16 * j + 4 * (lr & 3)];
-                const lds_h4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((CF_LDS lds_h4_t*)p);
-                const lds_h4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((CF_LDS lds_h4_t*)(p + 4 * LDW16));
-                const h4_t l4 = __builtin_bit_cast(h4_t, lo), h4 = __builtin_bit_cast(h4_t, hi);
-                bf[j] = h8_t{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+                bf[j] = b_frag_tr(p, p + 4 * LDW16);
             }
 #pragma unroll
             for (int i = 0; i < 4; i++)
@@ -216,7 +306,148 @@ void gemm_f16(cf_gemm_args_t a, Tiling t) {
         if (kt + 1 < nk) store_tiles(stage ^ 1);
         __syncthreads();
     }
-    store_tile<_Float16>(a, seg, N, m0 + wm, n0 + wn, lr, lq, acc);
+    if (t.epi_vec) epilogue_f16(a, seg, N, m0, n0, wm, wn, lr, lq, tid, acc, (float*)smem);
+    else store_tile<_Float16>(a, seg, N, m0 + wm, n0 + wn, lr, lq, acc);
+}
+
+// ---- pipelined kernel: full tiles only (M % 128, N % 128, K % 32 == 0, aligned).
+// Four LDS stages of 32 k, filled by global_load_lds_dwordx4 (global -> LDS without
+// VGPRs): three k-tiles are in flight while one is multiplied.  A lane-contiguous
+// 1 KB of LDS per load instruction fixes the LDS layout, so the global side is
+// permuted instead: the 16-byte chunk c of row r is stored at chunk c ^ swz(r), which
+// makes the MFMA A reads (16 rows x one chunk) and the W transpose reads (4 rows x 32 B
+// per 16-lane group) hit distinct banks.
+constexpr int BKA = 32;
+constexpr int STAGES = 4;
+constexpr int A_ST = BM * BKA;          // halves per stage: A [128][32]
+constexpr int W_ST = BKA * BN;          //                   W [32][128]
+constexpr int ST = A_ST + W_ST;         // 16 KB per stage
+
+__device__ __forceinline__ int swz_a(int row) { return (row >> 2) & 3; }
+__device__ __forceinline__ int swz_w(int row) { return ((row & 3) << 1) ^ (((row >> 3) & 1) << 3); }
+
+template <int N_OUT>
+__device__ __forceinline__ void wait_vm() {
+    // s_waitcnt vmcnt(N_OUT), expcnt/lgkmcnt left at their maxima (gfx9 encoding).
+    __builtin_amdgcn_s_waitcnt((N_OUT & 0xF) | ((N_OUT >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// 16 bytes per lane from global memory into LDS at lds_base + 16*lane (M0 = lds_base).
+// Issued as inline asm so the compiler does not treat the LDS ring as pending DMA
+// writes (it would then wait for every load before each LDS read); completion is
+// tracked with explicit vmcnt waits instead.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(g), "s"(lds_base) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+    return (uint32_t)(uintptr_t)(const CF_LDS void*)p;
+}
+
+// Workgroup barrier without the vmcnt(0) wait __syncthreads implies (the ring keeps
+// DMA loads in flight across it); the empty asm statements stop the compiler from
+// moving LDS accesses across the barrier.
+__device__ __forceinline__ void ring_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__global__ __launch_bounds__(kThreads, 2)
+void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
+    __shared__ __attribute__((aligned(16))) _Float16 smem[STAGES * ST];
+
+    int tile_m, tile_n;
+    tile_of_block(blockIdx.x, t.n_tiles_m, t.seg_start[3], tile_m, tile_n);
+    const int seg = find_seg(a, t, tile_n);
+    const int N = a.n[seg];
+    const int K = a.K;
+    const int m0 = tile_m * BM;
+    const int n0 = (tile_n - t.seg_start[seg]) * BN;
+    const _Float16* __restrict__ A = (const _Float16*)a.a;
+    const _Float16* __restrict__ W = (const _Float16*)a.w[seg];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = (wave & 1) * 64, wn = (wave >> 1) * 64;
+    const int lr = lane & 15, lq = lane >> 4;
+
+    // Wave w fills A slices u = 2w, 2w+1 (rows 16u .. 16u+15) and W slices u = 2w, 2w+1
+    // (k rows 4u .. 4u+3) of every stage; lane L owns physical chunk L%4 (A) / L%16 (W).
+    size_t a_off[2], w_off[2];
+#pragma unroll
+    for (int v = 0; v < 2; v++) {
+        const int u = 2 * wave + v;
+        const int ra = 16 * u + (lane >> 2), ca = (lane & 3) ^ swz_a(ra);
+        a_off[v] = (size_t)(m0 + ra) * K + 8 * ca;
+        const int rw = 4 * u + (lane >> 4), cw = (lane & 15) ^ swz_w(rw);
+        w_off[v] = (size_t)rw * N + n0 + 8 * cw;
+    }
+    const uint32_t smem_base = lds_offset(smem);
+    auto issue = [&](int stage, int k0) {
+        const uint32_t base = smem_base + (uint32_t)(stage * ST) * 2u;
+#pragma unroll
+        for (int v = 0; v < 2; v++) {
+            const int u = 2 * wave + v;
+            lds_dma16(A + a_off[v] + k0, __builtin_amdgcn_readfirstlane(base + (uint32_t)u * 1024u));
+            lds_dma16(W + w_off[v] + (size_t)k0 * N,
+                      __builtin_amdgcn_readfirstlane(base + (uint32_t)(A_ST * 2 + u * 1024)));
+        }
+    };
+
+    f4_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+    // Per-lane LDS read offsets inside a stage.
+    int a_rd[4], w_rd[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int row = wm + 16 * i + lr;
+        a_rd[i] = row * BKA + 8 * (lq ^ swz_a(row));
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int row = 8 * lq + 4 * h + (lr >> 2);
+            const int col = wn + 16 * j + 4 * (lr & 3);
+            w_rd[j][h] = row * BN + 8 * ((col >> 3) ^ swz_w(row)) + (col & 7);
+        }
+
+    const int nk = K / BKA;
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; s++)
+        if (s < nk) issue(s, s * BKA);
+    for (int kt = 0; kt < nk; kt++) {
+        // Tiles issued after kt that may still be in flight: min(STAGES-2, nk-1-kt), 4
+        // load instructions each.
+        const int ahead = min(STAGES - 2, nk - 1 - kt);
+        if (ahead >= 2) wait_vm<8>();
+        else if (ahead == 1) wait_vm<4>();
+        else wait_vm<0>();
+        ring_barrier();
+        if (kt + STAGES - 1 < nk) issue((kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BKA);
+        const _Float16* As = smem + (kt % STAGES) * ST;
+        const _Float16* Ws = As + A_ST;
+        h8_t af[4], bf[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) af[i] = *(const h8_t*)&As[a_rd[i]];
+#pragma unroll
+        for (int j = 0; j < 4; j++) bf[j] = b_frag_tr(Ws + w_rd[j][0], Ws + w_rd[j][1]);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    wait_vm<0>();
+    __syncthreads();
+    epilogue_f16(a, seg, N, m0, n0, wm, wn, lr, lq, tid, acc, (float*)smem);
 }
 
 // ------------------------------------------------------------------------- fp32 ---
@@ -228,8 +459,8 @@ void gemm_f32(cf_gemm_args_t a, Tiling t) {
     __shared__ float As[BK32 * LDM32];   // [k][m]
     __shared__ float Bs[BK32 * LDM32];   // [k][n]
 
-    const int tile_m = blockIdx.x % t.n_tiles_m;
-    const int tile_n = blockIdx.x / t.n_tiles_m;
+    int tile_m, tile_n;
+    tile_of_block(blockIdx.x, t.n_tiles_m, t.seg_start[3], tile_m, tile_n);
     const int seg = find_seg(a, t, tile_n);
     const int N = a.n[seg];
     const int m0 = tile_m * BM;
@@ -321,10 +552,23 @@ extern "C" int cf_launch_gemm(const cf_gemm_args_t* a, void* stream) {
     t.a_vec = (a->K % vec == 0) && ((uintptr_t)a->a % 16 == 0);
     for (int s = 0; s < a->nseg; s++)
         t.w_vec[s] = (a->n[s] % vec == 0) && ((uintptr_t)a->w[s] % 16 == 0);
+    // 8-element stores stay inside one destination row: N % 8 (row-major), d % 8 and
+    // S % 8 (head-major q/k and transposed v), with 16-byte aligned buffers.
+    uintptr_t ptrs = (uintptr_t)a->out[0] | (uintptr_t)a->residual;
+    for (int s = 1; s < a->nseg; s++) ptrs |= (uintptr_t)a->out[s];
+    int ev = (ptrs % 16 == 0);
+    if (a->out_kind == CF_GEMM_OUT_ROWMAJOR) ev = ev && a->n[0] % 8 == 0;
+    else ev = ev && a->d % 8 == 0 && a->S % 8 == 0;
+    t.epi_vec = ev;
     const long long blocks = (long long)acc * t.n_tiles_m;
     if (blocks <= 0 || blocks > 0x7fffffffLL) return (int)hipErrorInvalidValue;
     dim3 grid((unsigned)blocks);
-    if (a->elem == CF_ELEM_F16)
+    // Full tiles with aligned rows take the pipelined direct-to-LDS kernel.
+    bool full = a->elem == CF_ELEM_F16 && t.epi_vec && a->M % BM == 0 && a->K % BKA == 0 && t.a_vec;
+    for (int s = 0; s < a->nseg; s++) full = full && a->n[s] % BN == 0 && t.w_vec[s];
+    if (full)
+        hipLaunchKernelGGL(gemm_f16_async, grid, dim3(kThreads), 0, (hipStream_t)stream, *a, t);
+    else if (a->elem == CF_ELEM_F16)
         hipLaunchKernelGGL(gemm_f16, grid, dim3(kThreads), 0, (hipStream_t)stream, *a, t);
     else
         hipLaunchKernelGGL(gemm_f32, grid, dim3(kThreads), 0, (hipStream_t)stream, *a, t);
