@@ -180,7 +180,7 @@ def cpu_baseline_decode(budget_s: float):
 
 def read_traffic(kernel_prefix: str):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary, if present."""
-    path = os.path.join(ROOT, "profiles", "decode_attn_fast_config2_traffic.json")
+    path = os.path.join(ROOT, "profiles", f"{kernel_prefix}_decode_config2_traffic.json")
     if not os.path.exists(path):
         return None
     try:
@@ -199,6 +199,9 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU oracle timing")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-core", action="store_true", help="time only the headline kernel (for profiling)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run 5 device-to-device copies of 256 MiB: the known-size reference that "
+                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one MI355X only; multi-GPU runs are out of scope "
@@ -211,6 +214,16 @@ def main() -> int:
     log(f"device {caps.name.decode()} {caps.arch.decode()} CUs={caps.cu_count}")
     stream = cf.Stream()
     steps, warmup = args.steps, args.warmup
+    if args.copy_calibration:
+        lib = cf.load_library()
+        n = 256 << 20
+        src, dst = cf.DeviceBuffer(n), cf.DeviceBuffer(n)
+        src.fill_zero(stream)
+        for _ in range(5):
+            if lib.gpu_memcpy_d2d(dst.ptr, src.ptr, n, stream.handle) != 0:
+                raise RuntimeError("calibration copy failed")
+        stream.synchronize()
+        log(f"calibration: 5 copies of {n} bytes")
 
     log("decode core, config 2")
     ms, ms_split, ms_merge, alg_bytes, cfg = bench_decode_core(cf, stream, steps, warmup)
@@ -266,8 +279,8 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic (seeded N(0,1) fp16 Q/K/V; resident in HBM)",
-        "config": {"workload": "MHA_Decode GQA Llama-3-8B attention core (config 2): split-KV + LSE merge, "
-                               "one kernel per step", **cfg},
+        "config": {"workload": "MHA_Decode GQA Llama-3-8B attention core (config 2): split-KV + LSE merge "
+                               "(split kernel + merge kernel per step)", **cfg},
         "roofline": {"bound": "hbm", "achieved": round(gbs_split, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs_split / HBM_PEAK_GBS, 4), "traffic": read_traffic("split_f16"),
                      "kernel": "split_f16<128,4> (decode_attn.hip)", "alg_bytes_per_launch": alg_bytes,

@@ -78,7 +78,7 @@ def test_struct_layouts(native):
     assert ctypes.sizeof(cf.MhaDecodeParams) == 64       # mha_decode_int.h:6-15
     assert ctypes.sizeof(cf.MhaFusedParams) == 56        # mha_fused_int.h:7-17
     assert ctypes.sizeof(cf.TensorT) == 160              # platform.h:36-44
-    assert ctypes.sizeof(cf.OperatorRegistry) == 40      # operator.h:34-40
+    assert ctypes.sizeof(cf.OperatorRegistry) == 32      # src/operator/include/operator.h:34-40
 
 
 def test_registry_names(native):
@@ -168,6 +168,7 @@ class Graph:
 
     def tensor(self, arr, dtype=DT_F32):
         arr = np.ascontiguousarray(arr)
+        assert arr.itemsize == (2 if dtype == DT_F16 else 4), "host array must match the tensor's element size"
         shape = (c_int64 * max(arr.ndim, 1))(*arr.shape)
         t = self.lib.tensor_create(dtype, arr.ndim, shape)
         assert t
@@ -223,7 +224,7 @@ def test_graph_topological_order_and_cycle(native):
     assert native.graph_build(g.g) == 0
     gs = ctypes.cast(g.g, POINTER(c_int * 8)).contents   # first field num_nodes
     assert gs[0] == 2
-    order_ptr = ctypes.cast(g.g + 24, POINTER(POINTER(c_int))).contents   # topo_order
+    order_ptr = ctypes.cast(g.g + 32, POINTER(POINTER(c_int))).contents   # topo_order (after tensors)
     assert [order_ptr[0], order_ptr[1]] == [n1, n2]
     g.destroy()
     g = Graph(native)
@@ -239,7 +240,8 @@ def build_fused_graph(lib, c: FusedCase, f16_out=False):
     g = Graph(lib)
     tX, iX = g.tensor(c.X)
     tR, iR = g.tensor(c.R if c.R is not None else np.zeros_like(c.X))
-    tY, iY = g.tensor(np.zeros_like(c.X), DT_F16 if f16_out else DT_F32)
+    tY, iY = (g.tensor(np.zeros(c.X.shape, np.float16), DT_F16) if f16_out
+              else g.tensor(np.zeros_like(c.X), DT_F32))
     ws = [g.tensor(w)[0] for w in (c.WQ, c.bQ, c.WK, c.bK, c.WV, c.bV, c.WO, c.bO)]
     p = O.fused_params(c.B, c.S, c.D, c.H, c.H_kv, c.d, c.residual, c.causal)
     nid = g.node(OP_MHA_FUSED, [iX, iR], [iY], ws, p)
