@@ -277,6 +277,14 @@ static int is_kv(const inference_graph_t* g, int tid) {
     return tid >= 0 && (tid == g->kv_cache_K_tid || tid == g->kv_cache_V_tid);
 }
 
+/* Written by an operator during execution (so its device copy is the current one), as
+ * opposed to a graph input (no producer, or an OP_INPUT node), whose host data the
+ * caller may change between executions. */
+static int op_produced(const inference_graph_t* g, int tid) {
+    const int prod = g->tensors[tid].producer;
+    return prod >= 0 && g->nodes[prod].type != OP_INPUT;
+}
+
 int graph_execute(inference_graph_t* g, tensor_t* inputs[], tensor_t* outputs[], bool use_cuda) {
     if (!g || !g->topo_order) return -1;
     if (g->num_inputs > 0 && !inputs) return -1;
@@ -321,7 +329,7 @@ int graph_execute(inference_graph_t* g, tensor_t* inputs[], tensor_t* outputs[],
             if (tid < 0 || tid >= g->num_tensors) continue;
             tensor_t* t = g->tensors[tid].tensor;
             if (on_gpu) {
-                if (is_kv(g, tid) || g->tensors[tid].producer >= 0) {
+                if (is_kv(g, tid) || op_produced(g, tid)) {
                     if (tensor_copy_to_device(t) != 0) ret = -1;
                 } else if (!fresh[tid]) {
                     if (tensor_upload(t) != 0) ret = -1;
@@ -329,7 +337,7 @@ int graph_execute(inference_graph_t* g, tensor_t* inputs[], tensor_t* outputs[],
                 }
                 slots[i] = t->data_device;
             } else {
-                if (t->data_device && g->tensors[tid].producer >= 0 && tensor_copy_to_host(t) != 0) ret = -1;
+                if (t->data_device && op_produced(g, tid) && tensor_copy_to_host(t) != 0) ret = -1;
                 if (is_kv(g, tid) && t->data_device && tensor_copy_to_host(t) != 0) ret = -1;
                 slots[i] = t->data;
             }

@@ -1,0 +1,91 @@
+// cdna4.h — small device helpers shared by the gfx950 kernels: vector types, direct
+// global->LDS loads with explicit completion waits, and the LDS transposing read.
+#ifndef CF_CDNA4_H_
+#define CF_CDNA4_H_
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cdna4 {
+
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 lds_h4_t;
+#define CF_LDS __attribute__((address_space(3)))
+
+// s_waitcnt vmcnt(N), expcnt/lgkmcnt left at their maxima (gfx9 encoding).  The empty
+// asm after it keeps the compiler from hoisting LDS reads above the wait.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+    asm volatile("" ::: "memory");
+}
+
+// 16 bytes per lane from global memory into LDS at lds_base + 16*lane (M0 = lds_base).
+// Issued as inline asm so the compiler does not treat the LDS ring as pending DMA
+// writes (it would then wait for every load before each LDS read); completion is
+// tracked with explicit vmcnt waits instead.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(g), "s"(lds_base) : "memory", "m0");
+}
+// Same, addressing global memory as a uniform 64-bit base (SGPR pair) plus a per-lane
+// 32-bit byte offset: no per-lane 64-bit address arithmetic.
+__device__ __forceinline__ void lds_dma16_s(uint32_t voff, const void* sbase, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" :: "v"(voff), "s"(sbase), "s"(lds_base)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Reductions across lane i and lane i^16 / i^32 with the gfx950 row-swap permutes (VALU,
+// no LDS round trip).  v_permlane16_swap a, b swaps the odd 16-lane rows of a with the
+// even rows of b (v_permlane32_swap: the upper half of a with the lower half of b), so
+// with a = b = x every lane ends with {own value, partner value} in a and b; max and +
+// are commutative, so both partners get the same bits.  Issued as inline asm (with the
+// two wait states a VALU write needs before the permute reads it): the compiler's own
+// folding of these builtins treats the two results of swap(x, x) as equal, which they
+// are not across lanes.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void swap_xor16(float& a, float& b) {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap_xor32(float& a, float& b) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+#pragma clang diagnostic pop
+__device__ __forceinline__ float max_xor16(float x) { float a = x, b = x; swap_xor16(a, b); return fmaxf(a, b); }
+__device__ __forceinline__ float max_xor32(float x) { float a = x, b = x; swap_xor32(a, b); return fmaxf(a, b); }
+__device__ __forceinline__ float add_xor16(float x) { float a = x, b = x; swap_xor16(a, b); return a + b; }
+__device__ __forceinline__ float add_xor32(float x) { float a = x, b = x; swap_xor32(a, b); return a + b; }
+
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+    return (uint32_t)(uintptr_t)(const CF_LDS void*)p;
+}
+
+// Workgroup barrier without the vmcnt(0) wait __syncthreads implies (a ring keeps DMA
+// loads in flight across it); the empty asm statements stop the compiler from moving
+// LDS accesses across the barrier.
+__device__ __forceinline__ void ring_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// ds_read_b64_tr_b16: in each 16-lane group, lane i receives element i%4 of the 4-half
+// chunks addressed by lanes i/4, 4 + i/4, 8 + i/4, 12 + i/4.  With lane j addressing
+// X[kb + j/4][nb + 4(j%4)] of a row-major fp16 tile, lane i gets X[kb..kb+3][nb + i].
+__device__ __forceinline__ h4_t ds_read_tr4(const _Float16* p) {
+    return __builtin_bit_cast(h4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((CF_LDS lds_h4_t*)p));
+}
+
+__device__ __forceinline__ h8_t cat8(h4_t lo, h4_t hi) {
+    return h8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+}  // namespace cdna4
+
+#endif  // CF_CDNA4_H_

@@ -29,15 +29,17 @@
 #include <stdint.h>
 
 #include "kernels.h"
+#include "cdna4.h"
 
 namespace {
 
-typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
-typedef float f4_t __attribute__((ext_vector_type(4)));
+using namespace cdna4;
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLazyMax = 8.0f;           // fp16 split kernel: max headroom of p (log2 units)
 constexpr int kChunkMax = 4096;            // positions per split (LDS: chunk * G floats)
-constexpr int kF16Quantum = 32;            // fp16 split kernel: positions per double-block
+constexpr int kF16Quantum = 32;            // fp16 split kernel: positions per block
+constexpr int kDecodeStages = 4;           // fp16 split kernel: LDS ring depth (16 KB per stage at d = 128)
 constexpr int kF32Threads = 256;
 constexpr int kF32Unroll = 4;
 constexpr int kGenericThreads = 128;
@@ -52,186 +54,244 @@ __device__ __forceinline__ int attended(const cf_decode_attn_args_t& a, int b) {
     return min(max(cl + 1, 1), a.max_seq);
 }
 
-// Partial record of one split: [m (Gx)] [l (Gx)] [acc (Gx*D)].
+// Partial record of one split: [m (Gx)] [l (Gx)] [pad to 4 floats] [acc (Gx*D)], so
+// every record and its acc block start 16-byte aligned when D % 4 == 0.
+__host__ __device__ constexpr int part_hdr(int Gx) { return (2 * Gx + 3) & ~3; }
+__host__ __device__ constexpr int part_stride(int Gx, int D) { return part_hdr(Gx) + Gx * D; }
+
 __device__ __forceinline__ float* partial_at(const cf_decode_attn_args_t& a, int unit, int split, int Gx, int D) {
-    return a.partials + ((size_t)unit * a.n_split + split) * (size_t)(Gx * (D + 2));
+    return a.partials + ((size_t)unit * a.n_split + split) * (size_t)part_stride(Gx, D);
 }
 
 // ------------------------------------------------------------------ fp16 split ---
+// One wave streams `chunk` positions of one (b, kv head) for its whole GQA group, in
+// blocks of 32 positions.  K and V rows go straight from HBM into an NS-stage LDS ring
+// (global_load_lds_dwordx4, no VGPR staging), so NS-1 blocks (16 KB each at d = 128) are
+// in flight while one is computed.  Per block, on the matrix cores:
+//   scores  S^T (16 positions x 16 heads) = K (16 x 32 dims) . Q^T, two row blocks:
+//           lane (lr, lq) gets positions 4lq..4lq+3 and 16+4lq..16+4lq+3 of head lr;
+//   values  O^T (16 dims x 16 heads) += V^T (16 dims x 32 positions) . P^T, one MFMA per
+//           16 dims.  The k index of that MFMA runs over the block's positions in the
+//           order the score lanes already hold them, so P^T is the lane's own 8
+//           probabilities converted to fp16; V^T comes from the LDS ring with
+//           ds_read_b64_tr_b16 (4 positions of one dim per read) in the same order.
+// Online softmax per block: m <- max(m, block max), alpha = 2^(m_old - m) rescales the
+// lane's accumulator columns (each lane's column is its own head), p = 2^(s - m).
+// LDS rows are XOR-swizzled in 16-byte chunks (kswz for the K fragment reads, vswz for
+// the transposing V reads) so both read patterns are bank-conflict free.
+template <int D>
+__device__ __forceinline__ int kswz(int row) { return (row / (128 / D)) % (D / 8); }
+template <int D>
+__device__ __forceinline__ int vswz(int row) { return 2 * ((row / (128 / D)) % (D / 16)); }
+
 template <int D, int G>
 __global__ __launch_bounds__(64)
 void split_f16(cf_decode_attn_args_t a) {
-    constexpr int KT = D / 32;          // 32-dim MFMA steps
-    constexpr int LPR = D / 8;          // lanes per V row (8 halves each)
-    constexpr int RPW = 64 / LPR;       // V rows per wave load
-    constexpr int VU = 4;               // V loads in flight per lane per step
-    extern __shared__ float sc[];       // [chunk][G]
+    constexpr int KT = D / 32;          // 32-dim MFMA steps per 16 positions
+    constexpr int BP = 32;              // positions per block
+    constexpr int CPR = D / 8;          // 16-byte chunks per row
+    constexpr int RPI = 64 / CPR;       // rows per DMA instruction (1 KB)
+    constexpr int NI = BP / RPI;        // DMA instructions per block per tensor
+    constexpr int NL = 2 * NI;          // ... for K and V
+    constexpr int NS = kDecodeStages;
+    constexpr int TILE = BP * D;        // halves per block per tensor
+    constexpr int NT = D / 16;          // output tiles of 16 dims
+    constexpr int HDR = part_hdr(G);
+    static_assert((NS - 2) * NL < 64, "vmcnt range");
+    constexpr int QH = (G * D * 2 + 1023) / 1024 * 512;   // halves of the Q area (whole DMA KBs)
+    __shared__ __attribute__((aligned(16))) _Float16 ring[NS * 2 * TILE + QH];
 
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int T_b = attended(a, b);
     const int t0 = split * a.chunk;
     if (t0 >= T_b) return;
     const int t1 = min(t0 + a.chunk, T_b);
-    const int npos = t1 - t0;
+    const int nblk = (t1 - t0 + BP - 1) / BP;
     const int nsplit_b = (T_b + a.chunk - 1) / a.chunk;
     const int lane = threadIdx.x, lr = lane & 15, lq = lane >> 4;
 
     const size_t row_stride = (size_t)a.H_kv * D;
-    const _Float16* __restrict__ kb = (const _Float16*)a.k + ((size_t)b * a.max_seq * a.H_kv + kvh) * D;
-    const _Float16* __restrict__ vb = (const _Float16*)a.v + ((size_t)b * a.max_seq * a.H_kv + kvh) * D;
+    const size_t unit_off = ((size_t)b * a.max_seq * a.H_kv + kvh) * D;
+    const _Float16* __restrict__ kg = (const _Float16*)a.k + unit_off;
+    const _Float16* __restrict__ vg = (const _Float16*)a.v + unit_off;
     const int h0 = kvh * G;
 
-    // B operand Q^T: lane (lr, lq) holds Q[head lr][32kt + 8lq .. +7]; heads >= G are 0.
-    h8_t qf[KT];
-#pragma unroll
-    for (int kt = 0; kt < KT; kt++)
-        qf[kt] = lr < G ? *(const h8_t*)((const _Float16*)a.q + ((size_t)b * a.H_q + h0 + lr) * D + 32 * kt + 8 * lq)
-                        : h8_t{};
     const float qk_scale = a.scale * kLog2e;
 
-    // ---- pass 1: scores, 16 positions per MFMA block, two blocks in flight.
-    auto load_k = [&](int p0, h8_t (&kf)[KT]) {
-        const int pos = p0 + lr;
+    // DMA: instruction u of a block fills rows RPI*u .. +RPI-1; lane L writes physical
+    // chunk L % CPR of row RPI*u + L / CPR, which holds logical chunk (L % CPR) ^ swz(row).
+    // A full block is addressed as a uniform base (its first row) plus per-lane 32-bit
+    // offsets fixed for the whole loop; in the last, partial block rows past t1 are
+    // clamped to row t1 - 1 (always valid) and those positions get p = 0.
+    const uint32_t ring_base = lds_offset(ring);
+    const int drow = lane / CPR, dchunk = lane % CPR;
+    const uint32_t row_bytes = (uint32_t)row_stride * 2u;
+    uint32_t koff[NI], voff[NI];
 #pragma unroll
-        for (int kt = 0; kt < KT; kt++)
-            kf[kt] = pos < t1 ? *(const h8_t*)(kb + (size_t)pos * row_stride + 32 * kt + 8 * lq) : h8_t{};
-    };
-    float mrun = -INFINITY;
-    auto score = [&](int p0, const h8_t (&kf)[KT]) {
-        f4_t s = {0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < NI; u++) {
+        const int row = RPI * u + drow;
+        koff[u] = (uint32_t)row * row_bytes + 16u * (uint32_t)(dchunk ^ kswz<D>(row));
+        voff[u] = (uint32_t)row * row_bytes + 16u * (uint32_t)(dchunk ^ vswz<D>(row));
+    }
+    auto issue = [&](int blk) {
+        const int stage = blk % NS;
+        const int p0 = t0 + blk * BP;
+        const uint32_t kbase = ring_base + (uint32_t)(stage * 2 * TILE) * 2u;
+        const uint32_t vbase = kbase + (uint32_t)TILE * 2u;
+        if (p0 + BP <= t1) {
+            const _Float16* kblk = kg + (size_t)p0 * row_stride;
+            const _Float16* vblk = vg + (size_t)p0 * row_stride;
 #pragma unroll
-        for (int kt = 0; kt < KT; kt++) s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[kt], qf[kt], s, 0, 0, 0);
-        if (lr < G) {
+            for (int u = 0; u < NI; u++) {
+                lds_dma16_s(koff[u], kblk, kbase + u * 1024u);
+                lds_dma16_s(voff[u], vblk, vbase + u * 1024u);
+            }
+        } else {
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int pos = p0 + 4 * lq + i;
-                if (pos < t1) {
-                    const float x = s[i] * qk_scale;
-                    sc[(pos - t0) * G + lr] = x;
-                    mrun = fmaxf(mrun, x);
-                }
+            for (int u = 0; u < NI; u++) {
+                const int row = RPI * u + drow;
+                const size_t g_row = (size_t)min(p0 + row, t1 - 1) * row_stride;
+                lds_dma16(kg + g_row + 8 * (dchunk ^ kswz<D>(row)), kbase + u * 1024u);
+                lds_dma16(vg + g_row + 8 * (dchunk ^ vswz<D>(row)), vbase + u * 1024u);
             }
         }
     };
-    h8_t ka[KT], kc[KT];
-    load_k(t0, ka);
-    for (int p0 = t0; p0 < t1; p0 += 32) {
-        load_k(p0 + 16, kc);
-        score(p0, ka);
-        if (p0 + 32 < t1) load_k(p0 + 32, ka);
-        if (p0 + 16 < t1) score(p0 + 16, kc);
-    }
-    // First V rows go out now, so their latency overlaps the softmax pass below.
-    const int r = lane / LPR, c = lane - (lane / LPR) * LPR;
-    const _Float16* __restrict__ vrow = vb + 8 * c;
-    auto load_v = [&](int p0, h8_t (&vv)[VU]) {
-#pragma unroll
-        for (int u = 0; u < VU; u++) {
-            const int pos = p0 + u * RPW + r;
-            vv[u] = pos < t1 ? *(const h8_t*)(vrow + (size_t)pos * row_stride) : h8_t{};
-        }
-    };
-    h8_t va[VU], vc[VU];
-    load_v(t0, va);
-    // Max per head: lanes with equal lr hold the same head.
-    mrun = fmaxf(mrun, __shfl_xor(mrun, 16));
-    mrun = fmaxf(mrun, __shfl_xor(mrun, 32));
-    float M[G];
-#pragma unroll
-    for (int g = 0; g < G; g++) M[g] = __shfl(mrun, g);
-    __syncthreads();
 
-    // ---- probabilities and their sums (64 % G == 0, so a lane always sees one head).
-    float lsum = 0.0f;
+    // Per-lane LDS read offsets (halves) inside a stage.
+    int k_rd[2][KT];
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int kt = 0; kt < KT; kt++) {
+            const int row = 16 * h + lr;
+            k_rd[h][kt] = row * D + 8 * ((4 * kt + lq) ^ kswz<D>(row));
+        }
+    int v_rd[NT][2];
+#pragma unroll
+    for (int n = 0; n < NT; n++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const int row = 16 * hh + 4 * lq + (lr >> 2);
+            const int col = 16 * n + 4 * (lr & 3);                  // halves
+            v_rd[n][hh] = TILE + row * D + 8 * ((col >> 3) ^ vswz<D>(row)) + (col & 7);
+        }
+
+    f4_t acc[NT];
+#pragma unroll
+    for (int n = 0; n < NT; n++) acc[n] = f4_t{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.0f;      // head lr; lanes lr < G are meaningful
+
+    // Q (G rows of D halves, contiguous) also arrives by DMA, ahead of the first block,
+    // so the kernel issues no compiler-visible global loads whose waits would drain the
+    // ring; lanes past the G*D*2 bytes re-read the last 16 bytes of Q (never used).
     {
-        const int gm = lane % G;
-        float mg = M[0];
+        const _Float16* qg = (const _Float16*)a.q + ((size_t)b * a.H_q + h0) * D;
+        const uint32_t qbase = ring_base + (uint32_t)(NS * 2 * TILE) * 2u;
 #pragma unroll
-        for (int g = 1; g < G; g++) if (gm == g) mg = M[g];
-        for (int i = lane; i < npos * G; i += 64) {
-            const float p = exp2f(sc[i] - mg);
-            sc[i] = p;
-            lsum += p;
-        }
+        for (int u = 0; u < QH / 512; u++)
+            lds_dma16(qg + min(8 * (64 * u + lane), G * D - 8), __builtin_amdgcn_readfirstlane(qbase + u * 1024u));
     }
 #pragma unroll
-    for (int off = G; off < 64; off <<= 1) lsum += __shfl_xor(lsum, off);
-    float L[G];
-#pragma unroll
-    for (int g = 0; g < G; g++) L[g] = __shfl(lsum, g);
-    __syncthreads();
+    for (int s = 0; s < NS - 1; s++)
+        if (s < nblk) issue(s);
+    // B operand Q^T: lane (lr, lq) holds Q[head lr][32kt + 8lq .. +7]; heads >= G are 0.
+    h8_t qf[KT];
 
-    // ---- pass 2: acc[g][e] += p[g] * V[pos][8c + e], VU rows in flight per lane.
-    float acc[G][8];
+    for (int blk = 0; blk < nblk; blk++) {
+        // Blocks issued after this one that may still be in flight.
+        const int ahead = min(NS - 2, nblk - 1 - blk);
+        if (ahead >= 2) wait_vm<2 * NL>();
+        else if (ahead == 1) wait_vm<NL>();
+        else wait_vm<0>();
+        if (blk == 0) {                              // Q landed with block 0
+            const _Float16* qs = ring + NS * 2 * TILE + min(lr, G - 1) * D + 8 * lq;
 #pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) acc[g][e] = 0.0f;
-    auto accum = [&](int p0, const h8_t (&vv)[VU]) {
-#pragma unroll
-        for (int u = 0; u < VU; u++) {
-            const int pos = p0 + u * RPW + r;
-            if (pos < t1) {
-                float p[G];
-#pragma unroll
-                for (int g = 0; g < G; g++) p[g] = sc[(pos - t0) * G + g];
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float ve = (float)vv[u][e];
-#pragma unroll
-                    for (int g = 0; g < G; g++) acc[g][e] = __builtin_fmaf(p[g], ve, acc[g][e]);
-                }
-            }
+            for (int kt = 0; kt < KT; kt++) qf[kt] = lr < G ? *(const h8_t*)(qs + 32 * kt) : h8_t{};
         }
-    };
-    constexpr int VSTEP = VU * RPW;
-    for (int p0 = t0; p0 < t1; p0 += 2 * VSTEP) {
-        load_v(p0 + VSTEP, vc);
-        accum(p0, va);
-        if (p0 + 2 * VSTEP < t1) load_v(p0 + 2 * VSTEP, va);
-        if (p0 + VSTEP < t1) accum(p0 + VSTEP, vc);
+        // The stage refilled here was read by the previous block, whose LDS reads have
+        // all returned (their values fed its MFMAs): a single wave needs no barrier.
+        if (blk + NS - 1 < nblk) issue(blk + NS - 1);
+
+        const _Float16* st = ring + (blk % NS) * 2 * TILE;
+        f4_t s[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            s[h] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kt = 0; kt < KT; kt++)
+                s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const h8_t*)(st + k_rd[h][kt]), qf[kt], s[h], 0, 0, 0);
+        }
+        // Raw scores; positions past t1 (last block only) -> -inf.  scale > 0, so the
+        // max of the raw scores times scale*log2(e) is the max of the scaled ones.
+        const int p0 = t0 + blk * BP;
+        float x[8];
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) x[4 * h + j] = s[h][j];
+        if (p0 + BP > t1) {
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (p0 + 16 * h + 4 * lq + j >= t1) x[4 * h + j] = -INFINITY;
+        }
+        float mb = x[0];
+#pragma unroll
+        for (int i = 1; i < 8; i++) mb = fmaxf(mb, x[i]);
+        mb = max_xor32(max_xor16(mb)) * qk_scale;                   // finite: p0 < t1
+        // The running max moves only when a block exceeds it by more than kLazyMax (log2
+        // units): until then p = 2^(s - m) <= 2^kLazyMax, exact enough in fp16 and far
+        // from its range limit, and the accumulators need no rescaling.  The first block
+        // always moves it (m = -inf).  The rescale runs only if some head moved (a
+        // wave-uniform branch), so the accumulators normally stay in the matrix unit.
+        const bool grow = mb > m_run + kLazyMax;
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+            const float m_new = grow ? mb : m_run;                    // finite: p0 < t1
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);   // 0 on the first block
+            m_run = m_new;
+            l_run *= alpha;
+#pragma unroll
+            for (int n = 0; n < NT; n++) acc[n] *= alpha;
+        }
+        float ps = 0.0f;
+        h8_t pf;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(x[i], qk_scale, -m_run));
+            ps += p;
+            pf[i] = (_Float16)p;
+        }
+        l_run += ps;
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+            const h8_t vf = cat8(ds_read_tr4(st + v_rd[n][0]), ds_read_tr4(st + v_rd[n][1]));
+            acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, acc[n], 0, 0, 0);
+        }
     }
-    // Rows of the wave -> row 0.
-#pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            float v = acc[g][e];
-#pragma unroll
-            for (int off = LPR; off < 64; off <<= 1) v += __shfl_xor(v, off);
-            acc[g][e] = v;
-        }
 
+    // l: the lanes of one head hold partial sums over their positions.
+    l_run = add_xor32(add_xor16(l_run));
+    if (lr >= G) return;
+    // Lane (lr, lq) holds O^T rows d = 16n + 4lq + i of head h0 + lr.
     if (nsplit_b == 1) {
-        if (r == 0) {
-            _Float16* out = (_Float16*)a.o + ((size_t)b * a.H_q + h0) * D + 8 * c;
+        const float inv = 1.0f / l_run;
+        _Float16* out = (_Float16*)a.o + ((size_t)b * a.H_q + h0 + lr) * D + 4 * lq;
 #pragma unroll
-            for (int g = 0; g < G; g++) {
-                const float inv = 1.0f / L[g];
-                h8_t o;
+        for (int n = 0; n < NT; n++) {
+            h4_t o;
 #pragma unroll
-                for (int e = 0; e < 8; e++) o[e] = (_Float16)(acc[g][e] * inv);
-                *(h8_t*)(out + (size_t)g * D) = o;
-            }
+            for (int i = 0; i < 4; i++) o[i] = (_Float16)(acc[n][i] * inv);
+            *(h4_t*)(out + 16 * n) = o;
         }
         return;
     }
     float* part = partial_at(a, b * a.H_kv + kvh, split, G, D);
-    if (r == 0) {
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            f4_t lo = {acc[g][0], acc[g][1], acc[g][2], acc[g][3]};
-            f4_t hi = {acc[g][4], acc[g][5], acc[g][6], acc[g][7]};
-            *(f4_t*)(part + 2 * G + g * D + 8 * c) = lo;
-            *(f4_t*)(part + 2 * G + g * D + 8 * c + 4) = hi;
-        }
-    }
-    if (lane < G) {
-        float m = M[0], l = L[0];
-#pragma unroll
-        for (int g = 1; g < G; g++) if (lane == g) { m = M[g]; l = L[g]; }
-        part[lane] = m;
-        part[G + lane] = l;
+    for (int n = 0; n < NT; n++) *(f4_t*)(part + HDR + lr * D + 16 * n + 4 * lq) = acc[n];
+    if (lq == 0) {
+        part[lr] = m_run;
+        part[G + lr] = l_run;
     }
 }
 
@@ -389,7 +449,7 @@ void split_f32(cf_decode_attn_args_t a) {
         for (int w = 1; w < NW; w++) s += accbuf[w * G * D + idx];
         const int g = idx / D;
         if (part) {
-            part[2 * G + idx] = s;
+            part[part_hdr(G) + idx] = s;
         } else {
             float l = L[0];
 #pragma unroll
@@ -465,7 +525,7 @@ void split_generic(cf_decode_attn_args_t a) {
         const T* vc = vb + (size_t)t0 * row_stride + i;
         for (int j = 0; j < npos; j++) acc = __builtin_fmaf(sc[j], to_f(vc[(size_t)j * row_stride]), acc);
         if (nsplit_b == 1) out[i] = from_f<T>(acc / L);
-        else part[2 + i] = acc;
+        else part[part_hdr(1) + i] = acc;
     }
     if (nsplit_b > 1 && tid == 0) { part[0] = M; part[1] = L; }
 }
@@ -490,7 +550,7 @@ void merge_kernel(cf_decode_attn_args_t a, int Gx, int units_per_b) {
     const int T_b = attended(a, b);
     const int nsplit = (T_b + a.chunk - 1) / a.chunk;
     if (nsplit <= 1) return;                       // finished by the split kernel
-    const int stride = Gx * (D + 2);
+    const int stride = part_stride(Gx, D), hdr = part_hdr(Gx);
     const float* part = a.partials + (size_t)unit * a.n_split * stride;
     constexpr int NB = 16;
     float M = -INFINITY, num = 0.0f, den = 0.0f;
@@ -502,7 +562,7 @@ void merge_kernel(cf_decode_attn_args_t a, int Gx, int units_per_b) {
             const bool ok = s0 + j < nsplit;
             mv[j] = ok ? ps[g] : -INFINITY;
             lv[j] = ok ? ps[Gx + g] : 0.0f;
-            av[j] = ok ? ps[2 * Gx + g * D + i] : 0.0f;
+            av[j] = ok ? ps[hdr + g * D + i] : 0.0f;
         }
         float mc = mv[0];
 #pragma unroll
@@ -522,6 +582,78 @@ void merge_kernel(cf_decode_attn_args_t a, int Gx, int units_per_b) {
     ((T*)a.o)[idx] = from_f<T>(num / den);
 }
 
+// Row merge (D % 4 == 0): one workgroup per output row (unit, head g).  DV = D/4 threads
+// own 4 dims each; the SG = 256/DV thread groups take splits sg, sg+SG, ... with NB
+// records in flight per thread, so a sequence with hundreds of splits costs a few load
+// rounds instead of one per 16 splits; the SG running results are combined through LDS.
+template <typename T>
+__global__ __launch_bounds__(kMergeThreads)
+void merge_rows(cf_decode_attn_args_t a, int Gx, int units_per_b) {
+    const int D = a.d, DV = D >> 2, SG = kMergeThreads / DV;
+    const int row = blockIdx.x;
+    const int g = row % Gx, unit = row / Gx, b = unit / units_per_b;
+    const int T_b = attended(a, b);
+    const int nsplit = (T_b + a.chunk - 1) / a.chunk;
+    if (nsplit <= 1) return;                       // finished by the split kernel
+    const int tid = threadIdx.x, col = tid % DV, sg = tid / DV;
+    __shared__ float sm[kMergeThreads], sd[kMergeThreads];
+    __shared__ f4_t sn[kMergeThreads];
+    float M = -INFINITY, den = 0.0f;
+    f4_t num = {0.f, 0.f, 0.f, 0.f};
+    if (sg < SG) {
+        const int stride = part_stride(Gx, D), hdr = part_hdr(Gx);
+        const float* part = a.partials + (size_t)unit * a.n_split * stride;
+        constexpr int NB = 8;
+        for (int s0 = sg; s0 < nsplit; s0 += SG * NB) {
+            float mv[NB], lv[NB];
+            f4_t av[NB];
+#pragma unroll
+            for (int j = 0; j < NB; j++) {
+                const int sp = s0 + j * SG;
+                const bool ok = sp < nsplit;
+                const float* ps = part + (size_t)(ok ? sp : 0) * stride;
+                mv[j] = ok ? ps[g] : -INFINITY;
+                lv[j] = ok ? ps[Gx + g] : 0.0f;
+                av[j] = ok ? *(const f4_t*)(ps + hdr + g * D + 4 * col) : f4_t{0.f, 0.f, 0.f, 0.f};
+            }
+            float mc = mv[0];
+#pragma unroll
+            for (int j = 1; j < NB; j++) mc = fmaxf(mc, mv[j]);
+            const float m_new = fmaxf(M, mc);      // finite: split s0 < nsplit is valid
+            const float rescale = exp2f(M - m_new);
+            den *= rescale;
+            num *= rescale;
+#pragma unroll
+            for (int j = 0; j < NB; j++) {
+                const float w = exp2f(mv[j] - m_new);
+                den = __builtin_fmaf(w, lv[j], den);
+                num += w * av[j];
+            }
+            M = m_new;
+        }
+    }
+    sm[tid] = M;
+    sd[tid] = den;
+    sn[tid] = num;
+    __syncthreads();
+    if (sg == 0) {
+        float Mx = -INFINITY;
+        for (int k = 0; k < SG; k++) Mx = fmaxf(Mx, sm[k * DV + col]);
+        float dd = 0.0f;
+        f4_t nn = {0.f, 0.f, 0.f, 0.f};
+        for (int k = 0; k < SG; k++) {
+            const float mk = sm[k * DV + col];
+            const float w = mk == -INFINITY ? 0.0f : exp2f(mk - Mx);
+            dd = __builtin_fmaf(w, sd[k * DV + col], dd);
+            nn += w * sn[k * DV + col];
+        }
+        T* out = (T*)a.o + (size_t)row * D + 4 * col;
+        const float inv = 1.0f / dd;
+#pragma unroll
+        for (int e = 0; e < 4; e++) out[e] = from_f<T>(nn[e] * inv);
+    }
+}
+
 bool fast_supported(int elem, int d, int G) {
     (void)elem;
     return (d == 64 || d == 128) && (G == 1 || G == 2 || G == 4 || G == 8);
@@ -535,15 +667,15 @@ int quantum(int elem, int d) {
 bool use_fast(const cf_decode_attn_args_t* a) {
     const int G = a->H_q / a->H_kv;
     const bool aligned = (((uintptr_t)a->q | (uintptr_t)a->k | (uintptr_t)a->v | (uintptr_t)a->o) % 16) == 0;
-    return aligned && fast_supported(a->elem, a->d, G);
+    // The fp16 kernel scales the max of the raw scores, which needs scale > 0.
+    return aligned && fast_supported(a->elem, a->d, G) && (a->elem != CF_ELEM_F16 || a->scale > 0.0f);
 }
 
 template <int D, int G>
 hipError_t launch_split_fast(const cf_decode_attn_args_t& a, hipStream_t s) {
     dim3 grid((unsigned)a.n_split, (unsigned)a.H_kv, (unsigned)a.B);
     if (a.elem == CF_ELEM_F16) {
-        const size_t lds = (size_t)a.chunk * G * sizeof(float);
-        hipLaunchKernelGGL((split_f16<D, G>), grid, dim3(64), lds, s, a);
+        hipLaunchKernelGGL((split_f16<D, G>), grid, dim3(64), 0, s, a);
     } else {
         const int NW = kF32Threads / 64;
         const int sc_floats = a.chunk * G > NW * G * D ? a.chunk * G : NW * G * D;
@@ -578,7 +710,7 @@ extern "C" size_t cf_decode_attn_partials_floats(int32_t B, int32_t H_q, int32_t
                                                  int32_t n_split, int32_t elem) {
     // (b, kv head) units with G heads each, or (b, q head) units: the same total.
     (void)H_kv; (void)elem;
-    return (size_t)B * H_q * n_split * (d + 2);
+    return (size_t)B * H_q * n_split * (d + 4);   // >= units * n_split * part_stride(Gx, d)
 }
 
 extern "C" int cf_launch_decode_attn_split(const cf_decode_attn_args_t* a, void* stream) {
@@ -606,6 +738,14 @@ extern "C" int cf_launch_decode_attn_merge(const cf_decode_attn_args_t* a, void*
     const bool fast = use_fast(a);
     const int Gx = fast ? a->H_q / a->H_kv : 1;
     const int units_per_b = fast ? a->H_kv : a->H_q;
+    if (a->d % 4 == 0 && a->d / 4 <= kMergeThreads) {
+        dim3 grid((unsigned)((size_t)a->B * units_per_b * Gx));
+        if (a->elem == CF_ELEM_F16)
+            hipLaunchKernelGGL(merge_rows<_Float16>, grid, dim3(kMergeThreads), 0, s, *a, Gx, units_per_b);
+        else
+            hipLaunchKernelGGL(merge_rows<float>, grid, dim3(kMergeThreads), 0, s, *a, Gx, units_per_b);
+        return (int)hipGetLastError();
+    }
     const size_t total = (size_t)a->B * units_per_b * Gx * a->d;
     dim3 grid((unsigned)((total + kMergeThreads - 1) / kMergeThreads));
     if (a->elem == CF_ELEM_F16)

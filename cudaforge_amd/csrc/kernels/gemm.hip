@@ -24,14 +24,11 @@
 #include <stdint.h>
 
 #include "kernels.h"
+#include "cdna4.h"
 
 namespace {
 
-typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
-typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
-typedef float f4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 lds_h4_t;
-#define CF_LDS __attribute__((address_space(3)))
+using namespace cdna4;
 
 constexpr int kThreads = 256;
 constexpr int BM = 128, BN = 128;
@@ -325,36 +322,6 @@ constexpr int ST = A_ST + W_ST;         // 16 KB per stage
 
 __device__ __forceinline__ int swz_a(int row) { return (row >> 2) & 3; }
 __device__ __forceinline__ int swz_w(int row) { return ((row & 3) << 1) ^ (((row >> 3) & 1) << 3); }
-
-template <int N_OUT>
-__device__ __forceinline__ void wait_vm() {
-    // s_waitcnt vmcnt(N_OUT), expcnt/lgkmcnt left at their maxima (gfx9 encoding).
-    __builtin_amdgcn_s_waitcnt((N_OUT & 0xF) | ((N_OUT >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-// 16 bytes per lane from global memory into LDS at lds_base + 16*lane (M0 = lds_base).
-// Issued as inline asm so the compiler does not treat the LDS ring as pending DMA
-// writes (it would then wait for every load before each LDS read); completion is
-// tracked with explicit vmcnt waits instead.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(g), "s"(lds_base) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-__device__ __forceinline__ uint32_t lds_offset(const void* p) {
-    return (uint32_t)(uintptr_t)(const CF_LDS void*)p;
-}
-
-// Workgroup barrier without the vmcnt(0) wait __syncthreads implies (the ring keeps
-// DMA loads in flight across it); the empty asm statements stop the compiler from
-// moving LDS accesses across the barrier.
-__device__ __forceinline__ void ring_barrier() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
 
 __global__ __launch_bounds__(kThreads, 2)
 void gemm_f16_async(cf_gemm_args_t a, Tiling t) {

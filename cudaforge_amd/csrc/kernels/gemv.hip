@@ -13,8 +13,10 @@
 //       16-byte row segments), and the 8 columns become 8 A operands of 8 k values.
 // fp32: v_mfma_f32_16x16x4_f32.  A lane loads 1(k) x 4(n) twice per k step.
 // A workgroup (4 waves) owns a 128-column tile and one of `k_split` K chunks; waves
-// interleave k steps and reduce through LDS; the last workgroup of a tile (device-scope
-// counter) sums the K-chunk partials, adds the bias and scatters the result.
+// interleave k steps and reduce through LDS.  With k_split = 1 the workgroup adds the
+// bias and scatters the result; otherwise it writes an fp32 partial per K chunk and a
+// second launch (gemv_reduce) sums the partials, adds the bias and scatters.  The kernel
+// boundary orders the partials: no fences or atomics (each XCD has its own L2).
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>

@@ -59,10 +59,11 @@ static void plan_split(int elem, const decode_shape_t* s, int64_t t_max, int64_t
     if (g_chunk_override > 0) {
         c = cf_ceil_div(g_chunk_override, q) * q;
     } else {
-        /* Enough workgroups to keep every CU's memory pipeline full: the fp16 kernel
-         * is one wave per workgroup, so it wants ~16 per CU; the others are 2-4 waves. */
+        /* Enough workgroups to keep every CU's memory pipeline full.  The fp16 kernel
+         * is one wave with a 65 KB LDS ring (three 16 KB blocks in flight), two per CU;
+         * the others are 2-4 waves with registers as their only buffer. */
         const int64_t units = s->B * (fast ? s->H_kv : s->H);
-        const int64_t per_cu = (fast && elem == CF_ELEM_F16) ? 8 : 4;
+        const int64_t per_cu = (fast && elem == CF_ELEM_F16) ? 2 : 4;
         const int64_t target = per_cu * (int64_t)cf_cu_count();
         int64_t n = cf_ceil_div(target, units);
         const int64_t nmax = cf_ceil_div(t_max, q);
@@ -72,7 +73,7 @@ static void plan_split(int elem, const decode_shape_t* s, int64_t t_max, int64_t
     }
     if (c > cmax) c = cmax;
     if (c < q) c = q;
-    /* The merge kernel keeps 2 floats per (split, head) in LDS: at most 1024 splits. */
+    /* At most 1024 splits: bounds the partials workspace and the merge's serial loop. */
     if (cf_ceil_div(t_max, c) > 1024) c = cf_ceil_div(cf_ceil_div(t_max, 1024), q) * q;
     *chunk = c;
     *n_split = cf_ceil_div(t_max, c);

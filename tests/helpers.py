@@ -4,9 +4,16 @@ Box-Muller, or the reference tests' own glibc-rand / LCG fills)."""
 
 from __future__ import annotations
 
+import ctypes
+from ctypes import POINTER, c_int, c_int64, c_void_p
+
 import numpy as np
 
 import oracle as O
+
+# op_type_t values (include/graph.h, the reference's enum order) and data_type_t values.
+OP_MHA_FUSED, OP_MHA_DECODE, OP_CAUSAL_MASK, OP_RELU, OP_INPUT, OP_OUTPUT = 28, 29, 30, 0, 36, 37
+DT_F32, DT_F16 = 0, 1
 
 
 def max_abs(a, b) -> float:
@@ -156,3 +163,72 @@ def run_fused_gpu(case: FusedCase, stream=None):
     rc = cf.call_op(name, bufs, [Y], p, stream)
     assert rc == 0, f"{name} returned {rc}"
     return Y.download(stream).astype(np.float32)
+
+
+# ----------------------------------------------------------------------- graph ---
+
+class Graph:
+    """Small wrapper over the graph C-ABI; tensors are owned by the graph once added."""
+
+    def __init__(self, lib):
+        self.lib = lib
+        self.g = lib.graph_create()
+        assert self.g
+
+    @staticmethod
+    def _tensor(t):
+        import cudaforge_amd as cf
+        return ctypes.cast(t, POINTER(cf.TensorT)).contents
+
+    def tensor(self, arr, dtype=DT_F32):
+        arr = np.ascontiguousarray(arr)
+        assert arr.itemsize == (2 if dtype == DT_F16 else 4), "host array must match the tensor's element size"
+        shape = (c_int64 * max(arr.ndim, 1))(*arr.shape)
+        t = self.lib.tensor_create(dtype, arr.ndim, shape)
+        assert t
+        ctypes.memmove(self._tensor(t).data, arr.ctypes.data, arr.nbytes)
+        return t, self.lib.graph_add_tensor(self.g, t)
+
+    def write(self, t, arr):
+        """Overwrite a tensor's host data (same element count and size)."""
+        arr = np.ascontiguousarray(arr)
+        tt = self._tensor(t)
+        assert arr.size == tt.numel
+        ctypes.memmove(tt.data, arr.ctypes.data, arr.nbytes)
+
+    def node(self, op, ins, outs, weights=(), params=None):
+        ia = (c_int * max(len(ins), 1))(*ins)
+        oa = (c_int * max(len(outs), 1))(*outs)
+        wa = (c_void_p * max(len(weights), 1))(*weights)
+        pp = ctypes.addressof(params) if params is not None else None
+        ps = ctypes.sizeof(params) if params is not None else 0
+        return self.lib.graph_add_node(self.g, op, len(ins), ia, len(outs), oa, len(weights), wa, pp, ps)
+
+    def read(self, t, shape, dtype=np.float32):
+        out = np.empty(shape, dtype)
+        ctypes.memmove(out.ctypes.data, self._tensor(t).data, out.nbytes)
+        return out
+
+    def destroy(self):
+        self.lib.graph_destroy(self.g)
+
+
+def build_decode_graph(lib, c: DecodeCase):
+    """One OP_MHA_DECODE node with in-place KV caches registered through graph_set_kv_cache
+    (the reference's decode-session wiring, graph.c:133-153).  f16 cases use F16 tensors,
+    so the executor resolves mha_decode_f16_cuda.  Returns (graph, {name: tensor})."""
+    dt = DT_F16 if c.f16 else DT_F32
+    conv = (lambda a: O.to_f16(a)) if c.f16 else (lambda a: np.asarray(a, np.float32))
+    g = Graph(lib)
+    tX, iX = g.tensor(conv(c.X), dt)
+    tK, iK = g.tensor(conv(c.Kc), dt)
+    tV, iV = g.tensor(conv(c.Vc), dt)
+    tY, iY = g.tensor(conv(np.zeros_like(c.X)), dt)
+    ws = [g.tensor(conv(w), dt)[0] for w in (c.WQ, c.bQ, c.WK, c.bK, c.WV, c.bV, c.WO, c.bO)]
+    p = O.decode_params(c.B, c.D, c.H, c.H_kv, c.d, c.cache_len, c.max_seq)
+    g.node(OP_MHA_DECODE, [iX, iK, iV], [iY, iK, iV], ws, p)
+    lib.graph_set_input(g.g, g.node(OP_INPUT, [], [iX]))
+    lib.graph_set_output(g.g, g.node(OP_OUTPUT, [iY], []))
+    lib.graph_set_kv_cache(g.g, iK, iV)
+    assert lib.graph_build(g.g) == 0
+    return g, {"X": tX, "K": tK, "V": tV, "Y": tY}

@@ -21,14 +21,11 @@ import numpy as np
 import pytest
 
 import oracle as O
-from helpers import DecodeCase, FusedCase
+from helpers import (DT_F16, DT_F32, OP_CAUSAL_MASK, OP_INPUT, OP_MHA_DECODE, OP_MHA_FUSED, OP_OUTPUT,
+                     OP_RELU, DecodeCase, FusedCase, Graph)
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 INCLUDE = os.path.join(ROOT, "include")
-
-OP_MHA_FUSED, OP_MHA_DECODE, OP_CAUSAL_MASK, OP_RELU, OP_INPUT, OP_OUTPUT = 28, 29, 30, 0, 36, 37
-DT_F32, DT_F16 = 0, 1
-
 
 def declared_functions():
     names = set()
@@ -157,43 +154,6 @@ def test_fused_argument_validation(native):
 
 
 # ----------------------------------------------------------------------- graph ---
-
-class Graph:
-    """Small wrapper over the graph C-ABI; tensors are owned by the graph once added."""
-
-    def __init__(self, lib):
-        self.lib = lib
-        self.g = lib.graph_create()
-        assert self.g
-
-    def tensor(self, arr, dtype=DT_F32):
-        arr = np.ascontiguousarray(arr)
-        assert arr.itemsize == (2 if dtype == DT_F16 else 4), "host array must match the tensor's element size"
-        shape = (c_int64 * max(arr.ndim, 1))(*arr.shape)
-        t = self.lib.tensor_create(dtype, arr.ndim, shape)
-        assert t
-        tt = ctypes.cast(t, POINTER(__import__("cudaforge_amd").TensorT)).contents
-        ctypes.memmove(tt.data, arr.ctypes.data, arr.nbytes)
-        return t, self.lib.graph_add_tensor(self.g, t)
-
-    def node(self, op, ins, outs, weights=(), params=None):
-        ia = (c_int * max(len(ins), 1))(*ins)
-        oa = (c_int * max(len(outs), 1))(*outs)
-        wa = (c_void_p * max(len(weights), 1))(*weights)
-        pp = ctypes.addressof(params) if params is not None else None
-        ps = ctypes.sizeof(params) if params is not None else 0
-        return self.lib.graph_add_node(self.g, op, len(ins), ia, len(outs), oa, len(weights), wa, pp, ps)
-
-    def read(self, t, shape, dtype=np.float32):
-        import cudaforge_amd as cf
-        tt = ctypes.cast(t, POINTER(cf.TensorT)).contents
-        out = np.empty(shape, dtype)
-        ctypes.memmove(out.ctypes.data, tt.data, out.nbytes)
-        return out
-
-    def destroy(self):
-        self.lib.graph_destroy(self.g)
-
 
 _cpu_regs = []
 

@@ -8,6 +8,8 @@ slow), GQA group sizes 1..8, head sizes on the fast (64, 128) and generic paths,
 lengths, split-count invariance and non-aliased output caches.
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -181,3 +183,122 @@ def test_cache_len_zero_is_value_row(gpu):
     got = run_decode_attn_gpu(Q, K, V, 0, H_kv, False)
     want = np.repeat(V[:, 0], H // H_kv, axis=1)
     assert max_abs(want, got) <= 1e-6
+
+
+def test_config4_ragged_full_size(gpu):
+    """BASELINE config 4 at full size: B=4, 32/8 heads, d=128, capacity 32768, lengths
+    L_b ~ U[1024, 32768] (attended positions; cache_len_b = L_b - 1), fp16.  Every output
+    row against a float64 reference."""
+    B, H, H_kv, d, max_seq = 4, 32, 8, 128, 32768
+    L = O.uniform_int(B, 4, 1024, max_seq)
+    Q = O.round_f16(O.normal((B, H, d), 41))
+    K = O.round_f16(O.normal((B, max_seq, H_kv, d), 42))
+    V = O.round_f16(O.normal((B, max_seq, H_kv, d), 43))
+    got = run_decode_attn_gpu(Q, K, V, None, H_kv, True, seq_lens=L - 1)
+    ref = attn_ref64(Q, K, V, L, H_kv, float(1 / np.sqrt(d)))
+    assert max_abs(ref, got) <= TOL16
+
+
+@pytest.mark.parametrize("f16", [True, False])
+@pytest.mark.parametrize("chunk", [0, 256])
+def test_ragged_edge_lengths(gpu, native, f16, chunk):
+    """Per-sequence lengths at the split boundaries: one position, one short of a chunk,
+    exactly a chunk, one past it, a full cache."""
+    B, H, H_kv, d, max_seq = 8, 8, 2, 128, 1024
+    cl = np.array([0, 254, 255, 256, 511, 31, 32, max_seq - 1], np.int32)
+    Q = O.normal((B, H, d), 61)
+    K = O.normal((B, max_seq, H_kv, d), 62)
+    V = O.normal((B, max_seq, H_kv, d), 63)
+    if f16:
+        Q, K, V = O.round_f16(Q), O.round_f16(K), O.round_f16(V)
+    try:
+        native.mha_decode_set_split_chunk(chunk)
+        got = run_decode_attn_gpu(Q, K, V, None, H_kv, f16, seq_lens=cl)
+    finally:
+        native.mha_decode_set_split_chunk(0)
+    want = O.decode_attn(Q, K, V, cl + 1, float(1 / np.sqrt(d)), H_kv)
+    assert max_abs(want, got) <= (TOL16 if f16 else TOL32)
+
+
+def test_split_cap_1024(gpu, native):
+    """A requested chunk that would need more than 1024 splits is widened, not refused."""
+    B, H, H_kv, d, T = 1, 8, 2, 128, 40000
+    Q, K, V = (O.round_f16(O.normal(s, 70 + i)) for i, s in enumerate([(B, H, d), (B, T, H_kv, d), (B, T, H_kv, d)]))
+    try:
+        native.mha_decode_set_split_chunk(32)
+        got = run_decode_attn_gpu(Q, K, V, T - 1, H_kv, True)
+    finally:
+        native.mha_decode_set_split_chunk(0)
+    want = O.decode_attn(Q, K, V, np.full(B, T, np.int32), float(1 / np.sqrt(d)), H_kv)
+    assert max_abs(want, got) <= TOL16
+
+
+def test_config2_kv_permutation_invariance(gpu):
+    """Attention over a set of positions does not depend on their order: permuting K and V
+    rows together at full config-2 size changes only the summation order."""
+    B, H, H_kv, d, T = 16, 32, 8, 128, 4096
+    Q = O.round_f16(O.normal((B, H, d), 81))
+    K = O.round_f16(O.normal((B, T, H_kv, d), 82))
+    V = O.round_f16(O.normal((B, T, H_kv, d), 83))
+    perm = np.random.default_rng(84).permutation(T)
+    a = run_decode_attn_gpu(Q, K, V, T - 1, H_kv, True)
+    b = run_decode_attn_gpu(Q, np.ascontiguousarray(K[:, perm]), np.ascontiguousarray(V[:, perm]), T - 1, H_kv, True)
+    assert max_abs(a, b) <= 2e-3
+
+
+@pytest.mark.parametrize("f16", [True, False])
+def test_config2_linear_in_v(gpu, f16):
+    """Output is linear in V; scaling V by 2 is exact in binary floating point, so the
+    output must double bit for bit (any lost or double-counted term would break it).
+    Exception: fp16 outputs below 2^-14 are subnormal, where round-to-nearest on a fixed
+    2^-24 grid is not scale-invariant; there the two may differ by one 2^-24 step."""
+    B, H, H_kv, d, T = 16, 32, 8, 128, 4096
+    Q = O.round_f16(O.normal((B, H, d), 91))
+    K = O.round_f16(O.normal((B, T, H_kv, d), 92))
+    V = O.round_f16(O.normal((B, T, H_kv, d), 93))
+    a = run_decode_attn_gpu(Q, K, V, T - 1, H_kv, f16)
+    b = run_decode_attn_gpu(Q, K, V * np.float32(2), T - 1, H_kv, f16)
+    normal = np.abs(a) >= 2.0 ** -14 if f16 else np.ones(a.shape, bool)
+    assert np.array_equal(2 * a[normal], b[normal])
+    assert np.all(np.abs(2 * a[~normal] - b[~normal]) <= 2.0 ** -24)
+    assert normal.mean() > 0.99
+
+
+def test_decode_on_created_stream_matches_default(gpu):
+    """Ops enqueue on the caller's stream: a created (non-default) stream gives the same bits."""
+    import cudaforge_amd as cf
+    c = DecodeCase(4, 32, 8, 128, 600, cache_len=555, seed=12, f16=True)
+    a = run_decode_gpu(c)
+    s = cf.Stream()
+    b = run_decode_gpu(c, stream=s)
+    s.synchronize()
+    for x, y in zip(a, b):
+        assert np.array_equal(x, y)
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_graph_decode_two_steps_on_gpu(gpu, native, f16):
+    """graph_execute(use_cuda) over an OP_MHA_DECODE node with device-resident in-place
+    caches: step 1 at cache_len 5, then graph_update_cache_len(6) with a new token."""
+    from helpers import build_decode_graph
+    c = DecodeCase(2, 8, 2, 64, 16, cache_len=5, seed=31, f16=f16, wstd=0.1)
+    g, t = build_decode_graph(native, c)
+    dt = np.float16 if f16 else np.float32
+    tol = TOL16 if f16 else TOL32
+    ins, outs = (ctypes.c_void_p * 1)(t["X"]), (ctypes.c_void_p * 1)(t["Y"])
+    try:
+        assert native.graph_execute(g.g, ins, outs, True) == 0
+        want = c.oracle()
+        assert max_abs(want[0], g.read(t["Y"], c.X.shape, dt)) <= tol
+        c2 = DecodeCase(2, 8, 2, 64, 16, cache_len=6, seed=31, f16=f16, wstd=0.1)
+        c2.Kc, c2.Vc = want[1], want[2]
+        c2.X = O.normal(c.X.shape, 32)
+        if f16:
+            c2.X = O.round_f16(c2.X)
+        g.write(t["X"], O.to_f16(c2.X) if f16 else c2.X)
+        native.graph_update_cache_len(g.g, 6)
+        assert native.graph_execute(g.g, ins, outs, True) == 0
+        want2 = c2.oracle()
+        assert max_abs(want2[0], g.read(t["Y"], c.X.shape, dt)) <= tol
+    finally:
+        g.destroy()

@@ -8,6 +8,8 @@ selected batch rows (rows are independent, so a row of the full-size run must eq
 oracle on that row alone).
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -82,3 +84,45 @@ def test_config5_causal_full_size_row(gpu):
         setattr(sub, n, getattr(c, n))
     sub.X = c.X[2:3]
     assert max_abs(sub.oracle(), got[2:3]) <= TOL16
+
+
+def test_residual_flag_with_null_residual(gpu):
+    """has_residual with a NULL residual slot adds nothing (the reference's `R != NULL`
+    guard, mha_fused.c:165-170)."""
+    c = FusedCase(2, 64, 4, 4, 64, seed=9, f16=True, residual=False, bias_std=0.02)
+    want = c.oracle()
+    c.residual = True          # flag on, slot 1 stays NULL
+    got = run_fused_gpu(c)
+    assert max_abs(want, got) <= TOL16
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_graph_fused_on_gpu(gpu, native, f16):
+    """graph_execute(use_cuda) over one OP_MHA_FUSED node (the reference's GPU graph test,
+    tests/test_bert_mha.c:167-306): F32 tensors resolve to mha_fused_f32_cuda, F16 tensors
+    to mha_fused_f16_cuda."""
+    from helpers import DT_F16, DT_F32, OP_INPUT, OP_MHA_FUSED, OP_OUTPUT, Graph
+    import oracle as O
+    c = FusedCase(2, 48, 4, 2, 32, seed=17, f16=f16, residual=True, causal=True, bias_std=0.02)
+    dt, npdt = (DT_F16, np.float16) if f16 else (DT_F32, np.float32)
+    conv = (lambda a: O.to_f16(a)) if f16 else (lambda a: np.asarray(a, np.float32))
+    g = Graph(native)
+    try:
+        tX, iX = g.tensor(conv(c.X), dt)
+        tR, iR = g.tensor(conv(c.R), dt)
+        tY, iY = g.tensor(conv(np.zeros_like(c.X)), dt)
+        ws = [g.tensor(conv(w), dt)[0] for w in (c.WQ, c.bQ, c.WK, c.bK, c.WV, c.bV, c.WO, c.bO)]
+        p = O.fused_params(c.B, c.S, c.D, c.H, c.H_kv, c.d, True, True)
+        nid = g.node(OP_MHA_FUSED, [iX, iR], [iY], ws, p)
+        native.graph_set_input(g.g, g.node(OP_INPUT, [], [iX]))
+        native.graph_set_output(g.g, g.node(OP_OUTPUT, [iY], []))
+        assert native.graph_build(g.g) == 0
+        buf = ctypes.create_string_buffer(64)
+        assert native.graph_resolve_op(g.g, nid, True, buf, 64)
+        assert buf.value == (b"mha_fused_f16_cuda" if f16 else b"mha_fused_f32_cuda")
+        ins, outs = (ctypes.c_void_p * 1)(tX), (ctypes.c_void_p * 1)(tY)
+        assert native.graph_execute(g.g, ins, outs, True) == 0
+        got = g.read(tY, c.X.shape, npdt)
+        assert max_abs(c.oracle(), got) <= (TOL16 if f16 else TOL32)
+    finally:
+        g.destroy()
