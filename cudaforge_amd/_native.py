@@ -4,7 +4,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int64, c_size_t, c_void_p
+from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcudaforge_amd.so")
 
@@ -93,10 +93,14 @@ def _proto(lib):
         "operator_register": (c_int, [c_void_p]),
         "operator_time": (c_int, [c_char_p, POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_void_p, c_int, c_int,
                                   POINTER(c_float)]),
-        "mha_decode_attn_kernel_times": (c_int, [POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_void_p, c_int,
-                                                 c_int, c_int, POINTER(c_float), POINTER(c_float)]),
+        "operator_time_sets": (c_int, [c_char_p, POINTER(c_void_p), c_int, POINTER(c_void_p), c_int, c_int,
+                                       c_void_p, c_void_p, c_int, c_int, POINTER(c_float)]),
+        "mha_decode_attn_kernel_times": (c_int, [POINTER(c_void_p), c_int, c_int, POINTER(c_void_p), c_void_p,
+                                                 c_void_p, c_int, c_int, c_int, POINTER(c_float), POINTER(c_float)]),
         # decode planning knobs
         "mha_decode_set_split_chunk": (None, [c_int64]),
+        "cf_gemv_set_dma_tile": (None, [c_int32]),
+        "cf_decode_attn_set_stages": (None, [c_int32]),
         "mha_decode_plan": (c_int, [c_void_p, c_int, POINTER(c_int64), POINTER(c_int64)]),
         # host platform / tensors
         "platform_init": (c_int, []),

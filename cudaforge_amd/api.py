@@ -237,6 +237,32 @@ def time_op(name: str, inputs, outputs, params, stream: Stream | None, warmup: i
     return ms.value / iters
 
 
+def time_op_sets(name: str, input_sets, output_sets, params, stream: Stream | None, warmup: int,
+                 iters: int) -> float:
+    """Average milliseconds per call, rotating over several (inputs, outputs) sets: lists
+    of equal-length input lists and output lists; call j uses set j % len(input_sets).
+    Timed by operator_time_sets.  With a working set larger than the last-level cache,
+    every call reads HBM."""
+    lib = load_library()
+    if len(input_sets) != len(output_sets) or not input_sets:
+        raise ValueError("one output list per input set")
+    n_in, n_out = len(input_sets[0]), len(output_sets[0])
+    if any(len(x) != n_in for x in input_sets) or any(len(x) != n_out for x in output_sets):
+        raise ValueError("sets must have equal lengths")
+    ins = [_ptr(x) for s in input_sets for x in s]
+    outs = [_ptr(x) for s in output_sets for x in s]
+    in_arr = (c_void_p * len(ins))(*ins)
+    out_arr = (c_void_p * len(outs))(*outs)
+    ms = c_float(0.0)
+    st = stream.stream_t() if stream is not None else None
+    rc = lib.operator_time_sets(name.encode(), ctypes.cast(in_arr, POINTER(c_void_p)), n_in,
+                                ctypes.cast(out_arr, POINTER(c_void_p)), n_out, len(input_sets),
+                                ctypes.cast(ctypes.pointer(params), c_void_p), st, warmup, iters, ctypes.byref(ms))
+    if rc != 0:
+        raise RuntimeError(f"operator_time_sets({name}) returned {rc}")
+    return ms.value / iters
+
+
 def call_op(name: str, inputs, outputs, params, stream: Stream | None = None, extra_inputs=()) -> int:
     """Call a registered operator through its registry function pointer, exactly as the
     reference tests do (operator_find(...)->func(inputs, outputs, params, stream))."""

@@ -39,7 +39,9 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyMax = 8.0f;           // fp16 split kernel: max headroom of p (log2 units)
 constexpr int kChunkMax = 4096;            // positions per split (LDS: chunk * G floats)
 constexpr int kF16Quantum = 32;            // fp16 split kernel: positions per block
-constexpr int kDecodeStages = 4;           // fp16 split kernel: LDS ring depth (16 KB per stage at d = 128)
+constexpr int kDecodeStages = 3;           // fp16 split kernel: default LDS ring depth (16 KB per stage at d = 128;
+                                           // 3 stages = 3 workgroups per CU, best measured with HBM-resident KV)
+constexpr int kLdsPerCu = 160 * 1024;      // LDS of one gfx950 CU
 constexpr int kF32Threads = 256;
 constexpr int kF32Unroll = 4;
 constexpr int kGenericThreads = 128;
@@ -84,7 +86,7 @@ __device__ __forceinline__ int kswz(int row) { return (row / (128 / D)) % (D / 8
 template <int D>
 __device__ __forceinline__ int vswz(int row) { return 2 * ((row / (128 / D)) % (D / 16)); }
 
-template <int D, int G>
+template <int D, int G, int NS>
 __global__ __launch_bounds__(64)
 void split_f16(cf_decode_attn_args_t a) {
     constexpr int KT = D / 32;          // 32-dim MFMA steps per 16 positions
@@ -93,7 +95,6 @@ void split_f16(cf_decode_attn_args_t a) {
     constexpr int RPI = 64 / CPR;       // rows per DMA instruction (1 KB)
     constexpr int NI = BP / RPI;        // DMA instructions per block per tensor
     constexpr int NL = 2 * NI;          // ... for K and V
-    constexpr int NS = kDecodeStages;
     constexpr int TILE = BP * D;        // halves per block per tensor
     constexpr int NT = D / 16;          // output tiles of 16 dims
     constexpr int HDR = part_hdr(G);
@@ -671,11 +672,25 @@ bool use_fast(const cf_decode_attn_args_t* a) {
     return aligned && fast_supported(a->elem, a->d, G) && (a->elem != CF_ELEM_F16 || a->scale > 0.0f);
 }
 
+int g_stages = 0;   // tuning override of the fp16 ring depth (2..4; 0 = kDecodeStages)
+
+int f16_stages() { return g_stages >= 2 && g_stages <= 4 ? g_stages : kDecodeStages; }
+
+// Static LDS of split_f16<D, G, NS>: the ring plus the Q area.
+int f16_lds_bytes(int d, int G, int NS) {
+    const int qh = (G * d * 2 + 1023) / 1024 * 512;
+    return (NS * 2 * 32 * d + qh) * 2;
+}
+
 template <int D, int G>
 hipError_t launch_split_fast(const cf_decode_attn_args_t& a, hipStream_t s) {
     dim3 grid((unsigned)a.n_split, (unsigned)a.H_kv, (unsigned)a.B);
     if (a.elem == CF_ELEM_F16) {
-        hipLaunchKernelGGL((split_f16<D, G>), grid, dim3(64), 0, s, a);
+        switch (f16_stages()) {
+            case 2: hipLaunchKernelGGL((split_f16<D, G, 2>), grid, dim3(64), 0, s, a); break;
+            case 3: hipLaunchKernelGGL((split_f16<D, G, 3>), grid, dim3(64), 0, s, a); break;
+            default: hipLaunchKernelGGL((split_f16<D, G, 4>), grid, dim3(64), 0, s, a); break;
+        }
     } else {
         const int NW = kF32Threads / 64;
         const int sc_floats = a.chunk * G > NW * G * D ? a.chunk * G : NW * G * D;
@@ -699,6 +714,14 @@ hipError_t launch_split_g(const cf_decode_attn_args_t& a, int G, hipStream_t s) 
 
 extern "C" int32_t cf_decode_attn_chunk_quantum(int32_t elem, int32_t d, int32_t group) {
     return fast_supported(elem, d, group) ? quantum(elem, d) : 0;
+}
+
+extern "C" void cf_decode_attn_set_stages(int32_t stages) { g_stages = stages; }
+
+extern "C" int32_t cf_decode_attn_wgs_per_cu(int32_t elem, int32_t d, int32_t group) {
+    if (elem != CF_ELEM_F16 || !fast_supported(elem, d, group)) return 0;
+    const int n = kLdsPerCu / f16_lds_bytes(d, group, f16_stages());
+    return n < 1 ? 1 : n;
 }
 
 extern "C" int32_t cf_decode_attn_chunk_max(int32_t elem, int32_t d, int32_t group) {

@@ -9,24 +9,34 @@
 //   MFMA cols  <- batch rows m       (B operand = X, k-contiguous rows of X)
 //   MFMA k     <- reduction index k
 //
-// fp16: v_mfma_f32_16x16x32_f16.  A lane loads an 8(k) x 8(n) block of W (eight
-//       16-byte row segments), and the 8 columns become 8 A operands of 8 k values.
-// fp32: v_mfma_f32_16x16x4_f32.  A lane loads 1(k) x 4(n) twice per k step.
-// A workgroup (4 waves) owns a 128-column tile and one of `k_split` K chunks; waves
-// interleave k steps and reduce through LDS.  With k_split = 1 the workgroup adds the
-// bias and scatters the result; otherwise it writes an fp32 partial per K chunk and a
-// second launch (gemv_reduce) sums the partials, adds the bias and scatters.  The kernel
-// boundary orders the partials: no fences or atomics (each XCD has its own L2).
+// Two kernels:
+// * gemv_f16_dma (fp16, K % 32 == 0, every segment width % 64 == 0, 16-byte aligned):
+//   one wave per 64/128/256 columns and K chunk, W and X streamed by DMA into an LDS
+//   ring and multiplied as Y = X . W on MFMA (see the kernel); the K split is planned
+//   here from the CU count.
+// * gemv_kernel (any shape, fp16 or fp32), with the roles swapped:
+//   MFMA rows  <- output columns n   (A operand = W^T, transposed in registers)
+//   MFMA cols  <- batch rows m       (B operand = X, k-contiguous rows of X)
+//   MFMA k     <- reduction index k
+//   fp16: v_mfma_f32_16x16x32_f16.  A lane loads an 8(k) x 8(n) block of W (eight
+//         16-byte row segments), and the 8 columns become 8 A operands of 8 k values.
+//   fp32: v_mfma_f32_16x16x4_f32.  A lane loads 1(k) x 4(n) twice per k step.
+//   A workgroup (4 waves) owns a 128-column tile and one of `k_split` K chunks; waves
+//   interleave k steps and reduce through LDS.
+// With one K chunk the workgroup adds the bias and scatters the result; otherwise it
+// writes an fp32 partial per K chunk and a second launch (gemv_reduce) sums the
+// partials, adds the bias and scatters.  The kernel boundary orders the partials: no
+// fences or atomics (each XCD has its own L2).
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "kernels.h"
+#include "cdna4.h"
 
 namespace {
 
-typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
-typedef float f4_t __attribute__((ext_vector_type(4)));
+using namespace cdna4;
 
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
@@ -43,6 +53,9 @@ struct Tiles {
     int start[CF_GEMV_MAX_SEGS + 1];  // first column tile of each segment; start[nseg] = total
     int k_chunk;
     int vec_ok;
+    int bn;                           // columns per tile
+    int ks;                           // K chunks (workgroups along K)
+    int dma;                          // fp16 DMA path: its tile width (64/128/256), else 0
 };
 
 __device__ __forceinline__ float to_f(float x) { return x; }
@@ -197,19 +210,148 @@ void gemv_kernel(cf_gemv_args_t a, Tiles t) {
     }
 }
 
+// ---- fp16 DMA path: one wave per workgroup owns BN = 64, 128 or 256 columns and one K
+// chunk of an M tile of 16 rows.  Per 32-row k step, W (32 x BN) and X (16 x 32) go
+// from HBM straight into an NS-deep LDS ring (global_load_lds_dwordx4 with a uniform
+// base and per-lane offsets fixed for the whole loop, so the issue is scalar work), and
+// the wave runs BN/16 MFMAs  Y(16 rows x 16 cols) += X(16 x 32) . W(32 x 16): the X
+// fragment is one ds_read_b128, each W fragment two ds_read_b64_tr_b16 (8 consecutive k
+// of one column).  LDS rows are XOR-swizzled in 16-byte chunks so both read patterns
+// are bank-conflict free.  Wider tiles read longer contiguous row segments of W.
+constexpr int kDK = 32;
+
+template <int BN> struct Dma;
+template <> struct Dma<64>  { static constexpr int NS = 6; static constexpr int PER_CU = 4; };
+template <> struct Dma<128> { static constexpr int NS = 5; static constexpr int PER_CU = 3; };
+template <> struct Dma<256> { static constexpr int NS = 4; static constexpr int PER_CU = 2; };
+
+template <int BN>
+__device__ __forceinline__ int wswz(int row) {
+    if constexpr (BN == 64) return (((row >> 1) & 1) << 1) | (((row >> 3) & 1) << 2);
+    else return ((row & 3) << 1) | (((row >> 3) & 1) << 3);
+}
+__device__ __forceinline__ int xswz(int row) { return (row >> 2) & 3; }
+
+template <int NL, int N_AHEAD>
+__device__ __forceinline__ void wait_ahead(int ahead) {
+    if (ahead >= N_AHEAD) wait_vm<N_AHEAD * NL>();
+    else if constexpr (N_AHEAD > 0) wait_ahead<NL, N_AHEAD - 1>(ahead);
+}
+
+template <int BN>
+__global__ __launch_bounds__(64)
+void gemv_f16_dma(cf_gemv_args_t a, Tiles t) {
+    constexpr int NS = Dma<BN>::NS;
+    constexpr int CPR = BN / 8;                  // 16-byte chunks per W row
+    constexpr int RPI = 64 / CPR;                // W rows per DMA instruction
+    constexpr int NI = kDK / RPI;                // W DMA instructions per stage
+    constexpr int NL = NI + 1;                   // ... plus one for X
+    constexpr int NT = BN / 16;                  // MFMA column tiles
+    constexpr int STAGE = kDK * BN + kMTile * kDK;   // halves per stage: W then X
+    static_assert((NS - 2) * NL < 64, "vmcnt range");
+    __shared__ __attribute__((aligned(16))) _Float16 ring[NS * STAGE];
+
+    const int tile = blockIdx.x, ks = blockIdx.y, mt = blockIdx.z;
+    const int seg = seg_of(a, t, tile);
+    const cf_gemv_seg_t& sg = a.seg[seg];
+    const int N = (int)sg.n;
+    const int n0 = (tile - t.start[seg]) * BN;
+    const int kbeg = ks * t.k_chunk;
+    const int nst = (min(a.K, kbeg + t.k_chunk) - kbeg) / kDK;     // K % 32 == 0 on this path
+    const int lane = threadIdx.x, lr = lane & 15, lq = lane >> 4;
+    const _Float16* __restrict__ W = (const _Float16*)sg.w;
+    const _Float16* __restrict__ X = (const _Float16*)a.x;
+
+    // DMA: W instruction u fills k rows RPI*u .. (lane L: row RPI*u + L/CPR, physical
+    // chunk L%CPR = logical chunk (L%CPR) ^ wswz(row)); the X instruction fills the 16
+    // rows of the M tile (lane L: row L/4, clamped to the last real row, chunk
+    // (L%4) ^ xswz(row)).
+    uint32_t woff[NI];
+#pragma unroll
+    for (int u = 0; u < NI; u++) {
+        const int row = RPI * u + lane / CPR;
+        woff[u] = (uint32_t)row * (uint32_t)N * 2u + 16u * (uint32_t)((lane % CPR) ^ wswz<BN>(row));
+    }
+    const int xr = lane >> 2;
+    const uint32_t xoff = (uint32_t)min(mt * kMTile + xr, a.M - 1) * (uint32_t)a.K * 2u +
+                          16u * (uint32_t)((lane & 3) ^ xswz(xr));
+    const uint32_t base = lds_offset(ring);
+    auto issue = [&](int st) {
+        const int k0 = kbeg + st * kDK;
+        const uint32_t sb = base + (uint32_t)((st % NS) * STAGE) * 2u;
+        const _Float16* wb = W + (size_t)k0 * N + n0;
+#pragma unroll
+        for (int u = 0; u < NI; u++) lds_dma16_s(woff[u], wb, sb + u * 1024u);
+        lds_dma16_s(xoff, X + k0, sb + (uint32_t)(kDK * BN) * 2u);
+    };
+
+    // Per-lane LDS read offsets (halves) inside a stage.
+    const int x_rd = kDK * BN + lr * kDK + 8 * (lq ^ xswz(lr));
+    int w_rd[NT][2];
+#pragma unroll
+    for (int j = 0; j < NT; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int row = 8 * lq + 4 * h + (lr >> 2);
+            const int col = 16 * j + 4 * (lr & 3);
+            w_rd[j][h] = row * BN + 8 * ((col >> 3) ^ wswz<BN>(row)) + (col & 7);
+        }
+
+    f4_t acc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; j++) acc[j] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < NS - 1; st++)
+        if (st < nst) issue(st);
+    for (int st = 0; st < nst; st++) {
+        wait_ahead<NL, NS - 2>(min(NS - 2, nst - 1 - st));
+        // The stage refilled here was read by the previous step, whose LDS reads have
+        // all returned (their values fed its MFMAs): one wave needs no barrier.
+        if (st + NS - 1 < nst) issue(st + NS - 1);
+        const _Float16* sp = ring + (st % NS) * STAGE;
+        const h8_t xa = *(const h8_t*)(sp + x_rd);
+#pragma unroll
+        for (int j = 0; j < NT; j++) {
+            const h8_t wb = cat8(ds_read_tr4(sp + w_rd[j][0]), ds_read_tr4(sp + w_rd[j][1]));
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, wb, acc[j], 0, 0, 0);
+        }
+    }
+
+    // Lane (lr, lq) holds Y[m = 16mt + 4lq + i][n0 + 16j + lr].
+    if (t.ks == 1) {
+#pragma unroll
+        for (int j = 0; j < NT; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = mt * kMTile + 4 * lq + i;
+                if (m < a.M) store_out<_Float16>(a, sg, m, n0 + 16 * j + lr, acc[j][i]);
+            }
+    } else {
+        const int ncols = t.start[a.nseg] * BN;
+        const int Mp = gridDim.z * kMTile;
+#pragma unroll
+        for (int j = 0; j < NT; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = mt * kMTile + 4 * lq + i;
+                a.partials[((size_t)ks * Mp + m) * ncols + (size_t)tile * BN + 16 * j + lr] = acc[j][i];
+            }
+    }
+}
+
 // Sums the K-chunk partials of every output element and applies the epilogue.
 template <typename T>
 __global__ __launch_bounds__(256)
 void gemv_reduce(cf_gemv_args_t a, Tiles t) {
-    const int ncols = t.start[a.nseg] * kColTile;
+    const int ncols = t.start[a.nseg] * t.bn;
     const int Mp = (a.M + kMTile - 1) / kMTile * kMTile;
     const size_t total = (size_t)a.M * ncols;
     const size_t plane = (size_t)Mp * ncols;
     for (size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (size_t)gridDim.x * 256) {
         const int m = (int)(idx / ncols), col = (int)(idx - (size_t)m * ncols);
-        const int tile = col / kColTile;
+        const int tile = col / t.bn;
         const int seg = seg_of(a, t, tile);
-        const int n = (tile - t.start[seg]) * kColTile + (col - tile * kColTile);
+        const int n = (tile - t.start[seg]) * t.bn + (col - tile * t.bn);
         if (n >= a.seg[seg].n) continue;
         const float* p = a.partials + (size_t)m * ncols + col;
         // Eight independent loads in flight per round trip.
@@ -227,20 +369,64 @@ void gemv_reduce(cf_gemv_args_t a, Tiles t) {
     }
 }
 
+int cu_count_cached() {
+    static int dev_cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (dev_cus[dev] <= 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        dev_cus[dev] = n;
+    }
+    return dev_cus[dev];
+}
+
+int g_dma_bn = 0;   // tuning override of the DMA path's tile width (0 = automatic)
+
+// Tile width of the DMA path, or 0 if it does not apply: 128 columns (measured best at
+// the decode shapes; 64 and 256 ran 5-15 % slower), else the widest that divides every
+// segment.
+int dma_bn(const cf_gemv_args_t* a) {
+    if (a->elem != CF_ELEM_F16 || a->K % kDK != 0 || ((uintptr_t)a->x) % 16 != 0) return 0;
+    int bn = 128;
+    for (int s = 0; s < a->nseg; s++) {
+        if (((uintptr_t)a->seg[s].w) % 16 != 0) return 0;
+        while (bn >= 64 && a->seg[s].n % bn != 0) bn /= 2;
+    }
+    if (bn < 64) return 0;
+    if (g_dma_bn >= 64 && g_dma_bn <= bn) bn = g_dma_bn;
+    return bn;
+}
+
 Tiles make_tiles(const cf_gemv_args_t* a) {
     Tiles t{};
+    const int bn = dma_bn(a);
+    t.dma = bn;
+    t.bn = bn ? bn : kColTile;
     int acc = 0;
     for (int s = 0; s < a->nseg; s++) {
         t.start[s] = acc;
-        acc += (int)((a->seg[s].n + kColTile - 1) / kColTile);
+        acc += (int)((a->seg[s].n + t.bn - 1) / t.bn);
     }
     for (int s = a->nseg; s <= CF_GEMV_MAX_SEGS; s++) t.start[s] = acc;
-    const int kstep = a->elem == CF_ELEM_F16 ? Cfg<_Float16>::KSTEP : Cfg<float>::KSTEP;
-    const int vec = a->elem == CF_ELEM_F16 ? 8 : 4;
-    const int ks = a->k_split > 0 ? a->k_split : 1;
+    const int kstep = bn ? kDK : (a->elem == CF_ELEM_F16 ? Cfg<_Float16>::KSTEP : Cfg<float>::KSTEP);
+    int ks;
+    if (bn) {
+        // Enough one-wave workgroups per CU for the ring depth of this tile width.
+        const int per_cu = bn == 64 ? Dma<64>::PER_CU : bn == 128 ? Dma<128>::PER_CU : Dma<256>::PER_CU;
+        const int m_tiles = (a->M + kMTile - 1) / kMTile;
+        const int units = acc * m_tiles;
+        ks = (per_cu * cu_count_cached() + units - 1) / units;
+        if (ks > a->K / kDK) ks = a->K / kDK;
+        if (ks < 1) ks = 1;
+    } else {
+        ks = a->k_split > 0 ? a->k_split : 1;
+    }
     int chunk = (a->K + ks - 1) / ks;
     chunk = (chunk + kstep - 1) / kstep * kstep;
     t.k_chunk = chunk;
+    t.ks = (a->K + chunk - 1) / chunk;   // every chunk non-empty
+    const int vec = a->elem == CF_ELEM_F16 ? 8 : 4;
     int ok = (a->K % vec == 0) && (((uintptr_t)a->x) % 16 == 0);
     for (int s = 0; s < a->nseg; s++)
         ok = ok && (a->seg[s].n % vec == 0) && (((uintptr_t)a->seg[s].w) % 16 == 0);
@@ -251,34 +437,39 @@ Tiles make_tiles(const cf_gemv_args_t* a) {
 }  // namespace
 
 extern "C" int32_t cf_gemv_col_tile(int32_t elem) { (void)elem; return kColTile; }
+extern "C" void cf_gemv_set_dma_tile(int32_t bn) { g_dma_bn = bn; }
 extern "C" int32_t cf_gemv_k_step(int32_t elem) {
     return elem == CF_ELEM_F16 ? Cfg<_Float16>::KSTEP : Cfg<float>::KSTEP;
 }
 
 extern "C" size_t cf_gemv_partials_floats(const cf_gemv_args_t* a) {
-    if (a->k_split <= 1) return 0;
     const Tiles t = make_tiles(a);
+    if (t.ks <= 1) return 0;
     const size_t Mp = (size_t)((a->M + kMTile - 1) / kMTile) * kMTile;
-    return (size_t)a->k_split * Mp * (size_t)t.start[a->nseg] * kColTile;
+    return (size_t)t.ks * Mp * (size_t)t.start[a->nseg] * t.bn;
 }
 
 extern "C" int cf_launch_gemv(const cf_gemv_args_t* a, void* stream) {
     const Tiles t = make_tiles(a);
-    // Every K chunk must be non-empty (each writes its full partial plane).
-    const int ks = a->k_split > 0 ? a->k_split : 1;
-    if ((ks - 1) * t.k_chunk >= a->K) return (int)hipErrorInvalidValue;
+    if (a->M <= 0 || a->K <= 0 || t.start[a->nseg] <= 0) return (int)hipErrorInvalidValue;
     cf_gemv_args_t args = *a;
-    args.k_split = ks;
+    args.k_split = t.ks;
     hipStream_t s = (hipStream_t)stream;
     const int m_tiles = (a->M + kMTile - 1) / kMTile;
-    dim3 grid((unsigned)t.start[a->nseg], (unsigned)ks, (unsigned)m_tiles);
-    if (a->elem == CF_ELEM_F16)
+    dim3 grid((unsigned)t.start[a->nseg], (unsigned)t.ks, (unsigned)m_tiles);
+    if (t.dma == 256)
+        hipLaunchKernelGGL(gemv_f16_dma<256>, grid, dim3(64), 0, s, args, t);
+    else if (t.dma == 128)
+        hipLaunchKernelGGL(gemv_f16_dma<128>, grid, dim3(64), 0, s, args, t);
+    else if (t.dma == 64)
+        hipLaunchKernelGGL(gemv_f16_dma<64>, grid, dim3(64), 0, s, args, t);
+    else if (a->elem == CF_ELEM_F16)
         hipLaunchKernelGGL(gemv_kernel<_Float16>, grid, dim3(kThreads), 0, s, args, t);
     else
         hipLaunchKernelGGL(gemv_kernel<float>, grid, dim3(kThreads), 0, s, args, t);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || ks == 1) return (int)e;
-    const size_t total = (size_t)a->M * t.start[a->nseg] * kColTile;
+    if (e != hipSuccess || t.ks == 1) return (int)e;
+    const size_t total = (size_t)a->M * t.start[a->nseg] * t.bn;
     size_t blocks = (total + 255) / 256;
     if (blocks > 4096) blocks = 4096;
     if (a->elem == CF_ELEM_F16)

@@ -44,6 +44,11 @@ typedef struct {
 /* Positions one workgroup pass covers (chunk must be a multiple); 0 = generic kernel. */
 int32_t cf_decode_attn_chunk_quantum(int32_t elem, int32_t d, int32_t group);
 int32_t cf_decode_attn_chunk_max(int32_t elem, int32_t d, int32_t group);
+/* Workgroups of the fp16 split kernel that fit one CU (its LDS ring bounds it), or 0
+ * where that kernel does not apply. */
+int32_t cf_decode_attn_wgs_per_cu(int32_t elem, int32_t d, int32_t group);
+/* Tuning override of the fp16 split kernel's LDS ring depth (2..4; 0 = default 3). */
+void    cf_decode_attn_set_stages(int32_t stages);
 /* Workspace floats needed for the partials of a launch. */
 size_t  cf_decode_attn_partials_floats(int32_t B, int32_t H_q, int32_t H_kv, int32_t d,
                                        int32_t n_split, int32_t elem);
@@ -89,6 +94,9 @@ int32_t cf_gemv_col_tile(int32_t elem);
 int32_t cf_gemv_k_step(int32_t elem);
 size_t  cf_gemv_partials_floats(const cf_gemv_args_t* a);
 int     cf_launch_gemv(const cf_gemv_args_t* a, void* stream);
+/* Tuning override of the fp16 DMA path's column-tile width (64, 128 or 256; 0 =
+ * automatic: 128 where it divides every segment, else 64). */
+void    cf_gemv_set_dma_tile(int32_t bn);
 
 /* ---------------------------------------------------------------------------------
  * Prefill GEMM with fused epilogue: C = A·W + bias (+ residual), A (M, K) row-major,

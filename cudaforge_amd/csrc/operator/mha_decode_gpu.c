@@ -60,10 +60,11 @@ static void plan_split(int elem, const decode_shape_t* s, int64_t t_max, int64_t
         c = cf_ceil_div(g_chunk_override, q) * q;
     } else {
         /* Enough workgroups to keep every CU's memory pipeline full.  The fp16 kernel
-         * is one wave with a 65 KB LDS ring (three 16 KB blocks in flight), two per CU;
-         * the others are 2-4 waves with registers as their only buffer. */
+         * is one wave with an LDS ring, as many per CU as the ring allows; the others
+         * are 2-4 waves with registers as their only buffer. */
         const int64_t units = s->B * (fast ? s->H_kv : s->H);
-        const int64_t per_cu = (fast && elem == CF_ELEM_F16) ? 2 : 4;
+        const int32_t ring_cu = cf_decode_attn_wgs_per_cu(elem, (int)s->d, G);
+        const int64_t per_cu = ring_cu > 0 ? ring_cu : 4;
         const int64_t target = per_cu * (int64_t)cf_cu_count();
         int64_t n = cf_ceil_div(target, units);
         const int64_t nmax = cf_ceil_div(t_max, q);
@@ -132,39 +133,40 @@ static int attn_prepare(int elem, const void* inputs[], void* outputs[],
     return 0;
 }
 
-int mha_decode_attn_kernel_times(const void* inputs[], void* outputs[], const operator_params_t* params,
+int mha_decode_attn_kernel_times(const void* const* input_sets, int n_inputs, int n_sets,
+                                 void* outputs[], const operator_params_t* params,
                                  stream_t* stream, int elem_f16, int warmup, int iters,
                                  float* ms_split, float* ms_merge) {
-    if (!ms_split || !ms_merge || iters <= 0 || iters > 4096 || warmup < 0) return -1;
-    cf_decode_attn_args_t a;
-    int rc = attn_prepare(elem_f16 ? CF_ELEM_F16 : CF_ELEM_F32, inputs, outputs, params, &a);
-    if (rc != 0) return rc;
+    if (!input_sets || !ms_split || !ms_merge || iters <= 0 || iters > 4096 || warmup < 0 ||
+        n_inputs < 3 || n_sets < 1 || n_sets > 16)
+        return -1;
+    const int elem = elem_f16 ? CF_ELEM_F16 : CF_ELEM_F32;
+    cf_decode_attn_args_t a[16];
+    for (int s = 0; s < n_sets; s++) {
+        const int rc = attn_prepare(elem, (const void**)&input_sets[s * n_inputs], outputs, params, &a[s]);
+        if (rc != 0) return rc;
+    }
     void* st = cf_stream_of(stream);
+    int rc = 0;
     for (int i = 0; i < warmup; i++)
-        if ((rc = cf_launch_decode_attn(&a, st)) != 0) return rc;
-    gpu_event_t* ev = (gpu_event_t*)calloc((size_t)(3 * iters), sizeof(gpu_event_t));
-    if (!ev) return -1;
-    for (int i = 0; i < 3 * iters && rc == 0; i++) rc = gpu_event_create(&ev[i]);
-    for (int i = 0; i < iters && rc == 0; i++) {
-        rc = gpu_event_record(ev[3 * i], st);
-        if (rc == 0) rc = cf_launch_decode_attn_split(&a, st);
-        if (rc == 0) rc = gpu_event_record(ev[3 * i + 1], st);
-        if (rc == 0) rc = cf_launch_decode_attn_merge(&a, st);
-        if (rc == 0) rc = gpu_event_record(ev[3 * i + 2], st);
-    }
-    if (rc == 0) rc = gpu_event_synchronize(ev[3 * iters - 1]);
-    double s_sum = 0.0, m_sum = 0.0;
-    for (int i = 0; i < iters && rc == 0; i++) {
-        float t1 = 0.0f, t2 = 0.0f;
-        rc = gpu_event_elapsed_ms(&t1, ev[3 * i], ev[3 * i + 1]);
-        if (rc == 0) rc = gpu_event_elapsed_ms(&t2, ev[3 * i + 1], ev[3 * i + 2]);
-        s_sum += t1;
-        m_sum += t2;
-    }
-    for (int i = 0; i < 3 * iters; i++) if (ev[i]) gpu_event_destroy(ev[i]);
-    free(ev);
-    *ms_split = (float)(s_sum / iters);
-    *ms_merge = (float)(m_sum / iters);
+        if ((rc = cf_launch_decode_attn(&a[i % n_sets], st)) != 0) return rc;
+    /* `iters` split launches back to back between two events, then `iters` merge
+     * launches: per-launch events would add the dispatch latency of every launch. */
+    gpu_event_t ev[3] = {NULL, NULL, NULL};
+    for (int i = 0; i < 3 && rc == 0; i++) rc = gpu_event_create(&ev[i]);
+    if (rc == 0) rc = gpu_stream_synchronize(st);
+    if (rc == 0) rc = gpu_event_record(ev[0], st);
+    for (int i = 0; i < iters && rc == 0; i++) rc = cf_launch_decode_attn_split(&a[i % n_sets], st);
+    if (rc == 0) rc = gpu_event_record(ev[1], st);
+    for (int i = 0; i < iters && rc == 0; i++) rc = cf_launch_decode_attn_merge(&a[i % n_sets], st);
+    if (rc == 0) rc = gpu_event_record(ev[2], st);
+    if (rc == 0) rc = gpu_event_synchronize(ev[2]);
+    float t1 = 0.0f, t2 = 0.0f;
+    if (rc == 0) rc = gpu_event_elapsed_ms(&t1, ev[0], ev[1]);
+    if (rc == 0) rc = gpu_event_elapsed_ms(&t2, ev[1], ev[2]);
+    for (int i = 0; i < 3; i++) if (ev[i]) gpu_event_destroy(ev[i]);
+    *ms_split = t1 / (float)iters;
+    *ms_merge = t2 / (float)iters;
     return rc;
 }
 

@@ -24,11 +24,23 @@ int operator_time(const char* name, const void* inputs[], void* outputs[],
                   const operator_params_t* params, stream_t* stream,
                   int warmup, int iters, float* ms_total);
 
-/* The decode attention core (mha_decode_attn_{f16,f32}_cuda, same arguments) run
- * `iters` times (<= 4096) after `warmup` calls, with HIP events recorded around its
- * split kernel and its merge kernel separately; stores the mean duration of each (ms).
- * elem_f16 selects the fp16 (1) or fp32 (0) entry. */
-int mha_decode_attn_kernel_times(const void* inputs[], void* outputs[], const operator_params_t* params,
+/* As operator_time, rotating over `n_sets` (1..16) sets of `n_inputs` input and
+ * `n_outputs` output pointers (input_sets[s * n_inputs + i], output_sets[s * n_outputs
+ * + o]); call j uses set j % n_sets.  With a working set larger than the GPU's
+ * last-level cache (256 MB Infinity Cache on MI355X) every call reads its inputs from
+ * HBM, as a decode step does once the other layers of a model have run. */
+int operator_time_sets(const char* name, const void* const* input_sets, int n_inputs,
+                       void* const* output_sets, int n_outputs, int n_sets,
+                       const operator_params_t* params, stream_t* stream,
+                       int warmup, int iters, float* ms_total);
+
+/* The decode attention core (mha_decode_attn_{f16,f32}_cuda, inputs as for that entry,
+ * rotating over `n_sets` input sets laid out as in operator_time_sets): after `warmup`
+ * full calls, its split kernel is launched `iters` times (<= 4096) back to back between
+ * two HIP events, then its merge kernel likewise; stores the mean time per launch of
+ * each (ms).  elem_f16 selects the fp16 (1) or fp32 (0) entry. */
+int mha_decode_attn_kernel_times(const void* const* input_sets, int n_inputs, int n_sets,
+                                 void* outputs[], const operator_params_t* params,
                                  stream_t* stream, int elem_f16, int warmup, int iters,
                                  float* ms_split, float* ms_merge);
 

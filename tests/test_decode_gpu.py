@@ -302,3 +302,35 @@ def test_graph_decode_two_steps_on_gpu(gpu, native, f16):
         assert max_abs(want2[0], g.read(t["Y"], c.X.shape, dt)) <= tol
     finally:
         g.destroy()
+
+
+@pytest.mark.parametrize("bn", [64, 128, 256])
+def test_projection_tile_widths(gpu, native, bn):
+    """The fp16 projection kernel at each column-tile width (64/128/256) gives the same
+    decode result within tolerance (full op, config-2 head layout at reduced sizes)."""
+    c = DecodeCase(5, 8, 2, 128, 300, cache_len=299, seed=50 + bn, f16=True)
+    want = c.oracle()
+    try:
+        native.cf_gemv_set_dma_tile(bn)
+        got = run_decode_gpu(c)
+    finally:
+        native.cf_gemv_set_dma_tile(0)
+    for w, g in zip(want, got):
+        assert max_abs(w, g) <= TOL16
+
+
+@pytest.mark.parametrize("stages", [2, 3, 4])
+def test_split_ring_depths(gpu, native, stages):
+    """The fp16 split kernel at each LDS ring depth (2/3/4 stages), with ragged lengths that
+    end inside, at, and one past a 32-position block."""
+    B, H, H_kv, d, max_seq = 4, 16, 4, 128, 1200
+    lens = np.array([1199, 31, 32, 700], np.int32)     # cache_len_b; attended = +1
+    Q, K, V = (O.round_f16(O.normal(s, 90 + i)) for i, s in
+               enumerate([(B, H, d), (B, max_seq, H_kv, d), (B, max_seq, H_kv, d)]))
+    try:
+        native.cf_decode_attn_set_stages(stages)
+        got = run_decode_attn_gpu(Q, K, V, None, H_kv, True, seq_lens=lens)
+    finally:
+        native.cf_decode_attn_set_stages(0)
+    want = O.decode_attn(Q, K, V, lens + 1, float(1 / np.sqrt(d)), H_kv)
+    assert max_abs(want, got) <= TOL16
