@@ -86,6 +86,19 @@ __device__ __forceinline__ h8_t cat8(h4_t lo, h4_t hi) {
     return h8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
+// Compute units of the current device (cached per device; 256 on MI355X).
+inline int cu_count() {
+    static int dev_cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (dev_cus[dev] <= 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        dev_cus[dev] = n;
+    }
+    return dev_cus[dev];
+}
+
 }  // namespace cdna4
 
 #endif  // CF_CDNA4_H_

@@ -27,12 +27,11 @@
 #include <stdint.h>
 
 #include "kernels.h"
+#include "cdna4.h"
 
 namespace {
 
-typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
-typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
-typedef float f4_t __attribute__((ext_vector_type(4)));
+using namespace cdna4;
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kQB = 128;     // queries per workgroup (32 per wave)
@@ -223,6 +222,206 @@ void flash_f16(cf_flash_args_t a) {
     }
 }
 
+// ---- d = 64, S % 8 == 0: the same computation with K and V^T blocks streamed by DMA
+// (global_load_lds_dwordx4) into a kFlashStages-deep LDS ring instead of through
+// registers, so kFlashStages - 1 key blocks are in flight while one is used and no
+// wave waits on a block's loads before storing them.  K rows (128 B) and V^T rows (64
+// keys, 128 B) are XOR-swizzled in 16-byte chunks (chunk ^ (row / 2) % 8) so the K
+// fragment reads (16 rows, one chunk) and the V^T fragment reads (16 rows, 8 bytes) are
+// bank-conflict free.  Rows and chunks past the sequence end are clamped to the last
+// valid ones (S % 8 == 0 keeps every 8-key chunk whole) and get p = 0.  The row max is
+// reduced with the gfx950 row swaps, and the running max only moves when a block
+// exceeds it by more than kLazy (log2 units), so the accumulators are rarely rescaled.
+constexpr int kFlashStages = 3;
+constexpr float kLazy = 8.0f;
+
+__device__ __forceinline__ int fswz(int row) { return (row >> 1) & 7; }
+
+__global__ __launch_bounds__(kThreads, 3)
+void flash_f16_dma64(cf_flash_args_t a) {
+    constexpr int D = 64;
+    constexpr int KT = D / 32;                    // 32-dim steps of S^T
+    constexpr int UT = D / 16;                    // 16-dim tiles of O^T
+    constexpr int TILE = kKB * D;                 // halves per block per tensor (8 KB)
+    constexpr int NS = kFlashStages;
+    __shared__ __attribute__((aligned(16))) _Float16 ring[NS * 2 * TILE];
+
+    const int nqb = (a.S + kQB - 1) / kQB;
+    const int HB = a.B * a.H_q;
+    const int w = blockIdx.x, r8 = w & 7, rest = w >> 3;
+    const int qi = rest % nqb, grp = rest / nqb;
+    const int hb = grp * 8 + r8;
+    if (hb >= HB) return;                          // padding of the last group of 8
+    const int qb = a.causal ? (nqb - 1 - qi) : qi;
+    const int h = hb % a.H_q, b = hb / a.H_q;
+    const int S = a.S;
+    const int kvh = h / (a.H_q / a.H_kv);
+    const int q0 = qb * kQB;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 15, lq = lane >> 4;
+    const int qw = q0 + 32 * wave;                 // first query of this wave
+
+    const _Float16* __restrict__ qp = (const _Float16*)a.q + (((size_t)b * a.H_q + h) * S) * D;
+    const _Float16* __restrict__ kp = (const _Float16*)a.k + (((size_t)b * a.H_kv + kvh) * S) * D;
+    const _Float16* __restrict__ vp = (const _Float16*)a.vt + (((size_t)b * a.H_kv + kvh) * D) * (size_t)S;
+
+    // Q fragments first, waited for before the ring starts (the DMA loads are invisible
+    // to the compiler's wait counting).
+    int query[2];
+    h8_t qf[2][KT];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        query[j] = qw + 16 * j + lr;
+        const _Float16* qr = qp + (size_t)min(query[j], S - 1) * D + 8 * lq;
+#pragma unroll
+        for (int kt = 0; kt < KT; kt++) qf[j][kt] = *(const h8_t*)(qr + 32 * kt);
+    }
+    wait_vm<0>();
+
+    // DMA: each wave fills K rows 16w .. 16w+15 and V^T rows 16w .. 16w+15 of a stage,
+    // 8 rows per instruction; lane L writes physical chunk L % 8 of row 8u + L / 8.
+    const uint32_t ring_base = lds_offset(ring);
+    const int drow0 = 16 * wave + (lane >> 3), dch = lane & 7;
+    auto issue = [&](int blk) {
+        const int k0 = blk * kKB;
+        const uint32_t kb = ring_base + (uint32_t)((blk % NS) * 2 * TILE) * 2u;
+        const uint32_t vb = kb + (uint32_t)TILE * 2u;
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int row = drow0 + 8 * u;
+            const int kc = dch ^ fswz(row);
+            lds_dma16(kp + (size_t)min(k0 + row, S - 1) * D + 8 * kc,
+                      __builtin_amdgcn_readfirstlane(kb + (uint32_t)(16 * wave + 8 * u) * 128u));
+            const int vcol = min(k0 + 8 * (dch ^ fswz(row)), S - 8);
+            lds_dma16(vp + (size_t)row * S + vcol,
+                      __builtin_amdgcn_readfirstlane(vb + (uint32_t)(16 * wave + 8 * u) * 128u));
+        }
+    };
+    // Per-lane LDS read offsets (halves) inside a stage.
+    int k_rd[4][KT];
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int kt = 0; kt < KT; kt++) {
+            const int row = 16 * t + lr;
+            k_rd[t][kt] = row * D + 8 * ((4 * kt + lq) ^ fswz(row));
+        }
+    int v_rd[UT][2][2];
+#pragma unroll
+    for (int u = 0; u < UT; u++)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; s2++)
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                const int row = 16 * u + lr;
+                const int ch = 4 * s2 + 2 * hh + (lq >> 1);          // keys 32s + 16hh + 4lq
+                v_rd[u][s2][hh] = TILE + row * kKB + 8 * (ch ^ fswz(row)) + 4 * (lq & 1);
+            }
+
+    const float c = a.scale * kLog2e;
+    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.0f, 0.0f};
+    f4_t acc[2][UT];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int u = 0; u < UT; u++) acc[j][u] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+    const int k_end = a.causal ? min(S, q0 + kQB) : S;
+    const int nblk = (k_end + kKB - 1) / kKB;
+#pragma unroll
+    for (int st = 0; st < NS - 1; st++)
+        if (st < nblk) issue(st);
+    for (int bi = 0; bi < nblk; bi++) {
+        // Blocks issued after this one that may still be in flight (4 loads each).
+        if (min(NS - 2, nblk - 1 - bi) >= 1) wait_vm<4>();
+        else wait_vm<0>();
+        ring_barrier();                            // every wave's part of block bi landed;
+                                                   // block bi-1's stage is free again
+        if (bi + NS - 1 < nblk) issue(bi + NS - 1);
+        const int k0 = bi * kKB;
+        const _Float16* st = ring + (bi % NS) * 2 * TILE;
+
+        // S^T tiles: sc[j][t][i] = score(key k0 + 16t + 4*lq + i, query[j]).
+        f4_t sc[2][4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            sc[0][t] = f4_t{0.f, 0.f, 0.f, 0.f};
+            sc[1][t] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kt = 0; kt < KT; kt++) {
+                const h8_t kf = *(const h8_t*)(st + k_rd[t][kt]);
+                sc[0][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[0][kt], sc[0][t], 0, 0, 0);
+                sc[1][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[1][kt], sc[1][t], 0, 0, 0);
+            }
+        }
+        const bool edge = (k0 + kKB > S) || (a.causal && k0 + kKB - 1 > qw);
+        h8_t pf[2][2];
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            if (edge) {
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int key = k0 + 16 * t + 4 * lq + i;
+                        if (key >= S || (a.causal && key > query[j])) sc[j][t][i] = -INFINITY;
+                    }
+            }
+            float mloc = fmaxf(fmaxf(sc[j][0][0], sc[j][0][1]), fmaxf(sc[j][0][2], sc[j][0][3]));
+#pragma unroll
+            for (int t = 1; t < 4; t++)
+                mloc = fmaxf(mloc, fmaxf(fmaxf(sc[j][t][0], sc[j][t][1]), fmaxf(sc[j][t][2], sc[j][t][3])));
+            mloc = max_xor32(max_xor16(mloc)) * c;     // -inf if the whole row is masked
+            if (__builtin_amdgcn_ballot_w64(mloc > m_run[j] + kLazy)) {
+                const float m_new = mloc > m_run[j] + kLazy ? mloc : m_run[j];
+                const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_new);   // 0 on the first move
+                m_run[j] = m_new;
+                l_run[j] *= alpha;
+#pragma unroll
+                for (int u = 0; u < UT; u++) acc[j][u] *= alpha;
+            }
+            // Rows with nothing visible yet keep m = -inf: use 0 so p = 2^-inf = 0.
+            const float m_use = m_run[j] == -INFINITY ? 0.0f : m_run[j];
+            float psum = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][t][i], c, -m_use));
+                    psum += p;
+                    pf[j][t >> 1][(t & 1) * 4 + i] = (_Float16)p;
+                }
+            l_run[j] += psum;
+        }
+        // O^T[16u + 4*lq + i][query] += V^T . P^T; in 32-key step s, k-slot e of lane group
+        // lq is key 32s + 16*(e/4) + 4*lq + (e%4).
+#pragma unroll
+        for (int u = 0; u < UT; u++)
+#pragma unroll
+            for (int s2 = 0; s2 < 2; s2++) {
+                const h4_t lo = *(const h4_t*)(st + v_rd[u][s2][0]);
+                const h4_t hi = *(const h4_t*)(st + v_rd[u][s2][1]);
+                const h8_t vf = cat8(lo, hi);
+                acc[0][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[0][s2], acc[0][u], 0, 0, 0);
+                acc[1][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[1][s2], acc[1][u], 0, 0, 0);
+            }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const float l_tot = add_xor32(add_xor16(l_run[j]));
+        if (query[j] < S) {
+            const float inv = 1.0f / l_tot;
+            _Float16* op = (_Float16*)a.o + (((size_t)b * S + query[j]) * a.H_q + h) * D;
+#pragma unroll
+            for (int u = 0; u < UT; u++) {
+                const h4_t ov = {(_Float16)(acc[j][u][0] * inv), (_Float16)(acc[j][u][1] * inv),
+                                 (_Float16)(acc[j][u][2] * inv), (_Float16)(acc[j][u][3] * inv)};
+                *(h4_t*)(op + 16 * u + 4 * lq) = ov;
+            }
+        }
+    }
+}
+
 __device__ __forceinline__ float to_f(float x) { return x; }
 __device__ __forceinline__ float to_f(_Float16 x) { return (float)x; }
 template <typename T> __device__ __forceinline__ T from_f(float x) { return (T)x; }
@@ -276,7 +475,11 @@ void flash_generic(cf_flash_args_t a) {
     }
 }
 
+int g_flash_no_dma = 0;   // tuning/test switch: 1 = use the register-staged d = 64 kernel
+
 }  // namespace
+
+extern "C" void cf_flash_set_dma(int32_t enable) { g_flash_no_dma = enable ? 0 : 1; }
 
 extern "C" int cf_launch_flash_attn(const cf_flash_args_t* a, void* stream) {
     hipStream_t s = (hipStream_t)stream;
@@ -288,7 +491,9 @@ extern "C" int cf_launch_flash_attn(const cf_flash_args_t* a, void* stream) {
         const long long groups = ((long long)a->B * a->H_q + 7) / 8;
         if (groups * nqb * 8 > 0x7fffffffLL) return (int)hipErrorInvalidValue;
         dim3 grid((unsigned)(groups * nqb * 8));
-        if (a->d == 64) hipLaunchKernelGGL(flash_f16<64>, grid, dim3(kThreads), 0, s, *a);
+        if (a->d == 64 && a->S % 8 == 0 && !g_flash_no_dma)
+            hipLaunchKernelGGL(flash_f16_dma64, grid, dim3(kThreads), 0, s, *a);
+        else if (a->d == 64) hipLaunchKernelGGL(flash_f16<64>, grid, dim3(kThreads), 0, s, *a);
         else hipLaunchKernelGGL(flash_f16<128>, grid, dim3(kThreads), 0, s, *a);
         return (int)hipGetLastError();
     }

@@ -315,7 +315,6 @@ void gemm_f16(cf_gemm_args_t a, Tiling t) {
 // makes the MFMA A reads (16 rows x one chunk) and the W transpose reads (4 rows x 32 B
 // per 16-lane group) hit distinct banks.
 constexpr int BKA = 32;
-constexpr int STAGES = 4;
 constexpr int A_ST = BM * BKA;          // halves per stage: A [128][32]
 constexpr int W_ST = BKA * BN;          //                   W [32][128]
 constexpr int ST = A_ST + W_ST;         // 16 KB per stage
@@ -323,8 +322,13 @@ constexpr int ST = A_ST + W_ST;         // 16 KB per stage
 __device__ __forceinline__ int swz_a(int row) { return (row >> 2) & 3; }
 __device__ __forceinline__ int swz_w(int row) { return ((row & 3) << 1) ^ (((row >> 3) & 1) << 3); }
 
+// STAGES = 4 (64 KB, two workgroups per CU) or 3 (48 KB, three per CU): the launcher
+// takes 3 when there are more tiles than two per CU, so that no tile waits for a
+// second round.
+template <int STAGES>
 __global__ __launch_bounds__(kThreads, 2)
 void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
+    static_assert(STAGES * ST * 2 >= 64 * LDCF * 4, "the epilogue reuses the ring");
     __shared__ __attribute__((aligned(16))) _Float16 smem[STAGES * ST];
 
     int tile_m, tile_n;
@@ -502,7 +506,11 @@ void gemm_f32(cf_gemm_args_t a, Tiling t) {
     store_tile<float>(a, seg, N, m0 + wm, n0 + wn, lr, lq, acc);
 }
 
+int g_gemm_stages = 0;   // tuning override of the direct-to-LDS kernel's ring depth (3, 4; 0 = automatic)
+
 }  // namespace
+
+extern "C" void cf_gemm_set_stages(int32_t stages) { g_gemm_stages = stages; }
 
 extern "C" int cf_launch_gemm(const cf_gemm_args_t* a, void* stream) {
     if (a->nseg < 1 || a->nseg > 3 || a->M <= 0 || a->K <= 0) return (int)hipErrorInvalidValue;
@@ -533,8 +541,12 @@ extern "C" int cf_launch_gemm(const cf_gemm_args_t* a, void* stream) {
     // Full tiles with aligned rows take the pipelined direct-to-LDS kernel.
     bool full = a->elem == CF_ELEM_F16 && t.epi_vec && a->M % BM == 0 && a->K % BKA == 0 && t.a_vec;
     for (int s = 0; s < a->nseg; s++) full = full && a->n[s] % BN == 0 && t.w_vec[s];
-    if (full)
-        hipLaunchKernelGGL(gemm_f16_async, grid, dim3(kThreads), 0, (hipStream_t)stream, *a, t);
+    int stages = blocks > 2LL * cu_count() ? 3 : 4;
+    if (g_gemm_stages == 3 || g_gemm_stages == 4) stages = g_gemm_stages;
+    if (full && stages == 3)
+        hipLaunchKernelGGL(gemm_f16_async<3>, grid, dim3(kThreads), 0, (hipStream_t)stream, *a, t);
+    else if (full)
+        hipLaunchKernelGGL(gemm_f16_async<4>, grid, dim3(kThreads), 0, (hipStream_t)stream, *a, t);
     else if (a->elem == CF_ELEM_F16)
         hipLaunchKernelGGL(gemm_f16, grid, dim3(kThreads), 0, (hipStream_t)stream, *a, t);
     else

@@ -369,18 +369,6 @@ void gemv_reduce(cf_gemv_args_t a, Tiles t) {
     }
 }
 
-int cu_count_cached() {
-    static int dev_cus[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (dev_cus[dev] <= 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        dev_cus[dev] = n;
-    }
-    return dev_cus[dev];
-}
-
 int g_dma_bn = 0;   // tuning override of the DMA path's tile width (0 = automatic)
 
 // Tile width of the DMA path, or 0 if it does not apply: 128 columns (measured best at
@@ -416,7 +404,7 @@ Tiles make_tiles(const cf_gemv_args_t* a) {
         const int per_cu = bn == 64 ? Dma<64>::PER_CU : bn == 128 ? Dma<128>::PER_CU : Dma<256>::PER_CU;
         const int m_tiles = (a->M + kMTile - 1) / kMTile;
         const int units = acc * m_tiles;
-        ks = (per_cu * cu_count_cached() + units - 1) / units;
+        ks = (per_cu * cu_count() + units - 1) / units;
         if (ks > a->K / kDK) ks = a->K / kDK;
         if (ks < 1) ks = 1;
     } else {

@@ -124,6 +124,9 @@ typedef struct {
 } cf_gemm_args_t;
 
 int cf_launch_gemm(const cf_gemm_args_t* a, void* stream);
+/* Tuning override of the fp16 direct-to-LDS GEMM's ring depth (3 or 4 stages; 0 =
+ * automatic: 3, i.e. three workgroups per CU, when there are more than two tiles per CU). */
+void cf_gemm_set_stages(int32_t stages);
 
 /* ---------------------------------------------------------------------------------
  * Prefill attention (flash style, online softmax): q (B, H_q, S, d), k (B, H_kv, S, d),
@@ -141,6 +144,9 @@ typedef struct {
 } cf_flash_args_t;
 
 int cf_launch_flash_attn(const cf_flash_args_t* a, void* stream);
+/* Selects the fp16 d = 64 prefill attention kernel: 1 (default) the DMA-ring kernel where
+ * it applies (S % 8 == 0), 0 the register-staged one (tuning and tests). */
+void cf_flash_set_dma(int32_t enable);
 
 /* CausalMask (S, S) float on the device. */
 int cf_launch_causal_mask(float* mask, int64_t S, void* stream);
