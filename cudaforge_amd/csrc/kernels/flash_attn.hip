@@ -10,7 +10,8 @@
 // fp16 path (d = 64 or 128): a workgroup owns 128 queries, 32 per wave (two 16-query
 // column blocks, so every K and V^T fragment read from LDS feeds two MFMAs).  Key blocks
 // of 64 are staged in LDS (K as [key][dim], V^T as [dim][key]) through a two-stage ring
-// whose next block is loaded into registers while the current one is used.  Each wave
+// whose next block is loaded into registers while the current one is used (for d = 64
+// and S % 8 == 0, flash_f16_dma64 streams the blocks by DMA instead, see there).  Each wave
 // computes S^T = K·Q^T with v_mfma_f32_16x16x32_f16, so a lane holds 16 scores of ONE
 // query per column block: the row max and row sum are lane-local plus a 4-lane exchange.
 // The probabilities are converted to fp16 in registers and fed back as the B operand of
@@ -237,16 +238,19 @@ constexpr float kLazy = 8.0f;
 
 __device__ __forceinline__ int fswz(int row) { return (row >> 1) & 7; }
 
+template <int NJ>
 __global__ __launch_bounds__(kThreads, 3)
 void flash_f16_dma64(cf_flash_args_t a) {
     constexpr int D = 64;
+    constexpr int QW = 16 * NJ;                   // queries per wave
+    constexpr int QB = 4 * QW;                    // queries per workgroup
     constexpr int KT = D / 32;                    // 32-dim steps of S^T
     constexpr int UT = D / 16;                    // 16-dim tiles of O^T
     constexpr int TILE = kKB * D;                 // halves per block per tensor (8 KB)
     constexpr int NS = kFlashStages;
     __shared__ __attribute__((aligned(16))) _Float16 ring[NS * 2 * TILE];
 
-    const int nqb = (a.S + kQB - 1) / kQB;
+    const int nqb = (a.S + QB - 1) / QB;
     const int HB = a.B * a.H_q;
     const int w = blockIdx.x, r8 = w & 7, rest = w >> 3;
     const int qi = rest % nqb, grp = rest / nqb;
@@ -256,10 +260,10 @@ void flash_f16_dma64(cf_flash_args_t a) {
     const int h = hb % a.H_q, b = hb / a.H_q;
     const int S = a.S;
     const int kvh = h / (a.H_q / a.H_kv);
-    const int q0 = qb * kQB;
+    const int q0 = qb * QB;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 15, lq = lane >> 4;
-    const int qw = q0 + 32 * wave;                 // first query of this wave
+    const int qw = q0 + QW * wave;                 // first query of this wave
 
     const _Float16* __restrict__ qp = (const _Float16*)a.q + (((size_t)b * a.H_q + h) * S) * D;
     const _Float16* __restrict__ kp = (const _Float16*)a.k + (((size_t)b * a.H_kv + kvh) * S) * D;
@@ -267,10 +271,10 @@ void flash_f16_dma64(cf_flash_args_t a) {
 
     // Q fragments first, waited for before the ring starts (the DMA loads are invisible
     // to the compiler's wait counting).
-    int query[2];
-    h8_t qf[2][KT];
+    int query[NJ];
+    h8_t qf[NJ][KT];
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < NJ; j++) {
         query[j] = qw + 16 * j + lr;
         const _Float16* qr = qp + (size_t)min(query[j], S - 1) * D + 8 * lq;
 #pragma unroll
@@ -319,14 +323,19 @@ void flash_f16_dma64(cf_flash_args_t a) {
             }
 
     const float c = a.scale * kLog2e;
-    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.0f, 0.0f};
-    f4_t acc[2][UT];
+    float m_run[NJ], l_run[NJ];
+    f4_t acc[NJ][UT];
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int j = 0; j < NJ; j++) {
+        m_run[j] = -INFINITY;
+        l_run[j] = 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; j++)
 #pragma unroll
         for (int u = 0; u < UT; u++) acc[j][u] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-    const int k_end = a.causal ? min(S, q0 + kQB) : S;
+    const int k_end = a.causal ? min(S, q0 + QB) : S;
     const int nblk = (k_end + kKB - 1) / kKB;
 #pragma unroll
     for (int st = 0; st < NS - 1; st++)
@@ -342,22 +351,23 @@ void flash_f16_dma64(cf_flash_args_t a) {
         const _Float16* st = ring + (bi % NS) * 2 * TILE;
 
         // S^T tiles: sc[j][t][i] = score(key k0 + 16t + 4*lq + i, query[j]).
-        f4_t sc[2][4];
+        f4_t sc[NJ][4];
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            sc[0][t] = f4_t{0.f, 0.f, 0.f, 0.f};
-            sc[1][t] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < NJ; j++) sc[j][t] = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kt = 0; kt < KT; kt++) {
                 const h8_t kf = *(const h8_t*)(st + k_rd[t][kt]);
-                sc[0][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[0][kt], sc[0][t], 0, 0, 0);
-                sc[1][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[1][kt], sc[1][t], 0, 0, 0);
+#pragma unroll
+                for (int j = 0; j < NJ; j++)
+                    sc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[j][kt], sc[j][t], 0, 0, 0);
             }
         }
         const bool edge = (k0 + kKB > S) || (a.causal && k0 + kKB - 1 > qw);
-        h8_t pf[2][2];
+        h8_t pf[NJ][2];
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < NJ; j++) {
             if (edge) {
 #pragma unroll
                 for (int t = 0; t < 4; t++)
@@ -402,12 +412,13 @@ void flash_f16_dma64(cf_flash_args_t a) {
                 const h4_t lo = *(const h4_t*)(st + v_rd[u][s2][0]);
                 const h4_t hi = *(const h4_t*)(st + v_rd[u][s2][1]);
                 const h8_t vf = cat8(lo, hi);
-                acc[0][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[0][s2], acc[0][u], 0, 0, 0);
-                acc[1][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[1][s2], acc[1][u], 0, 0, 0);
+#pragma unroll
+                for (int j = 0; j < NJ; j++)
+                    acc[j][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[j][s2], acc[j][u], 0, 0, 0);
             }
     }
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < NJ; j++) {
         const float l_tot = add_xor32(add_xor16(l_run[j]));
         if (query[j] < S) {
             const float inv = 1.0f / l_tot;
@@ -475,11 +486,13 @@ void flash_generic(cf_flash_args_t a) {
     }
 }
 
-int g_flash_no_dma = 0;   // tuning/test switch: 1 = use the register-staged d = 64 kernel
+// Tuning/test switch for fp16 d = 64: 0 register-staged kernel, 1 DMA kernel with 32
+// queries per wave, 2 DMA kernel with 16 per wave, 3 (default) DMA kernel, chosen by size.
+int g_flash_mode = 3;
 
 }  // namespace
 
-extern "C" void cf_flash_set_dma(int32_t enable) { g_flash_no_dma = enable ? 0 : 1; }
+extern "C" void cf_flash_set_mode(int32_t mode) { g_flash_mode = mode >= 0 && mode <= 3 ? mode : 3; }
 
 extern "C" int cf_launch_flash_attn(const cf_flash_args_t* a, void* stream) {
     hipStream_t s = (hipStream_t)stream;
@@ -491,9 +504,17 @@ extern "C" int cf_launch_flash_attn(const cf_flash_args_t* a, void* stream) {
         const long long groups = ((long long)a->B * a->H_q + 7) / 8;
         if (groups * nqb * 8 > 0x7fffffffLL) return (int)hipErrorInvalidValue;
         dim3 grid((unsigned)(groups * nqb * 8));
-        if (a->d == 64 && a->S % 8 == 0 && !g_flash_no_dma)
-            hipLaunchKernelGGL(flash_f16_dma64, grid, dim3(kThreads), 0, s, *a);
-        else if (a->d == 64) hipLaunchKernelGGL(flash_f16<64>, grid, dim3(kThreads), 0, s, *a);
+        if (a->d == 64 && a->S % 8 == 0 && g_flash_mode != 0) {
+            // 16 queries per wave (64 per workgroup) doubles the workgroups, and with
+            // them the waves per SIMD that hide each block's latency chain; 32 per wave
+            // halves the LDS traffic per query (every wave reads the whole K/V^T block),
+            // better once there are two 128-query workgroups per CU.
+            const int nj = g_flash_mode == 1 ? 2 : g_flash_mode == 2 ? 1 : (groups * nqb * 8 < 2LL * cu_count() ? 1 : 2);
+            const long long nqb2 = (a->S + 64 * nj - 1) / (64 * nj);
+            dim3 grid2((unsigned)(groups * nqb2 * 8));
+            if (nj == 1) hipLaunchKernelGGL(flash_f16_dma64<1>, grid2, dim3(kThreads), 0, s, *a);
+            else hipLaunchKernelGGL(flash_f16_dma64<2>, grid2, dim3(kThreads), 0, s, *a);
+        } else if (a->d == 64) hipLaunchKernelGGL(flash_f16<64>, grid, dim3(kThreads), 0, s, *a);
         else hipLaunchKernelGGL(flash_f16<128>, grid, dim3(kThreads), 0, s, *a);
         return (int)hipGetLastError();
     }

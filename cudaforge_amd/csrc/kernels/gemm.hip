@@ -12,10 +12,11 @@
 //       k of one column per lane; it comes from W[k][n] with two ds_read_b64_tr_b16
 //       (gfx950 LDS transpose reads): in each 16-lane group, lane j addresses
 //       W[kb + j/4][nb + 4(j%4)] and lane i receives W[kb..kb+3][nb + i].
-//       Full tiles use a 4-stage ring filled by global_load_lds_dwordx4 (three k-tiles in
-//       flight, no VGPR staging); edge shapes use a 2-stage register-staged kernel.
-//       The output tile goes through LDS so stores are 16 bytes along the destination's
-//       contiguous direction.
+//       Full tiles use a 3- or 4-stage ring filled by global_load_lds_dwordx4 (no VGPR
+//       staging; 3 stages, i.e. three workgroups per CU, when there are more tiles than
+//       two per CU); edge shapes use a 2-stage register-staged kernel.  The output tile
+//       goes through LDS (fp16 in one pass without a residual, fp32 in two with one) so
+//       stores are 16 bytes along the destination's contiguous direction.
 // fp32: 128x128x16 tile with v_mfma_f32_16x16x4_f32, both tiles staged k-major so each
 //       operand is one conflict-free ds_read_b32 (the FP32 operator's parity path).
 // Tile edges are zero-filled on load and masked on store.
@@ -188,6 +189,47 @@ __device__ __forceinline__ void epilogue_f16(const cf_gemm_args_t& a, int seg, i
     }
 }
 
+// Epilogue without a residual (the QKV projection): bias is added in registers and the
+// sum rounded to fp16 once, exactly as the fp32 path rounds it, so the whole 128 x BN
+// tile fits LDS as fp16 and goes out in a single pass.  `Cs` must hold 128 x LDCH
+// halves and be free (after a barrier).
+constexpr int LDCH = BN + 8;
+__device__ __forceinline__ void epilogue_f16_nores(const cf_gemm_args_t& a, int seg, int N, int m0, int n0, int wm,
+                                                   int wn, int lr, int lq, int tid, const f4_t (&acc)[4][4],
+                                                   _Float16* Cs) {
+    const _Float16* __restrict__ bias = (const _Float16*)a.bias[seg];
+    _Float16* __restrict__ out = (_Float16*)a.out[seg];
+    const bool along_n = a.out_kind == CF_GEMM_OUT_ROWMAJOR || seg < 2;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int nl = wn + 16 * j + lr;
+        const float bv = (bias && n0 + nl < N) ? (float)bias[n0 + nl] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) Cs[(wm + 16 * i + 4 * lq + e) * LDCH + nl] = (_Float16)(acc[i][j][e] + bv);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < (BM * BN / 8) / kThreads; it++) {
+        const int ch = tid + it * kThreads;
+        if (along_n) {
+            const int r = ch >> 4, c8 = (ch & 15) * 8;
+            const int m = m0 + r, n = n0 + c8;
+            if (m >= a.M || n >= N) continue;
+            *(h8_t*)(out + row_part(a, seg, m) + col_part(a, seg, n)) = *(const h8_t*)&Cs[r * LDCH + c8];
+        } else {
+            const int col = ch & (BN - 1), r8 = (ch / BN) * 8;
+            const int m = m0 + r8, n = n0 + col;
+            if (m >= a.M || n >= N) continue;
+            h8_t v;
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = Cs[(r8 + e) * LDCH + col];
+            *(h8_t*)(out + row_part(a, seg, m) + col_part(a, seg, n)) = v;
+        }
+    }
+}
+
 // MFMA B operand (8 consecutive k of one column) from a W tile stored [k][n] in LDS:
 // two ds_read_b64_tr_b16.  p points at W[kb + lr/4][nb + 4*(lr%4)] of the caller's
 // lane; the second read is 4 rows further.
@@ -328,7 +370,7 @@ __device__ __forceinline__ int swz_w(int row) { return ((row & 3) << 1) ^ (((row
 template <int STAGES>
 __global__ __launch_bounds__(kThreads, 2)
 void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
-    static_assert(STAGES * ST * 2 >= 64 * LDCF * 4, "the epilogue reuses the ring");
+    static_assert(STAGES * ST * 2 >= 64 * LDCF * 4 && STAGES * ST >= BM * LDCH, "the epilogue reuses the ring");
     __shared__ __attribute__((aligned(16))) _Float16 smem[STAGES * ST];
 
     int tile_m, tile_n;
@@ -418,7 +460,10 @@ void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
     }
     wait_vm<0>();
     __syncthreads();
-    epilogue_f16(a, seg, N, m0, n0, wm, wn, lr, lq, tid, acc, (float*)smem);
+    if (a.residual == nullptr || a.out_kind != CF_GEMM_OUT_ROWMAJOR)
+        epilogue_f16_nores(a, seg, N, m0, n0, wm, wn, lr, lq, tid, acc, smem);
+    else
+        epilogue_f16(a, seg, N, m0, n0, wm, wn, lr, lq, tid, acc, (float*)smem);
 }
 
 // ------------------------------------------------------------------------- fp32 ---

@@ -144,9 +144,10 @@ typedef struct {
 } cf_flash_args_t;
 
 int cf_launch_flash_attn(const cf_flash_args_t* a, void* stream);
-/* Selects the fp16 d = 64 prefill attention kernel: 1 (default) the DMA-ring kernel where
- * it applies (S % 8 == 0), 0 the register-staged one (tuning and tests). */
-void cf_flash_set_dma(int32_t enable);
+/* Selects the fp16 d = 64 prefill attention kernel (tuning and tests): 0 the register-
+ * staged kernel, 1 / 2 the DMA-ring kernel with 32 / 16 queries per wave, 3 (default)
+ * the DMA-ring kernel where it applies (S % 8 == 0) with the width chosen by size. */
+void cf_flash_set_mode(int32_t mode);
 
 /* CausalMask (S, S) float on the device. */
 int cf_launch_causal_mask(float* mask, int64_t S, void* stream);

@@ -129,18 +129,19 @@ def test_graph_fused_on_gpu(gpu, native, f16):
 
 
 @pytest.mark.parametrize("causal", [False, True])
-def test_flash_dma_and_register_paths_agree(gpu, native, causal):
-    """The two fp16 d = 64 attention kernels (DMA ring, register staged) on a GQA shape
-    whose length is a multiple of 8 but not of the 64-key block: both within the FP16
-    bound of the oracle and close to each other."""
+def test_flash_kernel_variants_agree(gpu, native, causal):
+    """The fp16 d = 64 attention kernels (register staged; DMA ring with 32 or 16 queries
+    per wave) on a GQA shape whose length is a multiple of 8 but not of the 64-key
+    block: each within the FP16 bound of the oracle and close to the others."""
     c = FusedCase(2, 264, 8, 2, 64, seed=71, f16=True, causal=causal, residual=True, bias_std=0.02)
     want = c.oracle()
+    outs = []
     try:
-        native.cf_flash_set_dma(0)
-        reg = run_fused_gpu(c)
+        for mode in (0, 1, 2, 3):
+            native.cf_flash_set_mode(mode)
+            outs.append(run_fused_gpu(c))
     finally:
-        native.cf_flash_set_dma(1)
-    dma = run_fused_gpu(c)
-    assert max_abs(want, dma) <= TOL16
-    assert max_abs(want, reg) <= TOL16
-    assert max_abs(dma, reg) <= 1e-2
+        native.cf_flash_set_mode(3)
+    for o in outs:
+        assert max_abs(want, o) <= TOL16
+        assert max_abs(outs[0], o) <= 1e-2
