@@ -100,6 +100,7 @@ def _proto(lib):
         # decode planning knobs
         "mha_decode_set_split_chunk": (None, [c_int64]),
         "cf_gemv_set_dma_tile": (None, [c_int32]),
+        "cf_gemv_set_dma_ksplit": (None, [c_int32]),
         "cf_decode_attn_set_stages": (None, [c_int32]),
         "cf_gemm_set_stages": (None, [c_int32]),
         "cf_flash_set_mode": (None, [c_int32]),

@@ -5,23 +5,21 @@
 //
 // 1. split kernel, grid = (split, kv head, batch row).  A workgroup streams one `chunk`
 //    of positions of one (b, kv head) and serves the whole GQA group of G query heads
-//    (kv head = h / G, mha_decode.c:77) from a single read of every K and V row.
-//    Inside a split the softmax is exact and two-pass over LDS-resident scores:
-//      pass 1 streams K and stores s = q·k · scale·log2(e) (and its max),
-//      pass 2 streams V with p = 2^(s - m)  -> partial (m, l = Σp, acc = Σ p·v).
-//    fp16 (d = 64/128): one wave per workgroup.  Q·K^T runs on the matrix cores as
-//      S^T(16 positions x 16 heads) = K(16 x 32 dims) · Q^T(32 dims x 16 heads) with
-//      v_mfma_f32_16x16x32_f16, so a lane ends up holding 4 positions of ONE head and
-//      no cross-lane reduction is needed; the K tile loads are double-buffered.  P·V is
-//      on the VALU: a lane owns 8 dims of one V row and accumulates all G heads.
-//    fp32 (d = 64/128): four waves, lanes own 4 dims of a row, dot products reduced
-//      across the row's lanes.
+//    (kv head = h / G, mha_decode.c:77) from a single read of every K and V row, and
+//    writes a partial (m, l = sum p, acc = sum p*v) in the log2 domain.
+//    fp16 (d = 64/128, G = 1/2/4/8): one wave per workgroup, single pass with an online
+//      softmax over 32-position blocks that arrive by DMA in an LDS ring; both products
+//      on the matrix cores (see split_f16).
+//    fp32 (d = 64/128): four waves, two passes over LDS-resident scores (pass 1 streams
+//      K and stores s = q.k * scale*log2(e), pass 2 streams V with p = 2^(s - m)); lanes
+//      own 4 dims of a row and dot products are reduced across the row's lanes.
 //    Other head or group sizes: a generic kernel, one query head per workgroup.
-// 2. merge kernel, one thread per output element: the log-sum-exp combine
-//      O = Σ_s 2^(m_s - M)·acc_s / Σ_s 2^(m_s - M)·l_s
+// 2. merge kernel: the log-sum-exp combine
+//      O = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s
 //    (the reference's split/merge formula, mha_fused_cuda.cu:847-863 and :895-931,
-//    restated per (b, head) with the head index it lacked).  A sequence that fits in
-//    one split is finished by the split kernel and skipped here.
+//    restated per (b, head) with the head index it lacked); one workgroup per output
+//    row (merge_rows), or one thread per element when d % 4 != 0.  A sequence that fits
+//    in one split is finished by the split kernel and skipped here.
 // No fences or atomics: the kernel boundary orders the partials, which matters on
 // MI355X where each XCD has its own L2.
 

@@ -370,6 +370,7 @@ void gemv_reduce(cf_gemv_args_t a, Tiles t) {
 }
 
 int g_dma_bn = 0;   // tuning override of the DMA path's tile width (0 = automatic)
+int g_dma_ks = 0;   // tuning override of the DMA path's K split (0 = automatic)
 
 // Tile width of the DMA path, or 0 if it does not apply: 128 columns (measured best at
 // the decode shapes; 64 and 256 ran 5-15 % slower), else the widest that divides every
@@ -384,6 +385,40 @@ int dma_bn(const cf_gemv_args_t* a) {
     if (bn < 64) return 0;
     if (g_dma_bn >= 64 && g_dma_bn <= bn) bn = g_dma_bn;
     return bn;
+}
+
+// Reduce for the DMA path (tile widths are multiples of 64): a thread owns 4 adjacent
+// columns of one row and issues all of its K-chunk loads (16-byte) before summing, so
+// the whole reduction is one round trip to memory.
+__global__ __launch_bounds__(256)
+void gemv_reduce4(cf_gemv_args_t a, Tiles t) {
+    constexpr int MAXKS = 32;
+    const int ncols = t.start[a.nseg] * t.bn;
+    const int Mp = (a.M + kMTile - 1) / kMTile * kMTile;
+    const size_t plane = (size_t)Mp * ncols;
+    const size_t total = (size_t)a.M * (ncols / 4);
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= total) return;
+    const int m = (int)(idx / (ncols / 4));
+    const int col = (int)(idx - (size_t)m * (ncols / 4)) * 4;
+    const float* p = a.partials + (size_t)m * ncols + col;
+    f4_t v[MAXKS];
+#pragma unroll
+    for (int k = 0; k < MAXKS; k++)
+        if (k < a.k_split) v[k] = *(const f4_t*)(p + (size_t)k * plane);
+    f4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < MAXKS; k += 2) {
+        if (k < a.k_split) s0 += v[k];
+        if (k + 1 < a.k_split) s1 += v[k + 1];
+    }
+    s0 += s1;
+    const int tile = col / t.bn;
+    const int seg = seg_of(a, t, tile);
+    const int n = (tile - t.start[seg]) * t.bn + (col - tile * t.bn);
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        if (n + e < a.seg[seg].n) store_out<_Float16>(a, a.seg[seg], m, n + e, s0[e]);
 }
 
 Tiles make_tiles(const cf_gemv_args_t* a) {
@@ -406,6 +441,8 @@ Tiles make_tiles(const cf_gemv_args_t* a) {
         const int units = acc * m_tiles;
         ks = (per_cu * cu_count() + units - 1) / units;
         if (ks > a->K / kDK) ks = a->K / kDK;
+        if (g_dma_ks > 0) ks = g_dma_ks;
+        if (ks > 32) ks = 32;                 // gemv_reduce4 keeps all chunks in flight
         if (ks < 1) ks = 1;
     } else {
         ks = a->k_split > 0 ? a->k_split : 1;
@@ -426,6 +463,7 @@ Tiles make_tiles(const cf_gemv_args_t* a) {
 
 extern "C" int32_t cf_gemv_col_tile(int32_t elem) { (void)elem; return kColTile; }
 extern "C" void cf_gemv_set_dma_tile(int32_t bn) { g_dma_bn = bn; }
+extern "C" void cf_gemv_set_dma_ksplit(int32_t ks) { g_dma_ks = ks; }
 extern "C" int32_t cf_gemv_k_step(int32_t elem) {
     return elem == CF_ELEM_F16 ? Cfg<_Float16>::KSTEP : Cfg<float>::KSTEP;
 }
@@ -457,6 +495,11 @@ extern "C" int cf_launch_gemv(const cf_gemv_args_t* a, void* stream) {
         hipLaunchKernelGGL(gemv_kernel<float>, grid, dim3(kThreads), 0, s, args, t);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || t.ks == 1) return (int)e;
+    if (t.dma) {
+        const size_t total4 = (size_t)a->M * t.start[a->nseg] * t.bn / 4;
+        hipLaunchKernelGGL(gemv_reduce4, dim3((unsigned)((total4 + 255) / 256)), dim3(256), 0, s, args, t);
+        return (int)hipGetLastError();
+    }
     const size_t total = (size_t)a->M * t.start[a->nseg] * t.bn;
     size_t blocks = (total + 255) / 256;
     if (blocks > 4096) blocks = 4096;

@@ -97,6 +97,8 @@ int     cf_launch_gemv(const cf_gemv_args_t* a, void* stream);
 /* Tuning override of the fp16 DMA path's column-tile width (64, 128 or 256; 0 =
  * automatic: 128 where it divides every segment, else 64). */
 void    cf_gemv_set_dma_tile(int32_t bn);
+/* Tuning override of the fp16 DMA path's K split (1..32; 0 = automatic). */
+void    cf_gemv_set_dma_ksplit(int32_t ks);
 
 /* ---------------------------------------------------------------------------------
  * Prefill GEMM with fused epilogue: C = A·W + bias (+ residual), A (M, K) row-major,
