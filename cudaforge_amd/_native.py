@@ -82,6 +82,7 @@ def _proto(lib):
         "gpu_event_synchronize": (c_int, [c_void_p]),
         "gpu_event_elapsed_ms": (c_int, [POINTER(c_float), c_void_p, c_void_p]),
         "gpu_workspace_get": (c_void_p, [c_size_t]),
+        "gpu_workspace_get_stream": (c_void_p, [c_void_p, c_size_t]),
         "gpu_workspace_size": (c_size_t, []),
         "gpu_workspace_release": (None, []),
         "gpu_inject_alloc_failures": (None, [c_int]),

@@ -109,7 +109,7 @@ static size_t attn_args(int elem, const decode_shape_t* s, const int32_t* lens,
 }
 
 static int attn_prepare(int elem, const void* inputs[], void* outputs[],
-                        const operator_params_t* params, cf_decode_attn_args_t* a) {
+                        const operator_params_t* params, void* stream, cf_decode_attn_args_t* a) {
     if (!params || !inputs || !outputs) return -1;
     const mha_decode_params_t* p = (const mha_decode_params_t*)params;
     decode_shape_t s;
@@ -122,7 +122,7 @@ static int attn_prepare(int elem, const void* inputs[], void* outputs[],
         if (!lens) return -1;
     }
     const size_t part_bytes = attn_args(elem, &s, lens, a);
-    char* ws = (char*)gpu_workspace_get(part_bytes);
+    char* ws = (char*)gpu_workspace_get_stream(stream, part_bytes);
     if (!ws) return -1;
     a->partials = (float*)ws;
     a->q = inputs[0];
@@ -143,7 +143,8 @@ int mha_decode_attn_kernel_times(const void* const* input_sets, int n_inputs, in
     const int elem = elem_f16 ? CF_ELEM_F16 : CF_ELEM_F32;
     cf_decode_attn_args_t a[16];
     for (int s = 0; s < n_sets; s++) {
-        const int rc = attn_prepare(elem, (const void**)&input_sets[s * n_inputs], outputs, params, &a[s]);
+        const int rc = attn_prepare(elem, (const void**)&input_sets[s * n_inputs], outputs, params,
+                                    cf_stream_of(stream), &a[s]);
         if (rc != 0) return rc;
     }
     void* st = cf_stream_of(stream);
@@ -173,7 +174,7 @@ int mha_decode_attn_kernel_times(const void* const* input_sets, int n_inputs, in
 static int attn_core(int elem, const void* inputs[], void* outputs[],
                      const operator_params_t* params, stream_t* stream) {
     cf_decode_attn_args_t a;
-    const int rc = attn_prepare(elem, inputs, outputs, params, &a);
+    const int rc = attn_prepare(elem, inputs, outputs, params, cf_stream_of(stream), &a);
     if (rc != 0) return rc;
     return cf_launch_decode_attn(&a, cf_stream_of(stream));
 }
@@ -265,7 +266,7 @@ static int decode_op(int elem, const void* inputs[], void* outputs[],
     const size_t off_p1 = cf_ws_take(&cur, cf_gemv_partials_floats(&g1) * sizeof(float));
     const size_t off_pa = cf_ws_take(&cur, attn_part);
     const size_t off_p2 = cf_ws_take(&cur, cf_gemv_partials_floats(&g2) * sizeof(float));
-    char* data = (char*)gpu_workspace_get(cur);
+    char* data = (char*)gpu_workspace_get_stream(st, cur);
     if (!data) return -1;
 
     g1.seg[0].out = data + off_q;

@@ -38,7 +38,7 @@ static int fused_op(int elem, const void* inputs[], void* outputs[],
     const size_t off_k = cf_ws_take(&cur, (size_t)(B * S * kvd) * esz);
     const size_t off_v = cf_ws_take(&cur, (size_t)(B * S * kvd) * esz);
     const size_t off_o = cf_ws_take(&cur, (size_t)(B * S * D) * esz);
-    char* data = (char*)gpu_workspace_get(cur);
+    char* data = (char*)gpu_workspace_get_stream(st, cur);
     if (!data) return -1;
 
     cf_gemm_args_t g;

@@ -15,12 +15,19 @@ namespace {
 
 constexpr int kMaxDevices = 16;
 
+// One workspace per (device, stream): operators on different streams may run at the
+// same time, so each stream gets its own scratch.  kWsSlots streams per device; a new
+// stream beyond that takes over the least recently used slot (after a device sync).
+constexpr int kWsSlots = 16;
 struct Workspace {
-    void*  base = nullptr;
-    size_t bytes = 0;
+    void*         base = nullptr;
+    size_t        bytes = 0;
+    hipStream_t   stream = nullptr;
+    bool          used = false;
+    unsigned long last = 0;
 };
-
-Workspace g_ws[kMaxDevices];
+Workspace g_ws[kMaxDevices][kWsSlots];
+unsigned long g_ws_clock = 0;
 int g_inject_failures = 0;
 int g_initialized_device = -1;
 
@@ -195,43 +202,64 @@ int gpu_event_elapsed_ms(float* ms, gpu_event_t start, gpu_event_t stop) {
     return rc(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
 }
 
-void* gpu_workspace_get(size_t bytes) {
+void* gpu_workspace_get_stream(gpu_stream_t stream, size_t bytes) {
     const int dev = current_device();
     if (dev < 0 || dev >= kMaxDevices) return nullptr;
-    Workspace& ws = g_ws[dev];
+    hipStream_t st = (hipStream_t)stream;
+    Workspace* slot = nullptr;
+    for (int i = 0; i < kWsSlots && !slot; i++)
+        if (g_ws[dev][i].used && g_ws[dev][i].stream == st) slot = &g_ws[dev][i];
+    for (int i = 0; i < kWsSlots && !slot; i++)
+        if (!g_ws[dev][i].used) slot = &g_ws[dev][i];
+    if (!slot) {
+        slot = &g_ws[dev][0];
+        for (int i = 1; i < kWsSlots; i++)
+            if (g_ws[dev][i].last < slot->last) slot = &g_ws[dev][i];
+        (void)hipDeviceSynchronize();   // its previous stream may still be using it
+    }
+    slot->used = true;
+    slot->stream = st;
+    slot->last = ++g_ws_clock;
     const size_t need = ((bytes + 255) / 256) * 256;
-    if (ws.base && ws.bytes >= need) return ws.base;
+    if (slot->base && slot->bytes >= need) return slot->base;
     // Grow: in-flight kernels may still use the old buffer.
-    if (ws.base) {
+    if (slot->base) {
         (void)hipDeviceSynchronize();
-        (void)hipFree(ws.base);
-        ws.base = nullptr;
-        ws.bytes = 0;
+        (void)hipFree(slot->base);
+        slot->base = nullptr;
+        slot->bytes = 0;
     }
     size_t grow = need < (size_t)64 << 20 ? (size_t)64 << 20 : need + need / 4;
     void* p = gpu_device_alloc(grow);
     if (!p) return nullptr;
-    ws.base = p;
-    ws.bytes = grow;
+    slot->base = p;
+    slot->bytes = grow;
     return p;
 }
 
+void* gpu_workspace_get(size_t bytes) { return gpu_workspace_get_stream(nullptr, bytes); }
+
 size_t gpu_workspace_size(void) {
     const int dev = current_device();
-    return (dev >= 0 && dev < kMaxDevices) ? g_ws[dev].bytes : 0;
+    if (dev < 0 || dev >= kMaxDevices) return 0;
+    size_t total = 0;
+    for (int i = 0; i < kWsSlots; i++) total += g_ws[dev][i].bytes;
+    return total;
 }
 
 void gpu_workspace_release(void) {
     for (int d = 0; d < kMaxDevices; d++) {
-        if (g_ws[d].base) {
-            int prev = current_device();
-            (void)hipSetDevice(d);
-            (void)hipDeviceSynchronize();
-            (void)hipFree(g_ws[d].base);
-            (void)hipSetDevice(prev);
-            g_ws[d].base = nullptr;
-            g_ws[d].bytes = 0;
+        bool any = false;
+        for (int i = 0; i < kWsSlots; i++) any = any || g_ws[d][i].base;
+        if (!any) continue;
+        int prev = current_device();
+        (void)hipSetDevice(d);
+        (void)hipDeviceSynchronize();
+        for (int i = 0; i < kWsSlots; i++) {
+            if (g_ws[d][i].base) (void)hipFree(g_ws[d][i].base);
+            g_ws[d][i] = Workspace{};
         }
+        (void)hipSetDevice(prev);
     }
 }
 

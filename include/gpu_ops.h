@@ -98,13 +98,18 @@ int   gpu_event_record(gpu_event_t ev, gpu_stream_t stream);
 int   gpu_event_synchronize(gpu_event_t ev);
 int   gpu_event_elapsed_ms(float* ms, gpu_event_t start, gpu_event_t stop);
 
-/* Persistent scratch of the current device for split partials and projections.
- * Returns a 256-byte aligned device buffer of at least `bytes` bytes.  The buffer grows
- * (one synchronous reallocation, never during a launch sequence) when a larger size is
- * requested and is otherwise reused: operators that share it must be ordered on one
- * stream.  Returns NULL on allocation failure. */
+/* Persistent scratch for split partials and projections, one per (current device,
+ * stream): returns a 256-byte aligned device buffer of at least `bytes` bytes that only
+ * work on `stream` uses, so operators on different streams may run concurrently.  It
+ * grows (one synchronous reallocation) when a larger size is requested and is otherwise
+ * reused; work on one stream is ordered, so successive operators there may share it.
+ * Up to 16 streams per device keep their own buffer; a further stream takes over the
+ * least recently used one after a device synchronisation.  Not thread-safe (like the
+ * operator registry): one host thread drives a device.  NULL on allocation failure.
+ * gpu_workspace_get(bytes) is the default stream's buffer. */
+void*  gpu_workspace_get_stream(gpu_stream_t stream, size_t bytes);
 void*  gpu_workspace_get(size_t bytes);
-size_t gpu_workspace_size(void);
+size_t gpu_workspace_size(void);     /* bytes held on the current device, all streams */
 void   gpu_workspace_release(void);
 
 /* Allocation-failure injection for error-path tests: the next `n` device allocations

@@ -334,3 +334,32 @@ def test_split_ring_depths(gpu, native, stages):
         native.cf_decode_attn_set_stages(0)
     want = O.decode_attn(Q, K, V, lens + 1, float(1 / np.sqrt(d)), H_kv)
     assert max_abs(want, got) <= TOL16
+
+
+def test_concurrent_streams_have_separate_scratch(gpu):
+    """Two decode cores on two streams at once (each splits its KV and merges through
+    scratch memory) give the same bits as the same calls one after the other."""
+    import cudaforge_amd as cf
+    from helpers import dev
+    B, H, H_kv, d, T = 16, 32, 8, 128, 4096
+    sets = []
+    for i in range(2):
+        Q = O.round_f16(O.normal((B, H, d), 500 + i))
+        K = O.round_f16(O.normal((B, T, H_kv, d), 510 + i))
+        V = O.round_f16(O.normal((B, T, H_kv, d), 520 + i))
+        sets.append([dev(Q, True), dev(K, True), dev(V, True)])
+    p = cf.MhaDecodeParams(B, H * d, H, H_kv, d, float(1 / np.sqrt(d)), T - 1, T)
+    seq = []
+    for ins in sets:
+        out = cf.DeviceBuffer.empty((B, H, d), np.float16)
+        assert cf.call_op("mha_decode_attn_f16_cuda", ins, [out], p) == 0
+        seq.append(out.download())
+    streams = [cf.Stream(), cf.Stream()]
+    outs = [cf.DeviceBuffer.empty((B, H, d), np.float16) for _ in range(2)]
+    for _ in range(3):
+        for ins, out, st in zip(sets, outs, streams):
+            assert cf.call_op("mha_decode_attn_f16_cuda", ins, [out], p, st) == 0
+    for st in streams:
+        st.synchronize()
+    for out, want in zip(outs, seq):
+        assert np.array_equal(out.download(), want)
