@@ -148,6 +148,59 @@ def bench_decode_ragged(cf, stream, steps, warmup):
     return ms, alg, [int(x) + 1 for x in lens]
 
 
+def bench_decode_graph(cf, steps, warmup, B=16, H=32, H_kv=8, d=128, T=4096, seed=700):
+    """Config-2 decode through the graph executor, the host-buffer boundary: each step
+    copies X_new host->device, runs the MHA_Decode node against device-resident in-place
+    KV caches (graph_set_kv_cache), synchronises and copies Y back (graph.c:670-1115 is
+    the reference executor).  Host wall-clock per step, PCIe transfers included."""
+    import ctypes
+    from ctypes import POINTER, c_int, c_int64, c_void_p
+    import oracle as O
+    lib = cf.load_library()
+    D, kvd = H * d, H_kv * d
+    g = lib.graph_create()
+
+    def tensor(arr):
+        arr = np.ascontiguousarray(arr)
+        shape = (c_int64 * arr.ndim)(*arr.shape)
+        t = lib.tensor_create(1, arr.ndim, shape)                 # DTYPE_F16
+        tt = ctypes.cast(t, POINTER(cf.TensorT)).contents
+        ctypes.memmove(tt.data, arr.ctypes.data, arr.nbytes)
+        return t, lib.graph_add_tensor(g, t)
+
+    mk = (lambda shape, s, std=1.0: O.to_f16(O.normal(shape, seed + s, 0.0, std)))
+    tX, iX = tensor(mk((B, 1, D), 1))
+    _, iK = tensor(mk((B, T, H_kv, d), 2))
+    _, iV = tensor(mk((B, T, H_kv, d), 3))
+    tY, iY = tensor(np.zeros((B, 1, D), np.float16))
+    ws = [tensor(w)[0] for w in (mk((D, D), 4, 0.02), np.zeros(D, np.float16), mk((D, kvd), 6, 0.02),
+                                 np.zeros(kvd, np.float16), mk((D, kvd), 8, 0.02), np.zeros(kvd, np.float16),
+                                 mk((D, D), 10, 0.02), np.zeros(D, np.float16))]
+    cl0 = T - 1 - (warmup + steps)
+    p = cf.MhaDecodeParams(B, D, H, H_kv, d, float(1 / np.sqrt(d)), cl0, T)
+    node = lib.graph_add_node(g, 29, 3, (c_int * 3)(iX, iK, iV), 3, (c_int * 3)(iY, iK, iV), 8,
+                              (c_void_p * 8)(*ws), ctypes.addressof(p), ctypes.sizeof(p))
+    if node < 0:
+        raise RuntimeError("graph_add_node failed")
+    lib.graph_set_input(g, lib.graph_add_node(g, 36, 0, None, 1, (c_int * 1)(iX), 0, None, None, 0))
+    lib.graph_set_output(g, lib.graph_add_node(g, 37, 1, (c_int * 1)(iY), 0, None, 0, None, None, 0))
+    lib.graph_set_kv_cache(g, iK, iV)
+    if lib.graph_build(g) != 0:
+        raise RuntimeError("graph_build failed")
+    ins, outs = (c_void_p * 1)(tX), (c_void_p * 1)(tY)
+    t_start, cl = None, cl0
+    for i in range(warmup + steps):
+        if i == warmup:
+            t_start = time.perf_counter()
+        lib.graph_update_cache_len(g, cl)
+        if lib.graph_execute(g, ins, outs, True) != 0:
+            raise RuntimeError("graph_execute failed")
+        cl += 1
+    ms = (time.perf_counter() - t_start) * 1e3 / steps
+    lib.graph_destroy(g)
+    return ms
+
+
 def bench_fused(cf, stream, steps, warmup, B, S, H, d, causal, seed):
     D = H * d
     mk = (lambda shape, s, std=1.0: cf.DeviceBuffer.from_numpy(f16_normal(shape, seed + s, std)))
@@ -257,6 +310,12 @@ def main() -> int:
                                                "GB_s": round(alg_f / (ms_f * 1e-3) / 1e9, 1),
                                                "alg_bytes": alg_f}
         log(f"  {ms_f * 1e3:.2f} us/step")
+        log("decode through graph_execute, config 2 (host X/Y)")
+        ms_g = bench_decode_graph(cf, 50, 5)
+        extra["decode_graph_config2_f16"] = {"us_per_step": round(ms_g * 1e3, 2),
+                                             "note": "graph_execute per step: X_new H2D + op + sync + Y D2H, "
+                                                     "host wall-clock, KV caches device-resident"}
+        log(f"  {ms_g * 1e3:.2f} us/step")
         log("decode full op, config 1 (fp32)")
         ms_1, alg_1 = bench_decode_full(cf, stream, steps, warmup, f16=False, B=1, H=12, H_kv=12, d=64, T=1024)
         extra["decode_full_op_config1_f32"] = {"us_per_step": round(ms_1 * 1e3, 2),
