@@ -91,8 +91,12 @@ def test_attn_core_vs_oracle(gpu, f16, H, H_kv, d, T):
 
 
 @pytest.mark.parametrize("B,H,H_kv,d,max_seq,cl", [(4, 8, 2, 64, 300, 257), (2, 32, 8, 128, 520, 511),
-                                                   (20, 4, 4, 64, 70, 0), (3, 12, 12, 64, 600, 599)])
+                                                   (20, 4, 4, 64, 70, 0), (3, 12, 12, 64, 600, 599),
+                                                   (2, 6, 2, 16, 50, 33), (17, 4, 4, 32, 64, 63)])
 def test_full_decode_f16(gpu, B, H, H_kv, d, max_seq, cl):
+    """Full op in fp16.  The last two shapes have projection widths that are not
+    multiples of 64 (register-transposing projection kernel), a head size off the MFMA
+    split path (generic split kernel) and more than 16 batch rows (two M tiles)."""
     c = DecodeCase(B, H, H_kv, d, max_seq, cache_len=cl, seed=B + H, f16=True)
     want = c.oracle()
     got = run_decode_gpu(c)
