@@ -262,6 +262,46 @@ def read_traffic(kernel_prefix: str):
         return None
 
 
+def vendor_comparison(reps: int = 50) -> dict:
+    """The same prefill shapes through the vendor libraries, for context only (not the
+    product path): torch.matmul on fp16 (hipBLASLt on ROCm) for the plain projection
+    products, and torch's scaled_dot_product_attention for the attention.  Events on
+    torch's current stream."""
+    import torch
+    import torch.nn.functional as F
+    dev = "cuda"
+    out = {}
+
+    def timed(fn, n):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / n
+
+    g = torch.Generator(device=dev).manual_seed(0)
+    for name, (M, K, N) in {"config3_qkv": (4096, 768, 2304), "config3_wo": (4096, 768, 768),
+                            "config5_qkv": (4096, 1024, 3072), "config5_wo": (4096, 1024, 1024)}.items():
+        a = torch.randn(M, K, device=dev, dtype=torch.float16, generator=g)
+        w = torch.randn(K, N, device=dev, dtype=torch.float16, generator=g)
+        us = timed(lambda: a @ w, reps)
+        out[f"matmul_{name}"] = {"M": M, "K": K, "N": N, "us": round(us, 2),
+                                 "TFLOP_s": round(2 * M * N * K / us / 1e6, 1)}
+    for name, (B, H, S, d, causal) in {"config3": (8, 12, 512, 64, False),
+                                       "config5": (4, 16, 1024, 64, True)}.items():
+        q, k, v = (torch.randn(B, H, S, d, device=dev, dtype=torch.float16, generator=g) for _ in range(3))
+        us = timed(lambda: F.scaled_dot_product_attention(q, k, v, is_causal=causal), 20)
+        pairs = B * H * (S * (S + 1) // 2 if causal else S * S)
+        out[f"sdpa_{name}"] = {"B": B, "H": H, "S": S, "d": d, "causal": causal, "us": round(us, 2),
+                               "TFLOP_s": round(4 * pairs * d / us / 1e6, 1)}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -270,6 +310,8 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU oracle timing")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-core", action="store_true", help="time only the headline kernel (for profiling)")
+    ap.add_argument("--vendor", action="store_true",
+                    help="only time the prefill shapes through torch (hipBLASLt matmul, SDPA) for comparison")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 5 device-to-device copies of 256 MiB: the known-size reference that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
@@ -278,6 +320,10 @@ def main() -> int:
         print(json.dumps({"error": "this build measures one MI355X only; multi-GPU runs are out of scope "
                                    "(--gpus must be 1)", "n_gpus": args.gpus}))
         return 2
+
+    if args.vendor:
+        print(json.dumps({"vendor_comparison": vendor_comparison()}), flush=True)
+        return 0
 
     import cudaforge_amd as cf
     cf.init_gpu(0)
