@@ -35,7 +35,9 @@ using namespace cdna4;
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyMax = 8.0f;           // fp16 split kernel: max headroom of p (log2 units)
-constexpr int kChunkMax = 4096;            // positions per split (LDS: chunk * G floats)
+constexpr int kChunkMax = 4096;            // positions per split of the fp32 / generic kernels
+                                           // (their scores live in LDS: chunk * G floats)
+constexpr int kChunkMaxF16 = 1 << 20;      // fp16 split kernel: LDS use is independent of the chunk
 constexpr int kF16Quantum = 32;            // fp16 split kernel: positions per block
 constexpr int kDecodeStages = 3;           // fp16 split kernel: default LDS ring depth (16 KB per stage at d = 128;
                                            // 3 stages = 3 workgroups per CU, best measured with HBM-resident KV)
@@ -723,8 +725,7 @@ extern "C" int32_t cf_decode_attn_wgs_per_cu(int32_t elem, int32_t d, int32_t gr
 }
 
 extern "C" int32_t cf_decode_attn_chunk_max(int32_t elem, int32_t d, int32_t group) {
-    (void)elem; (void)d; (void)group;
-    return kChunkMax;
+    return elem == CF_ELEM_F16 && fast_supported(elem, d, group) ? kChunkMaxF16 : kChunkMax;
 }
 
 extern "C" size_t cf_decode_attn_partials_floats(int32_t B, int32_t H_q, int32_t H_kv, int32_t d,
@@ -736,7 +737,9 @@ extern "C" size_t cf_decode_attn_partials_floats(int32_t B, int32_t H_q, int32_t
 
 extern "C" int cf_launch_decode_attn_split(const cf_decode_attn_args_t* a, void* stream) {
     hipStream_t s = (hipStream_t)stream;
-    if (a->chunk <= 0 || a->chunk > kChunkMax || a->n_split <= 0) return (int)hipErrorInvalidValue;
+    if (a->chunk <= 0 || a->n_split <= 0) return (int)hipErrorInvalidValue;
+    const bool f16_fast = a->elem == CF_ELEM_F16 && use_fast(a);
+    if (a->chunk > (f16_fast ? kChunkMaxF16 : kChunkMax)) return (int)hipErrorInvalidValue;
     hipError_t err;
     if (use_fast(a)) {
         const int G = a->H_q / a->H_kv;

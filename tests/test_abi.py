@@ -310,19 +310,20 @@ def test_tensor_api(native):
 @pytest.mark.parametrize("B,H,H_kv,d,cl,max_seq,f16", [
     (16, 32, 8, 128, 4095, 4096, 1), (4, 32, 8, 128, -1, 32768, 1), (1, 12, 12, 64, 1023, 1024, 0),
     (1, 8, 2, 128, 39999, 40000, 1), (64, 32, 8, 128, 127, 128, 1), (3, 6, 2, 32, 249, 255, 1),
-    (2, 4, 4, 80, 0, 16, 0)])
+    (2, 4, 4, 80, 0, 16, 0), (1, 8, 8, 128, 8_000_000 - 1, 8_000_000, 1)])
 def test_decode_split_plan_invariants(native, B, H, H_kv, d, cl, max_seq, f16):
     """The split planner (host only): chunks are whole 32-position blocks on the fp16
-    kernel path, cover every attended position, stay within the kernel's limits
-    (chunk <= 4096, at most 1024 splits) and leave no split empty."""
+    kernel path, cover every attended position, stay within the kernel's limits (at most
+    1024 splits; chunk <= 4096 where scores live in LDS) and leave no split empty; an
+    8M-position cache plans too."""
     import cudaforge_amd as cf
     p = cf.MhaDecodeParams(B, H * d, H, H_kv, d, 0.1, cl, max_seq)
     chunk, n = ctypes.c_int64(0), ctypes.c_int64(0)
     assert native.mha_decode_plan(ctypes.addressof(p), f16, ctypes.byref(chunk), ctypes.byref(n)) == 0
     chunk, n = chunk.value, n.value
     t_max = max_seq if cl < 0 else cl + 1
-    assert 1 <= chunk <= 4096 and 1 <= n <= 1024
-    assert n * chunk >= t_max and (n - 1) * chunk < t_max
     fast_f16 = f16 and d in (64, 128) and (H // H_kv) in (1, 2, 4, 8)
+    assert 1 <= chunk <= (1 << 20 if fast_f16 else 4096) and 1 <= n <= 1024
+    assert n * chunk >= t_max and (n - 1) * chunk < t_max
     if fast_f16:
         assert chunk % 32 == 0

@@ -367,3 +367,17 @@ def test_concurrent_streams_have_separate_scratch(gpu):
         st.synchronize()
     for out, want in zip(outs, seq):
         assert np.array_equal(out.download(), want)
+
+
+def test_split_chunks_longer_than_4096(gpu, native):
+    """The fp16 split kernel takes chunks beyond 4096 positions (its LDS use does not
+    grow with the chunk), which long caches need once the 1024-split cap binds."""
+    B, H, H_kv, d, T = 1, 8, 2, 128, 20000
+    Q, K, V = (O.round_f16(O.normal(s, 120 + i)) for i, s in enumerate([(B, H, d), (B, T, H_kv, d), (B, T, H_kv, d)]))
+    try:
+        native.mha_decode_set_split_chunk(8192)
+        got = run_decode_attn_gpu(Q, K, V, T - 1, H_kv, True)
+    finally:
+        native.mha_decode_set_split_chunk(0)
+    want = O.decode_attn(Q, K, V, np.full(B, T, np.int32), float(1 / np.sqrt(d)), H_kv)
+    assert max_abs(want, got) <= TOL16
