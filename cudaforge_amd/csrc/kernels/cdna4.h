@@ -6,6 +6,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 namespace cdna4 {
 
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
@@ -20,6 +23,35 @@ template <int N>
 __device__ __forceinline__ void wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+    asm volatile("" ::: "memory");
+}
+
+// Wait until at most `ahead` (clamped to 0..N_AHEAD) ring stages of NL loads each are
+// still in flight.
+template <int NL, int N_AHEAD>
+__device__ __forceinline__ void wait_ahead(int ahead) {
+    if (ahead >= N_AHEAD) wait_vm<N_AHEAD * NL>();
+    else if constexpr (N_AHEAD > 0) wait_ahead<NL, N_AHEAD - 1>(ahead);
+}
+
+// Ring loops with the stage index as a compile-time constant: calls
+// step(i, std::integral_constant<int, i % NS>{}) for i = 0 .. n-1, unrolled NS times, so
+// that LDS addresses inside a stage become a per-lane register plus an immediate offset.
+template <typename F, int... S>
+__device__ __forceinline__ void stage_group(int i0, int n, F& step, std::integer_sequence<int, S...>) {
+    ((i0 + S < n ? step(i0 + S, std::integral_constant<int, S>{}) : void()), ...);
+}
+
+template <int NS, typename F>
+__device__ __forceinline__ void for_each_stage(int n, F&& step) {
+    for (int i0 = 0; i0 < n; i0 += NS) stage_group(i0, n, step, std::make_integer_sequence<int, NS>{});
+}
+
+// s_waitcnt lgkmcnt(0): every LDS read issued so far has returned its data, so a DMA
+// may refill the stage it read.
+__device__ __forceinline__ void wait_lds_reads() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4));
     asm volatile("" ::: "memory");
 }
 

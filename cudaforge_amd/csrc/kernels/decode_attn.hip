@@ -98,7 +98,7 @@ void split_f16(cf_decode_attn_args_t a) {
     constexpr int TILE = BP * D;        // halves per block per tensor
     constexpr int NT = D / 16;          // output tiles of 16 dims
     constexpr int HDR = part_hdr(G);
-    static_assert((NS - 2) * NL < 64, "vmcnt range");
+    static_assert((NS - 1) * NL < 64, "vmcnt range");
     constexpr int QH = (G * D * 2 + 1023) / 1024 * 512;   // halves of the Q area (whole DMA KBs)
     __shared__ __attribute__((aligned(16))) _Float16 ring[NS * 2 * TILE + QH];
 
@@ -134,8 +134,7 @@ void split_f16(cf_decode_attn_args_t a) {
         koff[u] = (uint32_t)row * row_bytes + 16u * (uint32_t)(dchunk ^ kswz<D>(row));
         voff[u] = (uint32_t)row * row_bytes + 16u * (uint32_t)(dchunk ^ vswz<D>(row));
     }
-    auto issue = [&](int blk) {
-        const int stage = blk % NS;
+    auto issue = [&](int blk, int stage) {           // stage == blk % NS
         const int p0 = t0 + blk * BP;
         const uint32_t kbase = ring_base + (uint32_t)(stage * 2 * TILE) * 2u;
         const uint32_t vbase = kbase + (uint32_t)TILE * 2u;
@@ -194,26 +193,29 @@ void split_f16(cf_decode_attn_args_t a) {
     }
 #pragma unroll
     for (int s = 0; s < NS - 1; s++)
-        if (s < nblk) issue(s);
+        if (s < nblk) issue(s, s);
     // B operand Q^T: lane (lr, lq) holds Q[head lr][32kt + 8lq .. +7]; heads >= G are 0.
     h8_t qf[KT];
 
-    for (int blk = 0; blk < nblk; blk++) {
+    // One block; its ring stage is a compile-time constant (for_each_stage).
+    auto step = [&](int blk, auto stage_c) {
+        constexpr int stage = decltype(stage_c)::value;
+        // Refill the stage of the previous block before waiting for this one, so all NS
+        // stages are in flight during the wait.  That block's LDS reads have returned
+        // (their values fed its MFMAs): a single wave needs no barrier.
+        if (blk + NS - 1 < nblk) {
+            wait_lds_reads();
+            issue(blk + NS - 1, (stage + NS - 1) % NS);
+        }
         // Blocks issued after this one that may still be in flight.
-        const int ahead = min(NS - 2, nblk - 1 - blk);
-        if (ahead >= 2) wait_vm<2 * NL>();
-        else if (ahead == 1) wait_vm<NL>();
-        else wait_vm<0>();
-        if (blk == 0) {                              // Q landed with block 0
+        wait_ahead<NL, NS - 1>(min(NS - 1, nblk - 1 - blk));
+        if (stage == 0 && blk == 0) {                // Q landed with block 0
             const _Float16* qs = ring + NS * 2 * TILE + min(lr, G - 1) * D + 8 * lq;
 #pragma unroll
             for (int kt = 0; kt < KT; kt++) qf[kt] = lr < G ? *(const h8_t*)(qs + 32 * kt) : h8_t{};
         }
-        // The stage refilled here was read by the previous block, whose LDS reads have
-        // all returned (their values fed its MFMAs): a single wave needs no barrier.
-        if (blk + NS - 1 < nblk) issue(blk + NS - 1);
 
-        const _Float16* st = ring + (blk % NS) * 2 * TILE;
+        const _Float16* st = ring + stage * 2 * TILE;
         f4_t s[2];
 #pragma unroll
         for (int h = 0; h < 2; h++) {
@@ -269,7 +271,8 @@ void split_f16(cf_decode_attn_args_t a) {
             const h8_t vf = cat8(ds_read_tr4(st + v_rd[n][0]), ds_read_tr4(st + v_rd[n][1]));
             acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, acc[n], 0, 0, 0);
         }
-    }
+    };
+    for_each_stage<NS>(nblk, step);
 
     // l: the lanes of one head hold partial sums over their positions.
     l_run = add_xor32(add_xor16(l_run));

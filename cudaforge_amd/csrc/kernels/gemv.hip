@@ -232,12 +232,6 @@ __device__ __forceinline__ int wswz(int row) {
 }
 __device__ __forceinline__ int xswz(int row) { return (row >> 2) & 3; }
 
-template <int NL, int N_AHEAD>
-__device__ __forceinline__ void wait_ahead(int ahead) {
-    if (ahead >= N_AHEAD) wait_vm<N_AHEAD * NL>();
-    else if constexpr (N_AHEAD > 0) wait_ahead<NL, N_AHEAD - 1>(ahead);
-}
-
 template <int BN>
 __global__ __launch_bounds__(64)
 void gemv_f16_dma(cf_gemv_args_t a, Tiles t) {
@@ -248,7 +242,7 @@ void gemv_f16_dma(cf_gemv_args_t a, Tiles t) {
     constexpr int NL = NI + 1;                   // ... plus one for X
     constexpr int NT = BN / 16;                  // MFMA column tiles
     constexpr int STAGE = kDK * BN + kMTile * kDK;   // halves per stage: W then X
-    static_assert((NS - 2) * NL < 64, "vmcnt range");
+    static_assert((NS - 1) * NL < 64, "vmcnt range");
     __shared__ __attribute__((aligned(16))) _Float16 ring[NS * STAGE];
 
     const int tile = blockIdx.x, ks = blockIdx.y, mt = blockIdx.z;
@@ -276,9 +270,9 @@ void gemv_f16_dma(cf_gemv_args_t a, Tiles t) {
     const uint32_t xoff = (uint32_t)min(mt * kMTile + xr, a.M - 1) * (uint32_t)a.K * 2u +
                           16u * (uint32_t)((lane & 3) ^ xswz(xr));
     const uint32_t base = lds_offset(ring);
-    auto issue = [&](int st) {
+    auto issue = [&](int st, int stage) {           // stage == st % NS
         const int k0 = kbeg + st * kDK;
-        const uint32_t sb = base + (uint32_t)((st % NS) * STAGE) * 2u;
+        const uint32_t sb = base + (uint32_t)(stage * STAGE) * 2u;
         const _Float16* wb = W + (size_t)k0 * N + n0;
 #pragma unroll
         for (int u = 0; u < NI; u++) lds_dma16_s(woff[u], wb, sb + u * 1024u);
@@ -302,20 +296,25 @@ void gemv_f16_dma(cf_gemv_args_t a, Tiles t) {
     for (int j = 0; j < NT; j++) acc[j] = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < NS - 1; st++)
-        if (st < nst) issue(st);
-    for (int st = 0; st < nst; st++) {
-        wait_ahead<NL, NS - 2>(min(NS - 2, nst - 1 - st));
-        // The stage refilled here was read by the previous step, whose LDS reads have
-        // all returned (their values fed its MFMAs): one wave needs no barrier.
-        if (st + NS - 1 < nst) issue(st + NS - 1);
-        const _Float16* sp = ring + (st % NS) * STAGE;
+        if (st < nst) issue(st, st);
+    for_each_stage<NS>(nst, [&](int st, auto stage_c) {
+        constexpr int stage = decltype(stage_c)::value;
+        // Refill the previous step's stage before waiting for this one, so all NS stages
+        // are in flight during the wait.  Its LDS reads have returned (their values fed
+        // its MFMAs): one wave needs no barrier.
+        if (st + NS - 1 < nst) {
+            wait_lds_reads();
+            issue(st + NS - 1, (stage + NS - 1) % NS);
+        }
+        wait_ahead<NL, NS - 1>(min(NS - 1, nst - 1 - st));
+        const _Float16* sp = ring + stage * STAGE;
         const h8_t xa = *(const h8_t*)(sp + x_rd);
 #pragma unroll
         for (int j = 0; j < NT; j++) {
             const h8_t wb = cat8(ds_read_tr4(sp + w_rd[j][0]), ds_read_tr4(sp + w_rd[j][1]));
             acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, wb, acc[j], 0, 0, 0);
         }
-    }
+    });
 
     // Lane (lr, lq) holds Y[m = 16mt + 4lq + i][n0 + 16j + lr].
     if (t.ks == 1) {
