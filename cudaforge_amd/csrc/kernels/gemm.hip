@@ -189,47 +189,6 @@ __device__ __forceinline__ void epilogue_f16(const cf_gemm_args_t& a, int seg, i
     }
 }
 
-// Epilogue without a residual (the QKV projection): bias is added in registers and the
-// sum rounded to fp16 once, exactly as the fp32 path rounds it, so the whole 128 x BN
-// tile fits LDS as fp16 and goes out in a single pass.  `Cs` must hold 128 x LDCH
-// halves and be free (after a barrier).
-constexpr int LDCH = BN + 8;
-__device__ __forceinline__ void epilogue_f16_nores(const cf_gemm_args_t& a, int seg, int N, int m0, int n0, int wm,
-                                                   int wn, int lr, int lq, int tid, const f4_t (&acc)[4][4],
-                                                   _Float16* Cs) {
-    const _Float16* __restrict__ bias = (const _Float16*)a.bias[seg];
-    _Float16* __restrict__ out = (_Float16*)a.out[seg];
-    const bool along_n = a.out_kind == CF_GEMM_OUT_ROWMAJOR || seg < 2;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int nl = wn + 16 * j + lr;
-        const float bv = (bias && n0 + nl < N) ? (float)bias[n0 + nl] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) Cs[(wm + 16 * i + 4 * lq + e) * LDCH + nl] = (_Float16)(acc[i][j][e] + bv);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int it = 0; it < (BM * BN / 8) / kThreads; it++) {
-        const int ch = tid + it * kThreads;
-        if (along_n) {
-            const int r = ch >> 4, c8 = (ch & 15) * 8;
-            const int m = m0 + r, n = n0 + c8;
-            if (m >= a.M || n >= N) continue;
-            *(h8_t*)(out + row_part(a, seg, m) + col_part(a, seg, n)) = *(const h8_t*)&Cs[r * LDCH + c8];
-        } else {
-            const int col = ch & (BN - 1), r8 = (ch / BN) * 8;
-            const int m = m0 + r8, n = n0 + col;
-            if (m >= a.M || n >= N) continue;
-            h8_t v;
-#pragma unroll
-            for (int e = 0; e < 8; e++) v[e] = Cs[(r8 + e) * LDCH + col];
-            *(h8_t*)(out + row_part(a, seg, m) + col_part(a, seg, n)) = v;
-        }
-    }
-}
-
 // MFMA B operand (8 consecutive k of one column) from a W tile stored [k][n] in LDS:
 // two ds_read_b64_tr_b16.  p points at W[kb + lr/4][nb + 4*(lr%4)] of the caller's
 // lane; the second read is 4 rows further.
@@ -349,6 +308,68 @@ void gemm_f16(cf_gemm_args_t a, Tiling t) {
     else store_tile<_Float16>(a, seg, N, m0 + wm, n0 + wn, lr, lq, acc);
 }
 
+// Epilogues of the pipelined kernel, straight from the accumulators (no LDS pass).
+// Full tiles only, with the 8-byte alignment the launcher's epi_vec check implies.
+//
+// Columns-contiguous destinations (row-major C, head-major q and k): the main loop
+// accumulates C^T (MFMA operands swapped), so acc[i][j][e] = C[m][n + e] with
+// m = m0 + wm + 16i + lr and n = n0 + wn + 16j + 4lq: four consecutive columns of one
+// row, one 8-byte store.  Bias, then the residual, are added in fp32 before the single
+// rounding to fp16.
+__device__ __forceinline__ void store_ct_f16(const cf_gemm_args_t& a, int seg, int m0, int n0, int wm, int wn,
+                                             int lr, int lq, const f4_t (&acc)[4][4]) {
+    const _Float16* __restrict__ bias = (const _Float16*)a.bias[seg];
+    const _Float16* __restrict__ res = a.out_kind == CF_GEMM_OUT_ROWMAJOR ? (const _Float16*)a.residual : nullptr;
+    _Float16* __restrict__ out = (_Float16*)a.out[seg];
+    float bv[4][4];
+    size_t cp[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int n = n0 + wn + 16 * j + 4 * lq;
+        cp[j] = col_part(a, seg, n);
+#pragma unroll
+        for (int e = 0; e < 4; e++) bv[j][e] = bias ? (float)bias[n + e] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const size_t rp = row_part(a, seg, m0 + wm + 16 * i + lr);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const size_t off = rp + cp[j];
+            float f[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) f[e] = acc[i][j][e] + bv[j][e];
+            if (res) {
+                const h4_t r = *(const h4_t*)(res + off);
+#pragma unroll
+                for (int e = 0; e < 4; e++) f[e] += (float)r[e];
+            }
+            *(h4_t*)(out + off) = h4_t{(_Float16)f[0], (_Float16)f[1], (_Float16)f[2], (_Float16)f[3]};
+        }
+    }
+}
+
+// Rows-contiguous destination (v^T, (B, H_kv, d, S)): the main loop accumulates C, so
+// acc[i][j][e] = C[m + e][n] with m = m0 + wm + 16i + 4lq and n = n0 + wn + 16j + lr:
+// four consecutive positions s of one (head, dim) row of v^T, one 8-byte store.
+__device__ __forceinline__ void store_cn_f16(const cf_gemm_args_t& a, int seg, int m0, int n0, int wm, int wn,
+                                             int lr, int lq, const f4_t (&acc)[4][4]) {
+    const _Float16* __restrict__ bias = (const _Float16*)a.bias[seg];
+    _Float16* __restrict__ out = (_Float16*)a.out[seg];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int n = n0 + wn + 16 * j + lr;
+        const size_t cp = col_part(a, seg, n);
+        const float bv = bias ? (float)bias[n] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const size_t off = row_part(a, seg, m0 + wm + 16 * i + 4 * lq) + cp;
+            *(h4_t*)(out + off) = h4_t{(_Float16)(acc[i][j][0] + bv), (_Float16)(acc[i][j][1] + bv),
+                                       (_Float16)(acc[i][j][2] + bv), (_Float16)(acc[i][j][3] + bv)};
+        }
+    }
+}
+
 // ---- pipelined kernel: full tiles only (M % 128, N % 128, K % 32 == 0, aligned).
 // Four LDS stages of 32 k, filled by global_load_lds_dwordx4 (global -> LDS without
 // VGPRs): three k-tiles are in flight while one is multiplied.  A lane-contiguous
@@ -370,7 +391,6 @@ __device__ __forceinline__ int swz_w(int row) { return ((row & 3) << 1) ^ (((row
 template <int STAGES>
 __global__ __launch_bounds__(kThreads, 2)
 void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
-    static_assert(STAGES * ST * 2 >= 64 * LDCF * 4 && STAGES * ST >= BM * LDCH, "the epilogue reuses the ring");
     __shared__ __attribute__((aligned(16))) _Float16 smem[STAGES * ST];
 
     int tile_m, tile_n;
@@ -436,34 +456,41 @@ void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
 #pragma unroll
     for (int s = 0; s < STAGES - 1; s++)
         if (s < nk) issue(s, s * BKA);
-    for (int kt = 0; kt < nk; kt++) {
-        // Tiles issued after kt that may still be in flight: min(STAGES-2, nk-1-kt), 4
-        // load instructions each.
-        const int ahead = min(STAGES - 2, nk - 1 - kt);
-        if (ahead >= 2) wait_vm<8>();
-        else if (ahead == 1) wait_vm<4>();
-        else wait_vm<0>();
-        ring_barrier();
-        if (kt + STAGES - 1 < nk) issue((kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BKA);
-        const _Float16* As = smem + (kt % STAGES) * ST;
-        const _Float16* Ws = As + A_ST;
-        h8_t af[4], bf[4];
+    // CT: accumulate C^T (operands swapped) for destinations contiguous along n.
+    auto main_loop = [&](auto ct_c) {
+        constexpr bool CT = decltype(ct_c)::value;
+        for (int kt = 0; kt < nk; kt++) {
+            // Tiles issued after kt that may still be in flight: min(STAGES-2, nk-1-kt), 4
+            // load instructions each.
+            const int ahead = min(STAGES - 2, nk - 1 - kt);
+            if (ahead >= 2) wait_vm<8>();
+            else if (ahead == 1) wait_vm<4>();
+            else wait_vm<0>();
+            ring_barrier();
+            if (kt + STAGES - 1 < nk) issue((kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BKA);
+            const _Float16* As = smem + (kt % STAGES) * ST;
+            const _Float16* Ws = As + A_ST;
+            h8_t af[4], bf[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) af[i] = *(const h8_t*)&As[a_rd[i]];
+            for (int i = 0; i < 4; i++) af[i] = *(const h8_t*)&As[a_rd[i]];
 #pragma unroll
-        for (int j = 0; j < 4; j++) bf[j] = b_frag_tr(Ws + w_rd[j][0], Ws + w_rd[j][1]);
+            for (int j = 0; j < 4; j++) bf[j] = b_frag_tr(Ws + w_rd[j][0], Ws + w_rd[j][1]);
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+            for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < 4; j++)
+                    acc[i][j] = CT ? __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[j], af[i], acc[i][j], 0, 0, 0)
+                                   : __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    };
+    // Every DMA load was waited for in the last step, and the epilogue does not touch LDS.
+    if (a.out_kind == CF_GEMM_OUT_ROWMAJOR || seg < 2) {
+        main_loop(std::true_type{});
+        store_ct_f16(a, seg, m0, n0, wm, wn, lr, lq, acc);
+    } else {
+        main_loop(std::false_type{});
+        store_cn_f16(a, seg, m0, n0, wm, wn, lr, lq, acc);
     }
-    wait_vm<0>();
-    __syncthreads();
-    if (a.residual == nullptr || a.out_kind != CF_GEMM_OUT_ROWMAJOR)
-        epilogue_f16_nores(a, seg, N, m0, n0, wm, wn, lr, lq, tid, acc, smem);
-    else
-        epilogue_f16(a, seg, N, m0, n0, wm, wn, lr, lq, tid, acc, (float*)smem);
 }
 
 // ------------------------------------------------------------------------- fp32 ---
