@@ -12,6 +12,7 @@ from .api import (  # noqa: F401
     MhaDecodeParams,
     MhaFusedParams,
     CausalMaskParams,
+    GraphMhaMatch,
     OperatorRegistry,
     Stream,
     Event,
@@ -19,6 +20,7 @@ from .api import (  # noqa: F401
     call_op,
     device_caps,
     find_op,
+    graph_detect_mha,
     gpu_available,
     init_gpu,
 )
@@ -32,12 +34,14 @@ __all__ = [
     "MhaDecodeParams",
     "MhaFusedParams",
     "CausalMaskParams",
+    "GraphMhaMatch",
     "OperatorRegistry",
     "Stream",
     "Event",
     "TensorT",
     "call_op",
     "device_caps",
+    "graph_detect_mha",
     "find_op",
     "gpu_available",
     "init_gpu",

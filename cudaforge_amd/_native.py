@@ -131,6 +131,7 @@ def _proto(lib):
         "graph_set_permanent_fusion": (None, [c_void_p, c_int]),
         "graph_execute": (c_int, [c_void_p, POINTER(c_void_p), POINTER(c_void_p), ctypes.c_bool]),
         "graph_resolve_op": (POINTER(OperatorRegistryEntry), [c_void_p, c_int, ctypes.c_bool, c_char_p, c_size_t]),
+        "graph_detect_mha": (c_int, [c_void_p, c_void_p, c_int]),
         "inference_engine_init": (c_int, []),
         "inference_engine_finalize": (None, []),
         "inference_session_load": (c_void_p, [c_char_p]),

@@ -41,6 +41,32 @@ class MhaFusedParams(ctypes.Structure):
     ]
 
 
+GRAPH_MHA_MAX_NODES = 24
+
+
+class GraphMhaMatch(ctypes.Structure):
+    """graph_mha_match_t (include/graph.h): one self-attention subgraph that graph_execute
+    runs as a single OP_MHA_FUSED node."""
+
+    _fields_ = [
+        ("out_node", ctypes.c_int),
+        ("num_nodes", ctypes.c_int),
+        ("nodes", ctypes.c_int * GRAPH_MHA_MAX_NODES),
+        ("input_tid", ctypes.c_int),
+        ("residual_tid", ctypes.c_int),
+        ("output_tid", ctypes.c_int),
+        ("weights", ctypes.c_void_p * 8),
+        ("params", MhaFusedParams),
+    ]
+
+
+def graph_detect_mha(graph, max_matches=8):
+    """The attention subgraphs graph_execute would fuse (list of GraphMhaMatch)."""
+    arr = (GraphMhaMatch * max_matches)()
+    n = load_library().graph_detect_mha(graph, ctypes.cast(arr, ctypes.c_void_p), max_matches)
+    return [arr[i] for i in range(n)]
+
+
 class CausalMaskParams(ctypes.Structure):
     _fields_ = [("seq_len", c_int64)]
 

@@ -13,8 +13,10 @@
  *   - an op's nonzero return aborts execution and is returned (graph.c:1019-1025).
  * Changes: graph inputs are re-uploaded on every execution (the reference uploaded once,
  * tensor.c:54, and reused stale data); KV-cache tensors are device-authoritative and
- * uploaded once; a CPU op that writes a KV cache refreshes its device copy.  The MHA
- * subgraph fusion pre-pass (graph.c:359-665) is not part of this build.
+ * uploaded once; a CPU op that writes a KV cache refreshes its device copy.  GPU
+ * executions run each self-attention subgraph that graph_detect_mha finds (graph_fuse.c,
+ * the reference's detect_and_fuse_mha, graph.c:347-665) as one OP_MHA_FUSED node, without
+ * rewriting the graph.
  */
 #include "graph.h"
 #include "gpu_ops.h"
@@ -235,10 +237,8 @@ static const char* op_name(op_type_t type) {
     }
 }
 
-const operator_registry_t* graph_resolve_op(const inference_graph_t* g, int node_id, bool use_cuda,
-                                            char* buf, size_t buf_len) {
-    if (!g || node_id < 0 || node_id >= g->num_nodes || !buf || buf_len < 8) return NULL;
-    const graph_node_t* n = &g->nodes[node_id];
+static const operator_registry_t* resolve_node(const inference_graph_t* g, const graph_node_t* n, bool use_cuda,
+                                               char* buf, size_t buf_len) {
     const char* base = op_name(n->type);
     buf[0] = '\0';
     if (!base) return NULL;
@@ -268,6 +268,12 @@ const operator_registry_t* graph_resolve_op(const inference_graph_t* g, int node
     return op;
 }
 
+const operator_registry_t* graph_resolve_op(const inference_graph_t* g, int node_id, bool use_cuda,
+                                            char* buf, size_t buf_len) {
+    if (!g || node_id < 0 || node_id >= g->num_nodes || !buf || buf_len < 8) return NULL;
+    return resolve_node(g, &g->nodes[node_id], use_cuda, buf, buf_len);
+}
+
 static size_t tensor_nbytes(const tensor_t* t) {
     const data_type_info_t* info = data_type_get_info(t->dtype);
     return info ? (size_t)t->numel * info->size : 0;
@@ -283,6 +289,91 @@ static int is_kv(const inference_graph_t* g, int tid) {
 static int op_produced(const inference_graph_t* g, int tid) {
     const int prod = g->tensors[tid].producer;
     return prod >= 0 && g->nodes[prod].type != OP_INPUT;
+}
+
+/* Runs one node: resolves its operator, moves its tensors to where the operator runs,
+ * calls it (graph.c:820-1030). */
+static int run_node(inference_graph_t* g, const graph_node_t* n, bool use_cuda, unsigned char* fresh) {
+    int ret = 0;
+    char name[64];
+    const operator_registry_t* op = resolve_node(g, n, use_cuda, name, sizeof(name));
+    if (!op) return -2;
+    const int on_gpu = use_cuda && strstr(name, "_cuda") != NULL;
+
+    const int in_slots = n->num_inputs + n->num_weights;
+    const int total = in_slots + n->num_outputs;
+    const void* local[32];
+    const void** slots = total <= 32 ? local : (const void**)malloc((size_t)total * sizeof(void*));
+    if (!slots) return -1;
+    void** outs = (void**)&slots[in_slots];
+
+    for (int i = 0; i < n->num_inputs && ret == 0; i++) {
+        const int tid = n->input_tensors[i];
+        slots[i] = NULL;
+        if (tid < 0 || tid >= g->num_tensors) continue;
+        tensor_t* t = g->tensors[tid].tensor;
+        if (on_gpu) {
+            if (is_kv(g, tid) || op_produced(g, tid)) {
+                if (tensor_copy_to_device(t) != 0) ret = -1;
+            } else if (!fresh[tid]) {
+                if (tensor_upload(t) != 0) ret = -1;
+                fresh[tid] = 1;
+            }
+            slots[i] = t->data_device;
+        } else {
+            if (t->data_device && op_produced(g, tid) && tensor_copy_to_host(t) != 0) ret = -1;
+            if (is_kv(g, tid) && t->data_device && tensor_copy_to_host(t) != 0) ret = -1;
+            slots[i] = t->data;
+        }
+    }
+    for (int w = 0; w < n->num_weights && ret == 0; w++) {
+        tensor_t* t = n->weights[w];
+        slots[n->num_inputs + w] = NULL;
+        if (!t) continue;
+        if (on_gpu) {
+            if (tensor_copy_to_device(t) != 0) ret = -1;
+            slots[n->num_inputs + w] = t->data_device;
+        } else {
+            slots[n->num_inputs + w] = t->data;
+        }
+    }
+    for (int i = 0; i < n->num_outputs && ret == 0; i++) {
+        const int tid = n->output_tensors[i];
+        outs[i] = NULL;
+        if (tid < 0 || tid >= g->num_tensors) continue;
+        tensor_t* t = g->tensors[tid].tensor;
+        if (on_gpu) {
+            if (!t->data_device) {
+                t->data_device = gpu_device_alloc(tensor_nbytes(t));
+                if (!t->data_device) ret = -1;
+            }
+            outs[i] = t->data_device;
+        } else {
+            outs[i] = t->data;
+        }
+    }
+    if (ret == 0) {
+        stream_t stream = {NULL};
+        ret = op->func(slots, outs, (const operator_params_t*)n->params, use_cuda ? &stream : NULL);
+    }
+    if (ret == 0 && use_cuda && !on_gpu) {
+        /* A CPU op wrote host data: device copies are stale.  KV caches stay
+         * device-authoritative, so refresh them; drop the others. */
+        for (int i = 0; i < n->num_outputs; i++) {
+            const int tid = n->output_tensors[i];
+            if (tid < 0 || tid >= g->num_tensors) continue;
+            tensor_t* t = g->tensors[tid].tensor;
+            if (!t->data_device) continue;
+            if (is_kv(g, tid)) {
+                if (tensor_upload(t) != 0) ret = -1;
+            } else {
+                gpu_device_free(t->data_device);
+                t->data_device = NULL;
+            }
+        }
+    }
+    if (slots != local) free((void*)slots);
+    return ret;
 }
 
 int graph_execute(inference_graph_t* g, tensor_t* inputs[], tensor_t* outputs[], bool use_cuda) {
@@ -306,90 +397,52 @@ int graph_execute(inference_graph_t* g, tensor_t* inputs[], tensor_t* outputs[],
     /* Tensors uploaded during this execution (so each external input moves once). */
     unsigned char* fresh = (unsigned char*)calloc((size_t)(g->num_tensors > 0 ? g->num_tensors : 1), 1);
     if (!fresh) return -1;
+
+    /* MHA subgraph fusion (graph.c:766-815, GPU executions only): each match runs as one
+     * OP_MHA_FUSED node in place of its last node; its other nodes are skipped. */
+    graph_mha_match_t* fz = NULL;
+    int* fused_at = NULL;
+    int n_fused = 0;
+    if (use_cuda && g->num_nodes > 0) {
+        const int cap = g->num_nodes / 8 + 1;
+        fz = (graph_mha_match_t*)malloc((size_t)cap * sizeof(*fz));
+        fused_at = (int*)malloc((size_t)g->num_nodes * sizeof(int));
+        if (!fz || !fused_at) { free(fz); free(fused_at); free(fresh); return -1; }
+        n_fused = graph_detect_mha(g, fz, cap);
+        for (int i = 0; i < g->num_nodes; i++) fused_at[i] = -1;
+        for (int k = 0; k < n_fused; k++)
+            for (int i = 0; i < fz[k].num_nodes; i++)
+                fused_at[fz[k].nodes[i]] = fz[k].nodes[i] == fz[k].out_node ? k : -2;
+    }
+
     int ret = 0;
     for (int oi = 0; oi < g->num_nodes && ret == 0; oi++) {
         const int nid = g->topo_order[oi];
         graph_node_t* n = &g->nodes[nid];
         if (n->type == OP_INPUT || n->type == OP_OUTPUT) continue;
-        char name[64];
-        const operator_registry_t* op = graph_resolve_op(g, nid, use_cuda, name, sizeof(name));
-        if (!op) { ret = -2; break; }
-        const int on_gpu = use_cuda && strstr(name, "_cuda") != NULL;
-
-        const int in_slots = n->num_inputs + n->num_weights;
-        const int total = in_slots + n->num_outputs;
-        const void* local[32];
-        const void** slots = total <= 32 ? local : (const void**)malloc((size_t)total * sizeof(void*));
-        if (!slots) { ret = -1; break; }
-        void** outs = (void**)&slots[in_slots];
-
-        for (int i = 0; i < n->num_inputs && ret == 0; i++) {
-            const int tid = n->input_tensors[i];
-            slots[i] = NULL;
-            if (tid < 0 || tid >= g->num_tensors) continue;
-            tensor_t* t = g->tensors[tid].tensor;
-            if (on_gpu) {
-                if (is_kv(g, tid) || op_produced(g, tid)) {
-                    if (tensor_copy_to_device(t) != 0) ret = -1;
-                } else if (!fresh[tid]) {
-                    if (tensor_upload(t) != 0) ret = -1;
-                    fresh[tid] = 1;
-                }
-                slots[i] = t->data_device;
-            } else {
-                if (t->data_device && op_produced(g, tid) && tensor_copy_to_host(t) != 0) ret = -1;
-                if (is_kv(g, tid) && t->data_device && tensor_copy_to_host(t) != 0) ret = -1;
-                slots[i] = t->data;
-            }
+        if (fused_at && fused_at[nid] == -2) continue;
+        if (fused_at && fused_at[nid] >= 0) {
+            graph_mha_match_t* m = &fz[fused_at[nid]];
+            int fin[2] = {m->input_tid, m->residual_tid};
+            int fout[1] = {m->output_tid};
+            graph_node_t fn;
+            memset(&fn, 0, sizeof(fn));
+            fn.type = OP_MHA_FUSED;
+            fn.num_inputs = 2;
+            fn.input_tensors = fin;
+            fn.num_outputs = 1;
+            fn.output_tensors = fout;
+            fn.num_weights = 8;
+            fn.weights = m->weights;
+            fn.params = &m->params;
+            fn.params_size = sizeof(m->params);
+            ret = run_node(g, &fn, use_cuda, fresh);
+        } else {
+            ret = run_node(g, n, use_cuda, fresh);
         }
-        for (int w = 0; w < n->num_weights && ret == 0; w++) {
-            tensor_t* t = n->weights[w];
-            slots[n->num_inputs + w] = NULL;
-            if (!t) continue;
-            if (on_gpu) {
-                if (tensor_copy_to_device(t) != 0) ret = -1;
-                slots[n->num_inputs + w] = t->data_device;
-            } else {
-                slots[n->num_inputs + w] = t->data;
-            }
-        }
-        for (int i = 0; i < n->num_outputs && ret == 0; i++) {
-            const int tid = n->output_tensors[i];
-            outs[i] = NULL;
-            if (tid < 0 || tid >= g->num_tensors) continue;
-            tensor_t* t = g->tensors[tid].tensor;
-            if (on_gpu) {
-                if (!t->data_device) {
-                    t->data_device = gpu_device_alloc(tensor_nbytes(t));
-                    if (!t->data_device) ret = -1;
-                }
-                outs[i] = t->data_device;
-            } else {
-                outs[i] = t->data;
-            }
-        }
-        if (ret == 0) {
-            stream_t stream = {NULL};
-            ret = op->func(slots, outs, (const operator_params_t*)n->params, use_cuda ? &stream : NULL);
-        }
-        if (ret == 0 && use_cuda && !on_gpu) {
-            /* A CPU op wrote host data: device copies are stale.  KV caches stay
-             * device-authoritative, so refresh them; drop the others. */
-            for (int i = 0; i < n->num_outputs; i++) {
-                const int tid = n->output_tensors[i];
-                if (tid < 0 || tid >= g->num_tensors) continue;
-                tensor_t* t = g->tensors[tid].tensor;
-                if (!t->data_device) continue;
-                if (is_kv(g, tid)) {
-                    if (tensor_upload(t) != 0) ret = -1;
-                } else {
-                    gpu_device_free(t->data_device);
-                    t->data_device = NULL;
-                }
-            }
-        }
-        if (slots != local) free((void*)slots);
     }
+    free(fz);
+    free(fused_at);
     free(fresh);
     if (ret != 0) return ret;
 

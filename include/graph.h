@@ -15,6 +15,7 @@
 
 #include "platform.h"
 #include "operator.h"
+#include "mha_fused_int.h"
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -116,10 +117,38 @@ void  graph_destroy(inference_graph_t* g);
 
 void  graph_set_kv_cache(inference_graph_t* g, int K_tensor_id, int V_tensor_id);
 void  graph_update_cache_len(inference_graph_t* g, int64_t new_cache_len);
+/* Accepted for source compatibility.  Fusion here is decided anew on every execution
+ * and never rewrites the graph, so the flag changes nothing. */
 void  graph_set_permanent_fusion(inference_graph_t* g, int enable);
 
 int   graph_execute(inference_graph_t* g, tensor_t* inputs[],
                     tensor_t* outputs[], bool use_cuda);
+
+/* One self-attention subgraph, the pattern of the reference's detect_and_fuse_mha
+ * (graph.c:347-665):
+ *   X -> 3 x [MatMul (-> Add bias) -> Reshape -> Transpose] -> Q, K, V
+ *   MatMul(Q, K) -> Mul(scale) (-> CausalMask) -> Softmax -> MatMul(., V)
+ *   -> Transpose -> Reshape -> MatMul(W_O) (-> Add b_O) (-> Add residual)
+ * Every intermediate tensor must have exactly one reader.  When use_cuda is set,
+ * graph_execute runs each match as one OP_MHA_FUSED node in place of the pattern's last
+ * node and skips the others; the graph itself is never modified. */
+#define GRAPH_MHA_MAX_NODES 24
+typedef struct {
+    int       out_node;                      /* the pattern's last node */
+    int       num_nodes;
+    int       nodes[GRAPH_MHA_MAX_NODES];    /* every node of the pattern */
+    int       input_tid;                     /* X (B, S, D) */
+    int       residual_tid;                  /* -1 without a residual Add */
+    int       output_tid;
+    tensor_t* weights[8];                    /* W_Q, b_Q, W_K, b_K, W_V, b_V, W_O, b_O */
+    mha_fused_params_t params;
+} graph_mha_match_t;
+
+/* Finds up to max_matches non-overlapping attention subgraphs (all of them, where the
+ * reference fused the first only); returns how many.  No counterpart in the reference,
+ * which keeps the detection static: it lets callers and tests see what graph_execute
+ * will fuse. */
+int   graph_detect_mha(const inference_graph_t* g, graph_mha_match_t* matches, int max_matches);
 
 /* Name the executor would dispatch a node to (for tests): writes into buf, returns the
  * registry entry or NULL. */

@@ -232,3 +232,84 @@ def build_decode_graph(lib, c: DecodeCase):
     lib.graph_set_kv_cache(g.g, iK, iV)
     assert lib.graph_build(g.g) == 0
     return g, {"X": tX, "K": tK, "V": tV, "Y": tY}
+
+
+# op_type_t values of the unfused attention pattern (include/graph.h enum order).
+OP_MATMUL, OP_ADD, OP_RESHAPE, OP_SOFTMAX, OP_MUL, OP_TRANSPOSE = 3, 8, 9, 11, 13, 16
+
+
+def build_attention_subgraph(g: Graph, c: FusedCase, x_id, r_id=None, *, bias=True, causal=False,
+                             scale=None, softmax_op=None, extra_scores_reader=False, wdtype=None):
+    """Appends the unfused self-attention block the reference's fusion pass recognises
+    (graph.c:347-358, the ONNX BERT export's node pattern) reading tensor x_id:
+      X -> 3 x [MatMul -> Add(bias) -> Reshape -> Transpose] -> Q, K, V;
+      MatMul(Q, K^T) -> Mul(scale) [-> CausalMask] -> Softmax -> MatMul(., V)
+      -> Transpose -> Reshape -> MatMul(W_O) -> Add(b_O) [-> Add(residual r_id)].
+    Intermediate tensors get their real shapes (never computed: the pattern runs fused).
+    Bias Adds take the bias as their second input and as their weight, as the
+    reference's Add nodes do.  Returns {name: id} for the nodes and tensors."""
+    B, S, D, H, H_kv, d = c.B, c.S, c.D, c.H, c.H_kv, c.d
+    dt = DT_F16 if c.f16 else DT_F32
+    npdt = np.float16 if c.f16 else np.float32
+    conv = (lambda a: O.to_f16(a)) if c.f16 else (lambda a: np.asarray(a, np.float32))
+    wdt = dt if wdtype is None else wdtype
+    wconv = (lambda a: O.to_f16(a)) if wdt == DT_F16 else (lambda a: np.asarray(a, np.float32))
+
+    def t(shape):
+        return g.tensor(np.zeros(shape, npdt), dt)
+
+    ids = {}
+    chains = {}
+    for name, W, bvec, heads, kt in (("q", c.WQ, c.bQ, H, False), ("k", c.WK, c.bK, H_kv, True),
+                                     ("v", c.WV, c.bV, H_kv, False)):
+        width = heads * d
+        w_t, _ = g.tensor(wconv(W), wdt)
+        _, mm_out = t((B, S, width))
+        ids["mm_" + name] = g.node(OP_MATMUL, [x_id], [mm_out], [w_t])
+        cur = mm_out
+        if bias:
+            b_t, b_id = g.tensor(wconv(bvec), wdt)
+            _, add_out = t((B, S, width))
+            ids["add_" + name] = g.node(OP_ADD, [cur, b_id], [add_out], [b_t])
+            cur = add_out
+        _, rs = t((B, S, heads, d))
+        ids["rs_" + name] = g.node(OP_RESHAPE, [cur], [rs])
+        _, tr = t((B, heads, d, S) if kt else (B, heads, S, d))
+        ids["tr_" + name] = g.node(OP_TRANSPOSE, [rs], [tr])
+        chains[name] = tr
+    _, scores = t((B, H, S, S))
+    ids["attn"] = g.node(OP_MATMUL, [chains["q"], chains["k"]], [scores])
+    if extra_scores_reader:
+        _, spare = t((B, H, S, S))
+        ids["spare"] = g.node(OP_RELU, [scores], [spare])
+    s_t, _ = g.tensor(np.full((1,), 1.0 / np.sqrt(d) if scale is None else scale, np.float32))
+    _, scaled = t((B, H, S, S))
+    ids["mul"] = g.node(OP_MUL, [scores], [scaled], [s_t])
+    cur = scaled
+    if causal:
+        _, masked = t((B, H, S, S))
+        ids["mask"] = g.node(OP_CAUSAL_MASK, [cur], [masked])
+        cur = masked
+    _, probs = t((B, H, S, S))
+    ids["softmax"] = g.node(OP_SOFTMAX if softmax_op is None else softmax_op, [cur], [probs])
+    _, ctx = t((B, H, S, d))
+    ids["pv"] = g.node(OP_MATMUL, [probs, chains["v"]], [ctx])
+    _, ctx_t = t((B, S, H, d))
+    ids["tr_o"] = g.node(OP_TRANSPOSE, [ctx], [ctx_t])
+    _, merged = t((B, S, D))
+    ids["rs_o"] = g.node(OP_RESHAPE, [ctx_t], [merged])
+    wo_t, _ = g.tensor(wconv(c.WO), wdt)
+    _, proj = t((B, S, D))
+    ids["mm_o"] = g.node(OP_MATMUL, [merged], [proj], [wo_t])
+    cur = proj
+    if bias:
+        bo_t, bo_id = g.tensor(wconv(c.bO), wdt)
+        _, projb = t((B, S, D))
+        ids["add_o"] = g.node(OP_ADD, [cur, bo_id], [projb], [bo_t])
+        cur = projb
+    if r_id is not None:
+        _, out = t((B, S, D))
+        ids["add_r"] = g.node(OP_ADD, [cur, r_id], [out])
+        cur = out
+    ids["out"] = cur
+    return ids

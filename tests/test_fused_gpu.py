@@ -145,3 +145,78 @@ def test_flash_kernel_variants_agree(gpu, native, causal):
     for o in outs:
         assert max_abs(want, o) <= TOL16
         assert max_abs(outs[0], o) <= 1e-2
+
+
+@pytest.mark.parametrize("f16,causal", [(False, False), (True, False), (True, True)])
+def test_graph_runs_unfused_attention_as_one_fused_op(gpu, native, f16, causal):
+    """An unfused self-attention block (MatMul/Add/Reshape/Transpose/Mul/[CausalMask]/
+    Softmax nodes, the reference fusion pass's pattern, graph.c:347-665) executed with
+    use_cuda: graph_execute runs it as one OP_MHA_FUSED (no MatMul or Softmax operator is
+    registered, so any unfused node would return -2) and the output matches the oracle."""
+    from helpers import DT_F16, DT_F32, OP_INPUT, OP_OUTPUT, Graph, build_attention_subgraph
+    import oracle as O
+    c = FusedCase(2, 40, 4, 2, 32, seed=23, f16=f16, residual=True, causal=causal, bias_std=0.02)
+    dt, npdt = (DT_F16, np.float16) if f16 else (DT_F32, np.float32)
+    conv = (lambda a: O.to_f16(a)) if f16 else (lambda a: np.asarray(a, np.float32))
+    g = Graph(native)
+    try:
+        tX, iX = g.tensor(conv(c.X), dt)
+        tR, iR = g.tensor(conv(c.R), dt)
+        ids = build_attention_subgraph(g, c, iX, iR, causal=causal)
+        native.graph_set_input(g.g, g.node(OP_INPUT, [], [iX]))
+        native.graph_set_output(g.g, g.node(OP_OUTPUT, [ids["out"]], []))
+        assert native.graph_build(g.g) == 0
+        tY = g.tensor(np.zeros(c.X.shape, npdt), dt)[0]
+        ins, outs = (ctypes.c_void_p * 1)(tX), (ctypes.c_void_p * 1)(tY)
+        assert native.graph_execute(g.g, ins, outs, True) == 0
+        got = g.read(tY, c.X.shape, npdt)
+        assert max_abs(c.oracle(), got) <= (TOL16 if f16 else TOL32)
+        # A second execution (fusion is decided per execution, the graph is unchanged).
+        assert native.graph_execute(g.g, ins, outs, True) == 0
+        assert max_abs(c.oracle(), g.read(tY, c.X.shape, npdt)) <= (TOL16 if f16 else TOL32)
+    finally:
+        g.destroy()
+
+
+def test_graph_fuses_every_layer(gpu, native):
+    """Two stacked attention blocks, each with the residual from its own input (BERT's
+    wiring): both run fused; the reference fused only the first (graph.c:655)."""
+    from helpers import DT_F32, OP_INPUT, OP_OUTPUT, Graph, build_attention_subgraph
+    import oracle as O
+    c = FusedCase(1, 24, 4, 4, 16, seed=29, residual=True, bias_std=0.02)
+    g = Graph(native)
+    try:
+        tX, iX = g.tensor(np.asarray(c.X, np.float32))
+        ids1 = build_attention_subgraph(g, c, iX, iX)
+        ids2 = build_attention_subgraph(g, c, ids1["out"], ids1["out"])
+        native.graph_set_input(g.g, g.node(OP_INPUT, [], [iX]))
+        native.graph_set_output(g.g, g.node(OP_OUTPUT, [ids2["out"]], []))
+        assert native.graph_build(g.g) == 0
+        tY = g.tensor(np.zeros_like(c.X, dtype=np.float32), DT_F32)[0]
+        ins, outs = (ctypes.c_void_p * 1)(tX), (ctypes.c_void_p * 1)(tY)
+        assert native.graph_execute(g.g, ins, outs, True) == 0
+        p = O.fused_params(c.B, c.S, c.D, c.H, c.H_kv, c.d, True, False)
+        w = [c.WQ, c.bQ, c.WK, c.bK, c.WV, c.bV, c.WO, c.bO]
+        y1 = O.mha_fused(c.X, c.X, *w, p)
+        y2 = O.mha_fused(y1, y1, *w, p)
+        assert max_abs(y2, g.read(tY, c.X.shape)) <= 2 * TOL32
+    finally:
+        g.destroy()
+
+
+def test_graph_broken_attention_pattern_is_not_fused(gpu, native):
+    """Softmax replaced by ReLU: no fusion, so the MatMul nodes find no operator (-2)."""
+    from helpers import DT_F32, OP_INPUT, OP_OUTPUT, OP_RELU, Graph, build_attention_subgraph
+    c = FusedCase(1, 8, 2, 2, 8, seed=31, residual=True)
+    g = Graph(native)
+    try:
+        tX, iX = g.tensor(np.asarray(c.X, np.float32))
+        ids = build_attention_subgraph(g, c, iX, iX, softmax_op=OP_RELU)
+        native.graph_set_input(g.g, g.node(OP_INPUT, [], [iX]))
+        native.graph_set_output(g.g, g.node(OP_OUTPUT, [ids["out"]], []))
+        assert native.graph_build(g.g) == 0
+        tY = g.tensor(np.zeros_like(c.X, dtype=np.float32), DT_F32)[0]
+        ins, outs = (ctypes.c_void_p * 1)(tX), (ctypes.c_void_p * 1)(tY)
+        assert native.graph_execute(g.g, ins, outs, True) == -2
+    finally:
+        g.destroy()
