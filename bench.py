@@ -103,7 +103,8 @@ def plan(cf, params, f16=True):
     return int(c.value), int(n.value)
 
 
-def bench_decode_full(cf, stream, steps, warmup, f16=True, B=16, H=32, H_kv=8, d=128, T=4096, seed=200, n_sets=1):
+def bench_decode_full(cf, stream, steps, warmup, f16=True, B=16, H=32, H_kv=8, d=128, T=4096, seed=200, n_sets=1,
+                      rope_base=None):
     D, kvd = H * d, H_kv * d
     dt = np.float16 if f16 else np.float32
 
@@ -125,6 +126,9 @@ def bench_decode_full(cf, stream, steps, warmup, f16=True, B=16, H=32, H_kv=8, d
         output_sets.append([cf.DeviceBuffer.empty((B, 1, D), dt), ins[1], ins[2]])
     p = cf.MhaDecodeParams(B, D, H, H_kv, d, float(1 / np.sqrt(d)), T - 1, T)
     name = "mha_decode_f16_cuda" if f16 else "mha_decode_f32_cuda"
+    if rope_base is not None:
+        p = cf.MhaDecodeRopeParams(p, rope_base, 0)
+        name = name.replace("mha_decode_", "mha_decode_rope_")
     from cudaforge_amd.api import time_op_sets
     ms = time_op_sets(name, input_sets, output_sets, p, stream, warmup, steps)
     esz = 2 if f16 else 4
@@ -356,6 +360,12 @@ def main() -> int:
                                                "GB_s": round(alg_f / (ms_f * 1e-3) / 1e9, 1),
                                                "alg_bytes": alg_f}
         log(f"  {ms_f * 1e3:.2f} us/step")
+        log("decode full op with RoPE (base 500000), config 2")
+        ms_fr, _ = bench_decode_full(cf, stream, steps, warmup, n_sets=KV_SETS, rope_base=500000.0)
+        extra["decode_full_op_config2_f16_rope"] = {"us_per_step": round(ms_fr * 1e3, 2),
+                                                    "GB_s": round(alg_f / (ms_fr * 1e-3) / 1e9, 1),
+                                                    "alg_bytes": alg_f}
+        log(f"  {ms_fr * 1e3:.2f} us/step")
         log("decode through graph_execute, config 2 (host X/Y)")
         ms_g = bench_decode_graph(cf, 50, 5)
         extra["decode_graph_config2_f16"] = {"us_per_step": round(ms_g * 1e3, 2),

@@ -11,6 +11,8 @@ from .api import (  # noqa: F401
     DeviceBuffer,
     MhaDecodeParams,
     MhaFusedParams,
+    MhaDecodeRopeParams,
+    RopeParams,
     CausalMaskParams,
     GraphMhaMatch,
     OperatorRegistry,
@@ -33,6 +35,8 @@ __all__ = [
     "DeviceBuffer",
     "MhaDecodeParams",
     "MhaFusedParams",
+    "MhaDecodeRopeParams",
+    "RopeParams",
     "CausalMaskParams",
     "GraphMhaMatch",
     "OperatorRegistry",

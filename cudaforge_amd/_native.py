@@ -132,6 +132,7 @@ def _proto(lib):
         "graph_execute": (c_int, [c_void_p, POINTER(c_void_p), POINTER(c_void_p), ctypes.c_bool]),
         "graph_resolve_op": (POINTER(OperatorRegistryEntry), [c_void_p, c_int, ctypes.c_bool, c_char_p, c_size_t]),
         "graph_detect_mha": (c_int, [c_void_p, c_void_p, c_int]),
+        "rope_table_device": (c_void_p, [c_float, c_int64, c_int64]),
         "inference_engine_init": (c_int, []),
         "inference_engine_finalize": (None, []),
         "inference_session_load": (c_void_p, [c_char_p]),
@@ -147,7 +148,8 @@ def _proto(lib):
         fn.argtypes = args
     for name in ("mha_decode_f32_cuda", "mha_decode_f16_cuda", "mha_decode_attn_f32_cuda",
                  "mha_decode_attn_f16_cuda", "mha_fused_f32_cuda", "mha_fused_f16_cuda",
-                 "causal_mask_f32_cuda"):
+                 "causal_mask_f32_cuda", "rope_f32_cuda", "rope_f16_cuda", "mha_decode_rope_f32_cuda",
+                 "mha_decode_rope_f16_cuda"):
         fn = getattr(lib, name)
         fn.restype = c_int
         fn.argtypes = [POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_void_p]

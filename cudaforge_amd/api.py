@@ -25,6 +25,18 @@ class MhaDecodeParams(ctypes.Structure):
     ]
 
 
+class RopeParams(ctypes.Structure):
+    """rope_params_t (include/rope_int.h; reference rope_int.h:6-11)."""
+
+    _fields_ = [("seq_len", c_int64), ("head_dim", c_int64), ("num_heads", c_int64), ("base", c_float)]
+
+
+class MhaDecodeRopeParams(ctypes.Structure):
+    """mha_decode_rope_params_t (include/rope_ops.h): decode params + the RoPE base."""
+
+    _fields_ = [("decode", MhaDecodeParams), ("rope_base", c_float), ("reserved", ctypes.c_int32)]
+
+
 class MhaFusedParams(ctypes.Structure):
     """mha_fused_params_t (include/mha_fused_int.h; reference mha_fused_int.h:7-17)."""
 

@@ -154,6 +154,37 @@ void cf_flash_set_mode(int32_t mode);
 /* CausalMask (S, S) float on the device. */
 int cf_launch_causal_mask(float* mask, int64_t S, void* stream);
 
+/* ---------------------------------------------------------------------------------
+ * Rotary position encoding (rope.hip).  Pair (2i, 2i+1) of every head at position pos
+ * is rotated by the angle whose (cos, sin) is table[pos * d/2 + i] (float2), computed on
+ * the host exactly as rope.c:38-45 does.  fp32 arithmetic without contraction, so the
+ * rotation matches the reference's CPU op bit for bit on the same table.
+ */
+typedef struct {
+    const void*  in;        /* (rows, H, d); rows = S */
+    void*        out;       /* may equal in */
+    const float* table;     /* (n_pos, d/2) x {cos, sin}; n_pos >= rows */
+    int64_t      rows;
+    int32_t      H, d;
+    int32_t      elem;      /* CF_ELEM_F32 / CF_ELEM_F16 */
+} cf_rope_args_t;
+int cf_launch_rope(const cf_rope_args_t* a, void* stream);
+
+/* Decode form: rotates, in place, Q (B, H_q, d) and the new K row of every sequence,
+ * k_cache[b, pos_b, :, :] of a (B, max_seq, H_kv, d) cache, at pos_b = lens[b] (or
+ * pos_uniform without lens); rows whose position is outside 0 .. max_seq-1 are skipped. */
+typedef struct {
+    void*          q;
+    void*          k_cache;
+    const float*   table;   /* n_pos >= max_seq */
+    const int32_t* lens;    /* may be NULL */
+    int64_t        pos_uniform;
+    int64_t        max_seq;
+    int32_t        B, H_q, H_kv, d;
+    int32_t        elem;
+} cf_rope_decode_args_t;
+int cf_launch_rope_decode(const cf_rope_decode_args_t* a, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,12 +5,14 @@
  * semantics, mha_decode_cuda.cu:159-198 for the GPU entry and registration), built as
  * three launches on the caller's stream:
  *   1. projection GEMV: X_new·[WQ | WK | WV] + b; Q goes to the workspace, K_new/V_new
- *      straight into row cache_len (or seq_lens[b]) of the output caches;
+ *      straight into row cache_len (or seq_lens[b]) of the output caches; the RoPE
+ *      variant (mha_decode_rope_*) then rotates Q and that K row in place;
  *   2. split-KV attention over positions 0..cache_len with the LSE merge;
  *   3. output GEMV: O·WO + bO -> Y.
  * Temporaries live in the persistent device workspace (no per-call allocation).
  */
 #include "mha_ops.h"
+#include "rope_ops.h"
 #include "gpu_ops.h"
 #include "op_common.h"
 #include "../kernels/kernels.h"
@@ -205,15 +207,20 @@ static int gemv_k_split(int elem, int64_t K, int64_t col_tiles, int64_t m_tiles)
     return (int)ks;
 }
 
+/* rope_base > 0: RoPE on Q and K_new between the projection and the attention. */
 static int decode_op(int elem, const void* inputs[], void* outputs[],
-                     const operator_params_t* params, stream_t* stream) {
-    if (!params || !inputs || !outputs) return -1;
+                     const mha_decode_params_t* p, float rope_base, stream_t* stream) {
+    if (!p || !inputs || !outputs) return -1;
     for (int i = 0; i < MHA_DECODE_NUM_INPUTS; i++) if (!inputs[i]) return -1;
     for (int i = 0; i < MHA_DECODE_NUM_OUTPUTS; i++) if (!outputs[i]) return -1;
-    const mha_decode_params_t* p = (const mha_decode_params_t*)params;
     decode_shape_t s;
     if (decode_shape(p, &s) != 0) return -1;
     if (s.H * s.d != s.D) return -1;
+    const float* rope_table = NULL;
+    if (rope_base > 0.0f) {
+        if (s.d & 1) return -1;
+        if (!(rope_table = rope_table_device(rope_base, s.d, s.max_seq))) return -1;
+    }
     const int32_t* lens = NULL;
     if (s.ragged) {
         lens = (const int32_t*)inputs[MHA_DECODE_SLOT_SEQLENS];
@@ -273,6 +280,23 @@ static int decode_op(int elem, const void* inputs[], void* outputs[],
     g1.partials = (float*)(data + off_p1);
     if ((rc = cf_launch_gemv(&g1, st)) != 0) return rc;
 
+    if (rope_table) {
+        cf_rope_decode_args_t r;
+        memset(&r, 0, sizeof(r));
+        r.q = data + off_q;
+        r.k_cache = outputs[1];
+        r.table = rope_table;
+        r.lens = lens;
+        r.pos_uniform = s.ragged ? 0 : s.cache_len;
+        r.max_seq = s.max_seq;
+        r.B = (int32_t)s.B;
+        r.H_q = (int32_t)s.H;
+        r.H_kv = (int32_t)s.H_kv;
+        r.d = (int32_t)s.d;
+        r.elem = elem;
+        if ((rc = cf_launch_rope_decode(&r, st)) != 0) return rc;
+    }
+
     a.q = data + off_q;
     a.k = outputs[1];
     a.v = outputs[2];
@@ -288,12 +312,41 @@ static int decode_op(int elem, const void* inputs[], void* outputs[],
 
 int mha_decode_f32_cuda(const void* inputs[], void* outputs[],
                         const operator_params_t* params, stream_t* stream) {
-    return decode_op(CF_ELEM_F32, inputs, outputs, params, stream);
+    return decode_op(CF_ELEM_F32, inputs, outputs, (const mha_decode_params_t*)params, 0.0f, stream);
 }
 
 int mha_decode_f16_cuda(const void* inputs[], void* outputs[],
                         const operator_params_t* params, stream_t* stream) {
-    return decode_op(CF_ELEM_F16, inputs, outputs, params, stream);
+    return decode_op(CF_ELEM_F16, inputs, outputs, (const mha_decode_params_t*)params, 0.0f, stream);
+}
+
+static int decode_rope(int elem, const void* inputs[], void* outputs[], const operator_params_t* params,
+                       stream_t* stream) {
+    const mha_decode_rope_params_t* rp = (const mha_decode_rope_params_t*)params;
+    if (!rp || !(rp->rope_base > 0.0f)) return -1;
+    return decode_op(elem, inputs, outputs, &rp->decode, rp->rope_base, stream);
+}
+
+int mha_decode_rope_f32_cuda(const void* inputs[], void* outputs[],
+                             const operator_params_t* params, stream_t* stream) {
+    return decode_rope(CF_ELEM_F32, inputs, outputs, params, stream);
+}
+
+int mha_decode_rope_f16_cuda(const void* inputs[], void* outputs[],
+                             const operator_params_t* params, stream_t* stream) {
+    return decode_rope(CF_ELEM_F16, inputs, outputs, params, stream);
+}
+
+int register_mha_decode_rope_f32_cuda(void) {
+    static const operator_registry_t reg = {"mha_decode_rope_f32_cuda", "f32", mha_decode_rope_f32_cuda, 1,
+                                            OP_FLAG_ALLOW_ALIAS};
+    return operator_register(&reg);
+}
+
+int register_mha_decode_rope_f16_cuda(void) {
+    static const operator_registry_t reg = {"mha_decode_rope_f16_cuda", "f16", mha_decode_rope_f16_cuda, 1,
+                                            OP_FLAG_ALLOW_ALIAS};
+    return operator_register(&reg);
 }
 
 /* Registrations (mha_decode_cuda.cu:192-198).  The attention-core entries are new. */

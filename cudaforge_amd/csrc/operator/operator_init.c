@@ -2,6 +2,7 @@
  * (X-macro expansion as in src/operator/operator_init.c:25-45). */
 #include "operator.h"
 #include "mha_ops.h"
+#include "rope_ops.h"
 
 int operator_init_all(void) {
     int ret = 0;

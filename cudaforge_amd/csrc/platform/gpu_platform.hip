@@ -263,7 +263,20 @@ void gpu_workspace_release(void) {
     }
 }
 
+static void (*g_at_finalize[8])(void);
+
+extern "C" int gpu_at_finalize(void (*fn)(void)) {
+    if (!fn) return -1;
+    for (auto& f : g_at_finalize) {
+        if (f == fn) return 0;
+        if (!f) { f = fn; return 0; }
+    }
+    return -1;
+}
+
 static void gpu_finalize_impl(void) {
+    for (auto f : g_at_finalize)
+        if (f) f();
     gpu_workspace_release();
     g_initialized_device = -1;
 }

@@ -112,6 +112,11 @@ void*  gpu_workspace_get(size_t bytes);
 size_t gpu_workspace_size(void);     /* bytes held on the current device, all streams */
 void   gpu_workspace_release(void);
 
+/* Registers fn to run at gpu_platform_finalize, before the workspaces are freed: for
+ * device tables an operator keeps across calls (the RoPE angle tables).  Up to 8
+ * callbacks; registering the same one again is a no-op.  0, or -1 when full. */
+int    gpu_at_finalize(void (*fn)(void));
+
 /* Allocation-failure injection for error-path tests: the next `n` device allocations
  * made through this module fail (return NULL).  n = 0 disables. */
 void  gpu_inject_alloc_failures(int n);

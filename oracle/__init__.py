@@ -17,6 +17,12 @@ Pinning status of each oracle function (see tests/test_oracle.py):
                           causal run == last row of a non-causal run over i+1 tokens),
                           GQA via repeated-KV equivalence.
   oracle_causal_mask_f32  pinned: vs the reference build (exact).
+  oracle_rope_f32         pinned: bit-exact vs the reference build (rope.c) on the
+                          tests/test_rope.c known-answer inputs and on larger seeded ones;
+                          norm preservation; position 0 = identity.
+  oracle_mha_decode_rope_f32  pinned: position 0 == plain decode (bit-exact); rotating the
+                          Q/K projection weights' output columns instead of Q and K_new
+                          gives the same result (fp32 rounding apart).
 """
 
 from __future__ import annotations
@@ -48,6 +54,11 @@ class FusedParams(ctypes.Structure):
                 ("scale", c_float), ("has_residual", ctypes.c_bool), ("causal", ctypes.c_bool)]
 
 
+class RopeParams(ctypes.Structure):
+    """rope_params_t (src/operator/nn/rope_int.h:6-11)."""
+    _fields_ = [("seq_len", c_int64), ("head_dim", c_int64), ("num_heads", c_int64), ("base", c_float)]
+
+
 def _build_if_missing(target: str, path: str) -> None:
     if not os.path.exists(path):
         subprocess.run(["make", "-C", HERE, target], check=True, stdout=subprocess.DEVNULL)
@@ -63,6 +74,8 @@ def lib():
         L.oracle_decode_attn_f32.argtypes = [F, F, F, F, c_int64, c_int64, c_int64, c_int64, c_int64,
                                              POINTER(c_int32), c_float]
         L.oracle_mha_fused_f32.argtypes = [POINTER(c_void_p), POINTER(c_void_p), c_void_p]
+        L.oracle_rope_f32.argtypes = [F, F, c_int64, c_int64, c_int64, c_float]
+        L.oracle_mha_decode_rope_f32.argtypes = [POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_float]
         L.oracle_causal_mask_f32.argtypes = [F, c_int64]
         L.oracle_causal_mask_f32.restype = None
         L.oracle_fill_normal.argtypes = [F, c_size_t, c_uint64, c_float, c_float]
@@ -98,7 +111,7 @@ def ref():
         if not ref_available():
             raise FileNotFoundError(REF_SO)
         L = ctypes.CDLL(REF_SO)
-        for n in ("mha_decode_f32", "mha_fused_f32", "causal_mask_f32"):
+        for n in ("mha_decode_f32", "mha_fused_f32", "causal_mask_f32", "rope_f32"):
             getattr(L, n).argtypes = [POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_void_p]
             getattr(L, n).restype = c_int
         _ref = L
@@ -221,6 +234,36 @@ def mha_fused(X, R, WQ, bQ, WK, bK, WV, bV, WO, bO, p: FusedParams, use_ref=Fals
     if rc != 0:
         raise ValueError(f"fused oracle returned {rc}")
     return Y
+
+
+def rope(x, base: float = 10000.0, use_ref=False) -> np.ndarray:
+    """RoPE op on x (S, H, d): row pos rotated by position pos (rope.c)."""
+    x = np.ascontiguousarray(x, np.float32)
+    S, H, d = x.shape
+    out = np.zeros_like(x)
+    if use_ref:
+        p = RopeParams(S, d, H, base)
+        rc = ref().rope_f32(_slots([x]), _slots([out]), ctypes.addressof(p), None)
+    else:
+        rc = lib().oracle_rope_f32(_fp(x), _fp(out), S, H, d, base)
+    if rc != 0:
+        raise ValueError(f"rope returned {rc}")
+    return out
+
+
+def mha_decode_rope(X, Kc, Vc, WQ, bQ, WK, bK, WV, bV, WO, bO, p: DecodeParams, rope_base: float,
+                    seq_lens=None):
+    """Decode op with RoPE on Q and K_new at the token's position; returns (Y, K_out, V_out)."""
+    arrs = [np.ascontiguousarray(a, np.float32) for a in (X, Kc, Vc, WQ, bQ, WK, bK, WV, bV, WO, bO)]
+    if seq_lens is not None:
+        arrs.append(np.ascontiguousarray(seq_lens, np.int32))
+    Y = np.zeros((p.batch_size, 1, p.hidden_size), np.float32)
+    Ko = np.zeros_like(arrs[1])
+    Vo = np.zeros_like(arrs[2])
+    rc = lib().oracle_mha_decode_rope_f32(_slots(arrs), _slots([Y, Ko, Vo]), ctypes.addressof(p), rope_base)
+    if rc != 0:
+        raise ValueError(f"decode rope oracle returned {rc}")
+    return Y, Ko, Vo
 
 
 def causal_mask(S: int, use_ref=False) -> np.ndarray:

@@ -17,7 +17,50 @@
  *   s_t = (Q·K_t)·scale with running max (:91-98), e_t = expf(s_t - max), sum (:101-105),
  *   clamp 1e-12 (:106), merged += (e_t / sum)·V_t (:109-114), y_j += Σ merged·WO (:117-121).
  * ---------------------------------------------------------------------------------- */
+/* RoPE of one position — src/operator/nn/rope.c:36-62: angle = pos / base^(2i/d) in
+ * float with powf, cosf, sinf; pair (2i, 2i+1) of each of the H heads of v (H x d)
+ * rotated by that angle. */
+void oracle_rope_at(float* v, int64_t H, int64_t d, int64_t pos, float base) {
+    const int64_t half_d = d / 2;
+    for (int64_t h = 0; h < H; h++) {
+        float* q = v + h * d;
+        for (int64_t i = 0; i < half_d; i++) {
+            const float angle = (float)pos / powf(base, (float)(2 * i) / (float)d);
+            const float c = cosf(angle);
+            const float s = sinf(angle);
+            const float x0 = q[2 * i];
+            const float x1 = q[2 * i + 1];
+            q[2 * i] = x0 * c - x1 * s;
+            q[2 * i + 1] = x0 * s + x1 * c;
+        }
+    }
+}
+
+/* RoPE op — src/operator/nn/rope.c:17-66: copy when not in place, then rotate row pos
+ * (H heads of d) by position pos for pos = 0 .. S-1. */
+int oracle_rope_f32(const float* in, float* out, int64_t S, int64_t H, int64_t d, float base) {
+    if (!in || !out || S < 0 || H <= 0 || d <= 0 || (d & 1)) return -1;
+    if (in != out) memcpy(out, in, (size_t)(S * H * d) * sizeof(float));
+    for (int64_t pos = 0; pos < S; pos++) oracle_rope_at(out + pos * H * d, H, d, pos, base);
+    return 0;
+}
+
+static int decode_impl(const void* inputs[], void* outputs[], const mha_decode_params_t* p, float rope_base);
+
 int oracle_mha_decode_f32(const void* inputs[], void* outputs[], const mha_decode_params_t* p) {
+    return decode_impl(inputs, outputs, p, 0.0f);
+}
+
+/* MHA_Decode with RoPE: the decode op above with rope.c's rotation applied to Q and to
+ * K_new at the token's position (cache_len, or the sequence's length when ragged)
+ * before K_new is appended and before the scores. */
+int oracle_mha_decode_rope_f32(const void* inputs[], void* outputs[], const mha_decode_params_t* p,
+                               float rope_base) {
+    if (!(rope_base > 0.0f)) return -1;
+    return decode_impl(inputs, outputs, p, rope_base);
+}
+
+static int decode_impl(const void* inputs[], void* outputs[], const mha_decode_params_t* p, float rope_base) {
     if (!p || !inputs || !outputs) return -1;
     for (int i = 0; i < 3; i++) if (!inputs[i]) return -1;
     if (!inputs[3] || !inputs[5] || !inputs[7] || !inputs[9]) return -1;
@@ -89,6 +132,7 @@ int oracle_mha_decode_f32(const void* inputs[], void* outputs[], const mha_decod
                 knew[di] = ka + (bK ? bK[kvo + di] : 0.0f);
                 vnew[di] = va + (bV ? bV[kvo + di] : 0.0f);
             }
+            if (rope_base > 0.0f) oracle_rope_at(knew, 1, d, cache_len, rope_base);
             const int64_t row = (b * max_seq + cache_len) * kv_dim + kvo;
             for (int64_t di = 0; di < d; di++) {
                 Ko[row + di] = knew[di];
@@ -104,6 +148,7 @@ int oracle_mha_decode_f32(const void* inputs[], void* outputs[], const mha_decod
                 for (int64_t j = 0; j < D; j++) acc += x[j] * WQ[j * D + ho + di];
                 q[di] = acc + (bQ ? bQ[ho + di] : 0.0f);
             }
+            if (rope_base > 0.0f) oracle_rope_at(q, 1, d, cache_len, rope_base);
             const int64_t total = cache_len + 1;
             float mx = -1e38f;
             for (int64_t t = 0; t < total; t++) {

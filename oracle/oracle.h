@@ -11,6 +11,10 @@
  *   oracle_decode_attn_f32  src/operator/nn/mha_decode.c:88-114 (attention core, Q given)
  *   oracle_mha_fused_f32    src/operator/nn/mha_fused.c:32-176
  *   oracle_causal_mask_f32  src/operator/nn/causal_mask.c:8-23
+ *   oracle_rope_f32, oracle_rope_at  src/operator/nn/rope.c:17-66
+ *   oracle_mha_decode_rope_f32  the decode op with rope.c's rotation of Q and K_new at
+ *                               the token's position (a composition the reference runs as
+ *                               two ops; no reference function computes it in one)
  * with the reference's fixed stack arrays (mha_decode.c:56,81,90,109) replaced by heap
  * buffers, GQA in the fused op (kv head = h / (H_q/H_kv), mha_decode.c:77), the causal
  * rule j <= i (mha_fused_cuda.cu:336, causal_mask.c:19) and ragged per-sequence cache
@@ -22,7 +26,11 @@
  *   - vs golden vectors written by that build (tests/golden/);
  *   - closed forms (T = 1, identical keys, one-hot scores), invariants (KV permutation,
  *     GQA == repeated-KV MHA, causal row == prefix attention, ragged == uniform) and a
- *     float64 brute force on tiny shapes.
+ *     float64 brute force on tiny shapes;
+ *   - RoPE: bit-exact vs the reference's rope.c built into oracle/_ref, the known-answer
+ *     inputs of tests/test_rope.c (srand(42)), norm preservation, position 0 = identity;
+ *     decode with RoPE: position 0 equals plain decode bit for bit, and rotating the
+ *     projection weights' output columns instead of Q and K_new gives the same result.
  */
 #ifndef CF_ORACLE_H_
 #define CF_ORACLE_H_
@@ -52,6 +60,14 @@ int oracle_decode_attn_f32(const float* Q, const float* K, const float* V, float
 int oracle_mha_fused_f32(const void* inputs[], void* outputs[], const mha_fused_params_t* p);
 
 void oracle_causal_mask_f32(float* mask, int64_t S);
+
+/* RoPE (rope.c): in/out (S, H, d), row pos rotated by position pos; in == out allowed. */
+int  oracle_rope_f32(const float* in, float* out, int64_t S, int64_t H, int64_t d, float base);
+/* One position: the H heads of v (H x d) rotated in place by position pos. */
+void oracle_rope_at(float* v, int64_t H, int64_t d, int64_t pos, float base);
+/* MHA_Decode with RoPE on Q and K_new (same slots as oracle_mha_decode_f32). */
+int  oracle_mha_decode_rope_f32(const void* inputs[], void* outputs[], const mha_decode_params_t* p,
+                                float rope_base);
 
 /* Seeded generators. */
 uint64_t oracle_splitmix64(uint64_t* state);
