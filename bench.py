@@ -46,9 +46,14 @@ def time_op(cf, name, inputs, outputs, params, stream, steps, warmup, extra=()):
     return _t(name, inputs, outputs, params, stream, warmup, steps, extra_inputs=extra)
 
 
+def normal(shape, seed, std=1.0):
+    """Seeded N(0, std) float32 synthetic data (numpy's PCG64; the GPU legs never call
+    the oracle)."""
+    return (np.random.default_rng(seed).standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
+
+
 def f16_normal(shape, seed, std=1.0):
-    import oracle as O
-    return O.to_f16(O.normal(shape, seed, 0.0, std))
+    return normal(shape, seed, std).astype(np.float16)
 
 
 # Independent input sets the decode legs rotate over: 3 x 268 MB of KV cache (plus the
@@ -109,9 +114,8 @@ def bench_decode_full(cf, stream, steps, warmup, f16=True, B=16, H=32, H_kv=8, d
     dt = np.float16 if f16 else np.float32
 
     def mk(shape, s, std=1.0):
-        import oracle as O
-        a = O.normal(shape, s, 0.0, std)
-        return cf.DeviceBuffer.from_numpy(O.to_f16(a) if f16 else a)
+        a = normal(shape, s, std)
+        return cf.DeviceBuffer.from_numpy(a.astype(np.float16) if f16 else a)
 
     input_sets, output_sets = [], []
     for i in range(n_sets):
@@ -137,9 +141,9 @@ def bench_decode_full(cf, stream, steps, warmup, f16=True, B=16, H=32, H_kv=8, d
 
 
 def bench_decode_ragged(cf, stream, steps, warmup):
-    import oracle as O
     B, H, H_kv, d, cap = 4, 32, 8, 128, 32768
-    lens = O.uniform_int(B, 404, 1024, cap) - 1        # cache_len_b; attended L_b = lens + 1
+    # Attended lengths L_b ~ U[1024, 32768] from a seed; cache_len_b = L_b - 1.
+    lens = np.random.default_rng(404).integers(1024, cap + 1, size=B).astype(np.int32) - 1
     L = cf.DeviceBuffer.from_numpy(lens.astype(np.int32))
     sets = [[cf.DeviceBuffer.from_numpy(f16_normal((B, H, d), 401 + 10 * i)),
              cf.DeviceBuffer.from_numpy(f16_normal((B, cap, H_kv, d), 402 + 10 * i)),
@@ -159,7 +163,6 @@ def bench_decode_graph(cf, steps, warmup, B=16, H=32, H_kv=8, d=128, T=4096, see
     the reference executor).  Host wall-clock per step, PCIe transfers included."""
     import ctypes
     from ctypes import POINTER, c_int, c_int64, c_void_p
-    import oracle as O
     lib = cf.load_library()
     D, kvd = H * d, H_kv * d
     g = lib.graph_create()
@@ -172,7 +175,7 @@ def bench_decode_graph(cf, steps, warmup, B=16, H=32, H_kv=8, d=128, T=4096, see
         ctypes.memmove(tt.data, arr.ctypes.data, arr.nbytes)
         return t, lib.graph_add_tensor(g, t)
 
-    mk = (lambda shape, s, std=1.0: O.to_f16(O.normal(shape, seed + s, 0.0, std)))
+    mk = (lambda shape, s, std=1.0: f16_normal(shape, seed + s, std))
     tX, iX = tensor(mk((B, 1, D), 1))
     _, iK = tensor(mk((B, T, H_kv, d), 2))
     _, iV = tensor(mk((B, T, H_kv, d), 3))
@@ -203,6 +206,21 @@ def bench_decode_graph(cf, steps, warmup, B=16, H=32, H_kv=8, d=128, T=4096, see
     ms = (time.perf_counter() - t_start) * 1e3 / steps
     lib.graph_destroy(g)
     return ms
+
+
+def bench_layer_neighbours(cf, stream, steps, warmup, rows=4096, D=768, F=3072, seed=900):
+    """LayerNorm (F16, BERT-base rows) and the FFN MatMul (F16, rows x D -> F with bias)."""
+    x = cf.DeviceBuffer.from_numpy(f16_normal((rows, D), seed))
+    g = cf.DeviceBuffer.from_numpy(f16_normal((D,), seed + 1, 0.1))
+    b = cf.DeviceBuffer.from_numpy(f16_normal((D,), seed + 2, 0.1))
+    y = cf.DeviceBuffer.empty((rows, D), np.float16)
+    ms_ln = time_op(cf, "layernorm_f16_cuda", [x, g, b], [y], cf.LayerNormParams(rows, D, 1e-12), stream, steps, warmup)
+    W = cf.DeviceBuffer.from_numpy(f16_normal((D, F), seed + 3, 0.02))
+    bias = cf.DeviceBuffer.from_numpy(f16_normal((F,), seed + 4, 0.02))
+    C = cf.DeviceBuffer.empty((rows, F), np.float16)
+    p = cf.MatmulParams(rows, F, D, False, False, 1, 0, 0, 0, 0)
+    ms_mm = time_op(cf, "matmul_f16_cuda", [x, W, bias], [C], p, stream, steps, warmup)
+    return ms_ln, 2 * rows * D * 2 + 2 * D * 2, ms_mm, 2 * rows * D * F
 
 
 def bench_fused(cf, stream, steps, warmup, B, S, H, d, causal, seed):
@@ -392,6 +410,13 @@ def main() -> int:
             extra[key] = {"us_per_step": round(ms_p * 1e3, 2), "TFLOP_s": round(tf, 1), "alg_flop": fl,
                           "mfma_frac": round(tf / FP16_PEAK_TFLOPS, 4)}
             log(f"  {ms_p * 1e3:.1f} us/step {tf:.1f} TFLOP/s")
+        log("layer neighbours: LayerNorm F16 (4096 x 768), FFN MatMul F16 (4096 x 768 -> 3072)")
+        ms_ln, by_ln, ms_mm, fl_mm = bench_layer_neighbours(cf, stream, max(steps // 4, 10), max(warmup // 2, 3))
+        extra["layernorm_f16_4096x768"] = {"us_per_step": round(ms_ln * 1e3, 2),
+                                           "GB_s": round(by_ln / (ms_ln * 1e-3) / 1e9, 1), "alg_bytes": by_ln}
+        extra["matmul_f16_ffn_4096x768x3072"] = {"us_per_step": round(ms_mm * 1e3, 2),
+                                                 "TFLOP_s": round(fl_mm / (ms_mm * 1e-3) / 1e12, 1), "alg_flop": fl_mm}
+        log(f"  LayerNorm {ms_ln * 1e3:.2f} us, MatMul {ms_mm * 1e3:.2f} us")
 
     cpu = None
     if not args.no_cpu:

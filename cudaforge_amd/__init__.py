@@ -13,6 +13,9 @@ from .api import (  # noqa: F401
     MhaFusedParams,
     MhaDecodeRopeParams,
     RopeParams,
+    LayerNormParams,
+    MatmulParams,
+    CastParams,
     CausalMaskParams,
     GraphMhaMatch,
     OperatorRegistry,
@@ -37,6 +40,9 @@ __all__ = [
     "MhaFusedParams",
     "MhaDecodeRopeParams",
     "RopeParams",
+    "LayerNormParams",
+    "MatmulParams",
+    "CastParams",
     "CausalMaskParams",
     "GraphMhaMatch",
     "OperatorRegistry",

@@ -37,6 +37,29 @@ class MhaDecodeRopeParams(ctypes.Structure):
     _fields_ = [("decode", MhaDecodeParams), ("rope_base", c_float), ("reserved", ctypes.c_int32)]
 
 
+class LayerNormParams(ctypes.Structure):
+    """layernorm_params_t (include/layernorm_int.h; reference layernorm_int.h:6-10)."""
+
+    _fields_ = [("N", c_int64), ("normalized_size", c_int64), ("epsilon", c_float)]
+
+
+class MatmulParams(ctypes.Structure):
+    """matmul_params_t (include/matmul_int.h; reference matmul_int.h:7-17)."""
+
+    _fields_ = [("M", c_int64), ("N", c_int64), ("K", c_int64), ("transpose_a", c_bool), ("transpose_b", c_bool),
+                ("batch_size", c_int64), ("stride_a", c_int64), ("stride_b", c_int64), ("stride_c", c_int64),
+                ("tuning_config", c_int)]
+
+
+class CastParams(ctypes.Structure):
+    """cast_params_t (include/cast_int.h; reference cast_int.h:12-16), ONNX dtype codes."""
+
+    _fields_ = [("src_dtype", c_int), ("dst_dtype", c_int), ("numel", c_int64)]
+
+
+ONNX_FLOAT, ONNX_FLOAT16, ONNX_INT64 = 1, 10, 7
+
+
 class MhaFusedParams(ctypes.Structure):
     """mha_fused_params_t (include/mha_fused_int.h; reference mha_fused_int.h:7-17)."""
 

@@ -300,12 +300,24 @@ static int run_node(inference_graph_t* g, const graph_node_t* n, bool use_cuda, 
     if (!op) return -2;
     const int on_gpu = use_cuda && strstr(name, "_cuda") != NULL;
 
-    const int in_slots = n->num_inputs + n->num_weights;
+    /* Input slots: tensor inputs, then weights, padded with NULLs to the count some ops
+     * always read (graph.c:886-895: activations 2, Conv/MatMul 3 for the optional bias,
+     * BatchNorm 6), so no op reads an output slot as an input. */
+    int in_slots = n->num_inputs + n->num_weights;
+    int reserve = 0;
+    switch (n->type) {
+        case OP_RELU: case OP_SIGMOID: case OP_GELU: case OP_SILU: case OP_EXP: case OP_TANH: reserve = 2; break;
+        case OP_CONV2D: case OP_MATMUL: reserve = 3; break;
+        case OP_BATCHNORM: reserve = 6; break;
+        default: break;
+    }
+    if (in_slots < reserve) in_slots = reserve;
     const int total = in_slots + n->num_outputs;
     const void* local[32];
     const void** slots = total <= 32 ? local : (const void**)malloc((size_t)total * sizeof(void*));
     if (!slots) return -1;
     void** outs = (void**)&slots[in_slots];
+    for (int i = n->num_inputs + n->num_weights; i < in_slots; i++) slots[i] = NULL;
 
     for (int i = 0; i < n->num_inputs && ret == 0; i++) {
         const int tid = n->input_tensors[i];

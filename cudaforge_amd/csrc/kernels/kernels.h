@@ -155,6 +155,34 @@ void cf_flash_set_mode(int32_t mode);
 int cf_launch_causal_mask(float* mask, int64_t S, void* stream);
 
 /* ---------------------------------------------------------------------------------
+ * Layer-neighbour kernels (layer_ops.hip) for the FP16 path around attention.
+ *
+ * LayerNorm over the last dimension (layernorm.c:96-120): per row, mean, population
+ * variance, y = (x - mean) / sqrt(var + eps) * gamma + beta, fp32 statistics.
+ */
+typedef struct {
+    const void* x;         /* (N, D) */
+    const void* gamma;     /* (D) */
+    const void* beta;      /* (D) */
+    void*       y;         /* (N, D); may equal x */
+    int64_t     N;
+    int32_t     D;
+    float       eps;
+    int32_t     elem;      /* all tensors CF_ELEM_F32 or all CF_ELEM_F16 */
+} cf_layernorm_args_t;
+int cf_launch_layernorm(const cf_layernorm_args_t* a, void* stream);
+
+/* Element conversions of the Cast op (cast_cuda.cu:6-64): kind selects the pair;
+ * f32 -> f16 rounds to nearest even, f32 -> i64 truncates toward zero. */
+enum { CF_CAST_I64_F32 = 0, CF_CAST_F32_I64 = 1, CF_CAST_F32_F16 = 2, CF_CAST_F16_F32 = 3 };
+int cf_launch_cast(const void* in, void* out, int64_t n, int32_t kind, void* stream);
+
+/* out (cols, rows) = in (rows, cols)^T for `batch` slices (strides in elements);
+ * elem_bytes 2 or 4. */
+int cf_launch_transpose(const void* in, void* out, int64_t rows, int64_t cols, int64_t batch,
+                        int64_t in_stride, int64_t out_stride, int32_t elem_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------
  * Rotary position encoding (rope.hip).  Pair (2i, 2i+1) of every head at position pos
  * is rotated by the angle whose (cos, sin) is table[pos * d/2 + i] (float2), computed on
  * the host exactly as rope.c:38-45 does.  fp32 arithmetic without contraction, so the

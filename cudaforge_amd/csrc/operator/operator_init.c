@@ -3,6 +3,7 @@
 #include "operator.h"
 #include "mha_ops.h"
 #include "rope_ops.h"
+#include "layer_ops.h"
 
 int operator_init_all(void) {
     int ret = 0;

@@ -17,6 +17,10 @@ Pinning status of each oracle function (see tests/test_oracle.py):
                           causal run == last row of a non-causal run over i+1 tokens),
                           GQA via repeated-KV equivalence.
   oracle_causal_mask_f32  pinned: vs the reference build (exact).
+  oracle_layernorm_f32    pinned: bit-exact vs the reference build (layernorm.c, scalar
+                          path); constant rows give beta.
+  oracle_matmul_f32       pinned: bit-exact vs the reference build (matmul.c) with
+                          transposes, batches and bias; identity matrices.
   oracle_rope_f32         pinned: bit-exact vs the reference build (rope.c) on the
                           tests/test_rope.c known-answer inputs and on larger seeded ones;
                           norm preservation; position 0 = identity.
@@ -54,6 +58,26 @@ class FusedParams(ctypes.Structure):
                 ("scale", c_float), ("has_residual", ctypes.c_bool), ("causal", ctypes.c_bool)]
 
 
+class LayerNormParams(ctypes.Structure):
+    """layernorm_params_t (src/operator/nn/layernorm_int.h:6-10)."""
+    _fields_ = [("N", c_int64), ("normalized_size", c_int64), ("epsilon", c_float)]
+
+
+class MatmulParams(ctypes.Structure):
+    """matmul_params_t (src/operator/blas/matmul_int.h:7-17)."""
+    _fields_ = [("M", c_int64), ("N", c_int64), ("K", c_int64), ("transpose_a", ctypes.c_bool),
+                ("transpose_b", ctypes.c_bool), ("batch_size", c_int64), ("stride_a", c_int64),
+                ("stride_b", c_int64), ("stride_c", c_int64), ("tuning_config", c_int)]
+
+
+class CastParams(ctypes.Structure):
+    """cast_params_t (src/operator/nn/cast_int.h:12-16); dtypes are ONNX codes."""
+    _fields_ = [("src_dtype", c_int), ("dst_dtype", c_int), ("numel", c_int64)]
+
+
+ONNX_FLOAT, ONNX_FLOAT16, ONNX_INT64 = 1, 10, 7
+
+
 class RopeParams(ctypes.Structure):
     """rope_params_t (src/operator/nn/rope_int.h:6-11)."""
     _fields_ = [("seq_len", c_int64), ("head_dim", c_int64), ("num_heads", c_int64), ("base", c_float)]
@@ -75,6 +99,9 @@ def lib():
                                              POINTER(c_int32), c_float]
         L.oracle_mha_fused_f32.argtypes = [POINTER(c_void_p), POINTER(c_void_p), c_void_p]
         L.oracle_rope_f32.argtypes = [F, F, c_int64, c_int64, c_int64, c_float]
+        L.oracle_layernorm_f32.argtypes = [F, F, F, F, c_int64, c_int64, c_float]
+        L.oracle_matmul_f32.argtypes = [F, F, F, F, c_int64, c_int64, c_int64, c_int, c_int, c_int64, c_int64,
+                                        c_int64, c_int64]
         L.oracle_mha_decode_rope_f32.argtypes = [POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_float]
         L.oracle_causal_mask_f32.argtypes = [F, c_int64]
         L.oracle_causal_mask_f32.restype = None
@@ -111,7 +138,8 @@ def ref():
         if not ref_available():
             raise FileNotFoundError(REF_SO)
         L = ctypes.CDLL(REF_SO)
-        for n in ("mha_decode_f32", "mha_fused_f32", "causal_mask_f32", "rope_f32"):
+        for n in ("mha_decode_f32", "mha_fused_f32", "causal_mask_f32", "rope_f32", "layernorm_f32", "cast_f32",
+                  "matmul_f32"):
             getattr(L, n).argtypes = [POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_void_p]
             getattr(L, n).restype = c_int
         _ref = L
@@ -234,6 +262,56 @@ def mha_fused(X, R, WQ, bQ, WK, bK, WV, bV, WO, bO, p: FusedParams, use_ref=Fals
     if rc != 0:
         raise ValueError(f"fused oracle returned {rc}")
     return Y
+
+
+def layernorm(x, gamma, beta, eps=1e-5, use_ref=False) -> np.ndarray:
+    """LayerNorm over the last axis of x (layernorm.c, scalar path)."""
+    x = np.ascontiguousarray(x, np.float32)
+    g = np.ascontiguousarray(gamma, np.float32)
+    b = np.ascontiguousarray(beta, np.float32)
+    D = x.shape[-1]
+    N = x.size // D
+    y = np.zeros_like(x)
+    if use_ref:
+        p = LayerNormParams(N, D, eps)
+        rc = ref().layernorm_f32(_slots([x, g, b]), _slots([y]), ctypes.addressof(p), None)
+    else:
+        rc = lib().oracle_layernorm_f32(_fp(x), _fp(g), _fp(b), _fp(y), N, D, eps)
+    if rc != 0:
+        raise ValueError(f"layernorm returned {rc}")
+    return y
+
+
+def matmul(A, B, bias=None, M=None, N=None, K=None, transpose_a=False, transpose_b=False, batch=1,
+           stride_a=0, stride_b=0, stride_c=0, use_ref=False) -> np.ndarray:
+    """matmul.c: C = A·B (+ bias) per batch slice; A, B flat or shaped, sizes explicit."""
+    A = np.ascontiguousarray(A, np.float32)
+    B = np.ascontiguousarray(B, np.float32)
+    bb = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    C = np.zeros(max(batch, 1) * M * N if batch > 1 else M * N, np.float32)
+    if batch > 1:
+        C = np.zeros((batch - 1) * stride_c + M * N, np.float32)
+    if use_ref:
+        p = MatmulParams(M, N, K, transpose_a, transpose_b, batch, stride_a, stride_b, stride_c, 0)
+        rc = ref().matmul_f32(_slots([A, B, bb]), _slots([C]), ctypes.addressof(p), None)
+    else:
+        rc = lib().oracle_matmul_f32(_fp(A), _fp(B), None if bb is None else _fp(bb), _fp(C), M, N, K,
+                                     int(transpose_a), int(transpose_b), batch, stride_a, stride_b, stride_c)
+    if rc != 0:
+        raise ValueError(f"matmul returned {rc}")
+    return C
+
+
+def cast_ref(x, src_dtype: int, dst_dtype: int) -> np.ndarray:
+    """The reference's CPU cast (cast.c), for the conversions it shares with its CUDA op."""
+    x = np.ascontiguousarray(x)
+    out_dt = {ONNX_FLOAT: np.float32, ONNX_FLOAT16: np.uint16, ONNX_INT64: np.int64}[dst_dtype]
+    out = np.zeros(x.size, out_dt)
+    p = CastParams(src_dtype, dst_dtype, x.size)
+    rc = ref().cast_f32(_slots([x]), _slots([out]), ctypes.addressof(p), None)
+    if rc != 0:
+        raise ValueError(rc)
+    return out.view(np.float16) if dst_dtype == ONNX_FLOAT16 else out
 
 
 def rope(x, base: float = 10000.0, use_ref=False) -> np.ndarray:

@@ -17,6 +17,55 @@
  *   s_t = (Q·K_t)·scale with running max (:91-98), e_t = expf(s_t - max), sum (:101-105),
  *   clamp 1e-12 (:106), merged += (e_t / sum)·V_t (:109-114), y_j += Σ merged·WO (:117-121).
  * ---------------------------------------------------------------------------------- */
+/* LayerNorm — src/operator/nn/layernorm.c:96-120 (the scalar path): per row, mean of x,
+ * population variance of (x - mean), inv_std = 1 / sqrtf(var/D + eps),
+ * y = (x - mean) * inv_std * gamma + beta, each sum accumulated in order. */
+int oracle_layernorm_f32(const float* x, const float* gamma, const float* beta, float* y,
+                         int64_t N, int64_t D, float eps) {
+    if (!x || !gamma || !beta || !y || N < 0 || D <= 0) return -1;
+    for (int64_t n = 0; n < N; n++) {
+        const float* xn = x + n * D;
+        float* yn = y + n * D;
+        float mean = 0.0f;
+        for (int64_t d = 0; d < D; d++) mean += xn[d];
+        mean /= (float)D;
+        float var = 0.0f;
+        for (int64_t d = 0; d < D; d++) {
+            const float diff = xn[d] - mean;
+            var += diff * diff;
+        }
+        var = var / (float)D + eps;
+        const float inv_std = 1.0f / sqrtf(var);
+        for (int64_t d = 0; d < D; d++) yn[d] = (xn[d] - mean) * inv_std * gamma[d] + beta[d];
+    }
+    return 0;
+}
+
+/* MatMul — src/operator/blas/matmul.c:14-50: per batch slice, C[i][j] = Σ_k a·b in k order
+ * (+ bias[j]), A (M, K) or, transposed, (K, M); B (K, N) or, transposed, (N, K). */
+int oracle_matmul_f32(const float* A, const float* B, const float* bias, float* C, int64_t M, int64_t N,
+                      int64_t K, int transpose_a, int transpose_b, int64_t batch, int64_t stride_a,
+                      int64_t stride_b, int64_t stride_c) {
+    if (!A || !B || !C || M < 0 || N < 0 || K < 0) return -1;
+    if (batch <= 0) batch = 1;
+    for (int64_t bi = 0; bi < batch; bi++) {
+        const float* Ab = A + bi * stride_a;
+        const float* Bb = B + bi * stride_b;
+        float* Cb = C + bi * stride_c;
+        for (int64_t i = 0; i < M; i++)
+            for (int64_t j = 0; j < N; j++) {
+                float sum = 0.0f;
+                for (int64_t k = 0; k < K; k++) {
+                    const float av = transpose_a ? Ab[k * M + i] : Ab[i * K + k];
+                    const float bv = transpose_b ? Bb[j * K + k] : Bb[k * N + j];
+                    sum += av * bv;
+                }
+                Cb[i * N + j] = sum + (bias ? bias[j] : 0.0f);
+            }
+    }
+    return 0;
+}
+
 /* RoPE of one position — src/operator/nn/rope.c:36-62: angle = pos / base^(2i/d) in
  * float with powf, cosf, sinf; pair (2i, 2i+1) of each of the H heads of v (H x d)
  * rotated by that angle. */

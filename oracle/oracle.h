@@ -12,6 +12,8 @@
  *   oracle_mha_fused_f32    src/operator/nn/mha_fused.c:32-176
  *   oracle_causal_mask_f32  src/operator/nn/causal_mask.c:8-23
  *   oracle_rope_f32, oracle_rope_at  src/operator/nn/rope.c:17-66
+ *   oracle_layernorm_f32    src/operator/nn/layernorm.c:85-122 (scalar path)
+ *   oracle_matmul_f32       src/operator/blas/matmul.c:14-50
  *   oracle_mha_decode_rope_f32  the decode op with rope.c's rotation of Q and K_new at
  *                               the token's position (a composition the reference runs as
  *                               two ops; no reference function computes it in one)
@@ -27,6 +29,8 @@
  *   - closed forms (T = 1, identical keys, one-hot scores), invariants (KV permutation,
  *     GQA == repeated-KV MHA, causal row == prefix attention, ragged == uniform) and a
  *     float64 brute force on tiny shapes;
+ *   - LayerNorm and MatMul: bit-exact vs layernorm.c / matmul.c built into oracle/_ref
+ *     (no USE_AVX2: the scalar path), plus closed forms (constant rows, identity matrices);
  *   - RoPE: bit-exact vs the reference's rope.c built into oracle/_ref, the known-answer
  *     inputs of tests/test_rope.c (srand(42)), norm preservation, position 0 = identity;
  *     decode with RoPE: position 0 equals plain decode bit for bit, and rotating the
@@ -60,6 +64,14 @@ int oracle_decode_attn_f32(const float* Q, const float* K, const float* V, float
 int oracle_mha_fused_f32(const void* inputs[], void* outputs[], const mha_fused_params_t* p);
 
 void oracle_causal_mask_f32(float* mask, int64_t S);
+
+/* LayerNorm over the last dimension: x, y (N, D); gamma, beta (D). */
+int  oracle_layernorm_f32(const float* x, const float* gamma, const float* beta, float* y,
+                          int64_t N, int64_t D, float eps);
+/* Batched MatMul with optional transposes and bias (bias may be NULL). */
+int  oracle_matmul_f32(const float* A, const float* B, const float* bias, float* C, int64_t M, int64_t N,
+                       int64_t K, int transpose_a, int transpose_b, int64_t batch, int64_t stride_a,
+                       int64_t stride_b, int64_t stride_c);
 
 /* RoPE (rope.c): in/out (S, H, d), row pos rotated by position pos; in == out allowed. */
 int  oracle_rope_f32(const float* in, float* out, int64_t S, int64_t H, int64_t d, float base);
