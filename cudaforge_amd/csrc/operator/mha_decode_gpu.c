@@ -67,7 +67,12 @@ static void plan_split(int elem, const decode_shape_t* s, int64_t t_max, int64_t
         const int64_t units = s->B * (fast ? s->H_kv : s->H);
         const int32_t ring_cu = cf_decode_attn_wgs_per_cu(elem, (int)s->d, G);
         const int64_t per_cu = ring_cu > 0 ? ring_cu : 4;
-        const int64_t target = per_cu * (int64_t)cf_cu_count();
+        int64_t target = per_cu * (int64_t)cf_cu_count();
+        /* Ragged: the grid spans max_seq, but a sequence only runs the splits its length
+         * reaches, so plan four times as many (shorter) splits; the busy ones then fill
+         * the CUs and rebalance as short sequences finish.  Measured on config 4 shapes:
+         * 1-17 % faster than one split per CU slot. */
+        if (s->ragged) target *= 4;
         int64_t n = cf_ceil_div(target, units);
         const int64_t nmax = cf_ceil_div(t_max, q);
         if (n > nmax) n = nmax;
