@@ -227,9 +227,12 @@ void flash_f16(cf_flash_args_t a) {
 // (global_load_lds_dwordx4) into a kFlashStages-deep LDS ring instead of through
 // registers, so kFlashStages - 1 key blocks are in flight while one is used and no
 // wave waits on a block's loads before storing them.  K rows (128 B) and V^T rows (64
-// keys, 128 B) are XOR-swizzled in 16-byte chunks (chunk ^ (row / 2) % 8) so the K
-// fragment reads (16 rows, one chunk) and the V^T fragment reads (16 rows, 8 bytes) are
-// bank-conflict free.  Rows and chunks past the sequence end are clamped to the last
+// keys, 128 B) are XOR-swizzled in 16-byte chunks so the K fragment reads (16 rows, one
+// chunk: chunk ^ (row / 2) % 8) and the V^T fragment reads (16 rows, 8 bytes: chunk ^
+// (row / 2 ^ row / 16) % 8) are bank-conflict free.  The V^T term in row / 16 makes the
+// reads of row blocks u and u+1 differ by more than a constant, so the compiler keeps
+// them as separate ds_read_b64 instead of pairing them into ds_read2st64_b64, which
+// measured four times the LDS cycles (SQ_LDS_BANK_CONFLICT) on gfx950.  Rows and chunks past the sequence end are clamped to the last
 // valid ones (S % 8 == 0 keeps every 8-key chunk whole) and get p = 0.  The row max is
 // reduced with the gfx950 row swaps, and the running max only moves when a block
 // exceeds it by more than kLazy (log2 units), so the accumulators are rarely rescaled.
@@ -237,6 +240,7 @@ constexpr int kFlashStages = 3;
 constexpr float kLazy = 8.0f;
 
 __device__ __forceinline__ int fswz(int row) { return (row >> 1) & 7; }
+__device__ __forceinline__ int vswz(int row) { return ((row >> 1) ^ (row >> 4)) & 7; }
 
 template <int NJ>
 __global__ __launch_bounds__(kThreads, 3)
@@ -296,7 +300,7 @@ void flash_f16_dma64(cf_flash_args_t a) {
             const int kc = dch ^ fswz(row);
             lds_dma16(kp + (size_t)min(k0 + row, S - 1) * D + 8 * kc,
                       __builtin_amdgcn_readfirstlane(kb + (uint32_t)(16 * wave + 8 * u) * 128u));
-            const int vcol = min(k0 + 8 * (dch ^ fswz(row)), S - 8);
+            const int vcol = min(k0 + 8 * (dch ^ vswz(row)), S - 8);
             lds_dma16(vp + (size_t)row * S + vcol,
                       __builtin_amdgcn_readfirstlane(vb + (uint32_t)(16 * wave + 8 * u) * 128u));
         }
@@ -319,7 +323,7 @@ void flash_f16_dma64(cf_flash_args_t a) {
             for (int hh = 0; hh < 2; hh++) {
                 const int row = 16 * u + lr;
                 const int ch = 4 * s2 + 2 * hh + (lq >> 1);          // keys 32s + 16hh + 4lq
-                v_rd[u][s2][hh] = TILE + row * kKB + 8 * (ch ^ fswz(row)) + 4 * (lq & 1);
+                v_rd[u][s2][hh] = TILE + row * kKB + 8 * (ch ^ vswz(row)) + 4 * (lq & 1);
             }
 
     const float c = a.scale * kLog2e;

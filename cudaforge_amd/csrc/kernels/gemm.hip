@@ -40,6 +40,7 @@ struct Tiling {
     int a_vec;          // A rows may be read with vector loads (alignment and K)
     int w_vec[3];       // W rows of segment s may be read with vector loads
     int epi_vec;        // fp16 epilogue may use 8-element stores (alignment and shape)
+    int group_m;        // tile rows per group of the XCD-aware tile order
 };
 
 __device__ __forceinline__ float to_f(float x) { return x; }
@@ -54,15 +55,15 @@ template <typename T> __device__ __forceinline__ T from_f(float x) { return (T)x
 constexpr int kXcds = 8;
 constexpr int kGroupM = 4;
 
-__device__ __forceinline__ void tile_of_block(int blk, int tiles_m, int tiles_n, int& tm, int& tn) {
+__device__ __forceinline__ void tile_of_block(int blk, int tiles_m, int tiles_n, int group_m, int& tm, int& tn) {
     const int T = tiles_m * tiles_n;
     const int x = blk % kXcds, j = blk / kXcds;
     const int base = T / kXcds, rem = T % kXcds;
     const int t = x * base + min(x, rem) + j;      // position in the tile order
-    const int per_group = kGroupM * tiles_n;
+    const int per_group = group_m * tiles_n;
     const int g = t / per_group;
-    const int first_m = g * kGroupM;
-    const int gm = min(tiles_m - first_m, kGroupM);
+    const int first_m = g * group_m;
+    const int gm = min(tiles_m - first_m, group_m);
     const int r = t - g * per_group;
     tm = first_m + r % gm;
     tn = r / gm;
@@ -211,7 +212,7 @@ void gemm_f16(cf_gemm_args_t a, Tiling t) {
     __shared__ __attribute__((aligned(16))) _Float16 smem[2 * (A_STAGE + W_STAGE)];
 
     int tile_m, tile_n;
-    tile_of_block(blockIdx.x, t.n_tiles_m, t.seg_start[3], tile_m, tile_n);
+    tile_of_block(blockIdx.x, t.n_tiles_m, t.seg_start[3], t.group_m, tile_m, tile_n);
     const int seg = find_seg(a, t, tile_n);
     const int N = a.n[seg];
     const int m0 = tile_m * BM;
@@ -382,7 +383,10 @@ constexpr int A_ST = BM * BKA;          // halves per stage: A [128][32]
 constexpr int W_ST = BKA * BN;          //                   W [32][128]
 constexpr int ST = A_ST + W_ST;         // 16 KB per stage
 
-__device__ __forceinline__ int swz_a(int row) { return (row >> 2) & 3; }
+// A rows are 64 B (4 chunks).  (row >> 1) & 3 is the permutation under which the
+// fragment reads (ds_read_b128, 16 rows x one chunk) measure conflict-free on gfx950
+// (SQ_LDS_BANK_CONFLICT); (row >> 2) & 3 and row & 3 both measure two-way conflicts.
+__device__ __forceinline__ int swz_a(int row) { return (row >> 1) & 3; }
 __device__ __forceinline__ int swz_w(int row) { return ((row & 3) << 1) ^ (((row >> 3) & 1) << 3); }
 
 // STAGES = 4 (64 KB, two workgroups per CU) or 3 (48 KB, three per CU): the launcher
@@ -394,7 +398,7 @@ void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
     __shared__ __attribute__((aligned(16))) _Float16 smem[STAGES * ST];
 
     int tile_m, tile_n;
-    tile_of_block(blockIdx.x, t.n_tiles_m, t.seg_start[3], tile_m, tile_n);
+    tile_of_block(blockIdx.x, t.n_tiles_m, t.seg_start[3], t.group_m, tile_m, tile_n);
     const int seg = find_seg(a, t, tile_n);
     const int N = a.n[seg];
     const int K = a.K;
@@ -503,7 +507,7 @@ void gemm_f32(cf_gemm_args_t a, Tiling t) {
     __shared__ float Bs[BK32 * LDM32];   // [k][n]
 
     int tile_m, tile_n;
-    tile_of_block(blockIdx.x, t.n_tiles_m, t.seg_start[3], tile_m, tile_n);
+    tile_of_block(blockIdx.x, t.n_tiles_m, t.seg_start[3], t.group_m, tile_m, tile_n);
     const int seg = find_seg(a, t, tile_n);
     const int N = a.n[seg];
     const int m0 = tile_m * BM;
@@ -584,6 +588,10 @@ int g_gemm_stages = 0;   // tuning override of the direct-to-LDS kernel's ring d
 
 extern "C" void cf_gemm_set_stages(int32_t stages) { g_gemm_stages = stages; }
 
+int g_gemm_group_m = 0;  // tuning override of the tile-order group height (0 = kGroupM)
+
+extern "C" void cf_gemm_set_group_m(int32_t group_m) { g_gemm_group_m = group_m > 0 ? group_m : 0; }
+
 extern "C" int cf_launch_gemm(const cf_gemm_args_t* a, void* stream) {
     if (a->nseg < 1 || a->nseg > 3 || a->M <= 0 || a->K <= 0) return (int)hipErrorInvalidValue;
     Tiling t{};
@@ -607,6 +615,7 @@ extern "C" int cf_launch_gemm(const cf_gemm_args_t* a, void* stream) {
     if (a->out_kind == CF_GEMM_OUT_ROWMAJOR) ev = ev && a->n[0] % 8 == 0;
     else ev = ev && a->d % 8 == 0 && a->S % 8 == 0;
     t.epi_vec = ev;
+    t.group_m = g_gemm_group_m > 0 ? g_gemm_group_m : kGroupM;
     const long long blocks = (long long)acc * t.n_tiles_m;
     if (blocks <= 0 || blocks > 0x7fffffffLL) return (int)hipErrorInvalidValue;
     dim3 grid((unsigned)blocks);

@@ -129,6 +129,8 @@ int cf_launch_gemm(const cf_gemm_args_t* a, void* stream);
 /* Tuning override of the fp16 direct-to-LDS GEMM's ring depth (3 or 4 stages; 0 =
  * automatic: 3, i.e. three workgroups per CU, when there are more than two tiles per CU). */
 void cf_gemm_set_stages(int32_t stages);
+/* Tuning override of the tile order's group height (M tiles per group; 0 = default). */
+void cf_gemm_set_group_m(int32_t group_m);
 
 /* ---------------------------------------------------------------------------------
  * Prefill attention (flash style, online softmax): q (B, H_q, S, d), k (B, H_kv, S, d),
