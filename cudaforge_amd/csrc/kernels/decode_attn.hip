@@ -658,6 +658,63 @@ void merge_rows(cf_decode_attn_args_t a, int Gx, int units_per_b) {
     }
 }
 
+// Merge, one wave per output row (D = 64 or 128; DPL = D / 64 dims per lane), four rows
+// per workgroup, no LDS: lane s holds (m, l) of splits s, s + 64, ...; the wave reduces
+// M = max m and den = sum 2^(m - M) l with shuffles, then accumulates the splits'
+// accumulator rows weighted by 2^(m_s - M) (broadcast from lane s % 64), eight in flight.
+template <typename T, int DPL>
+__global__ __launch_bounds__(256)
+void merge_wave(cf_decode_attn_args_t a, int Gx, int units_per_b, int rows) {
+    constexpr int D = 64 * DPL;
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int g = row % Gx, unit = row / Gx, b = unit / units_per_b;
+    const int nsplit = (attended(a, b) + a.chunk - 1) / a.chunk;
+    if (nsplit <= 1) return;                       // finished by the split kernel
+    const int stride = part_stride(Gx, D), hdr = part_hdr(Gx);
+    const float* part = a.partials + (size_t)unit * a.n_split * stride;
+    float M = -INFINITY;
+    for (int sp = lane; sp < nsplit; sp += 64) M = fmaxf(M, part[(size_t)sp * stride + g]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    float den = 0.0f;
+    float num[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; e++) num[e] = 0.0f;
+    for (int s0 = 0; s0 < nsplit; s0 += 64) {
+        const int sp = s0 + lane;
+        float w = 0.0f;
+        if (sp < nsplit) {
+            w = exp2f(part[(size_t)sp * stride + g] - M);
+            den = __builtin_fmaf(w, part[(size_t)sp * stride + Gx + g], den);
+        }
+        const int n = min(64, nsplit - s0);
+        for (int j0 = 0; j0 < n; j0 += 8) {
+            float ws[8];
+            float av[8][DPL];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                ws[j] = __shfl(w, j0 + j, 64);
+                const bool ok = j0 + j < n;
+                const float* ps = part + (size_t)(s0 + (ok ? j0 + j : 0)) * stride + hdr + g * D + DPL * lane;
+#pragma unroll
+                for (int e = 0; e < DPL; e++) av[j][e] = ok ? ps[e] : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+#pragma unroll
+                for (int e = 0; e < DPL; e++) num[e] = __builtin_fmaf(ws[j], av[j][e], num[e]);
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) den += __shfl_xor(den, off, 64);
+    const float inv = 1.0f / den;
+    T* out = (T*)a.o + (size_t)row * D + DPL * lane;
+#pragma unroll
+    for (int e = 0; e < DPL; e++) out[e] = from_f<T>(num[e] * inv);
+}
+
 bool fast_supported(int elem, int d, int G) {
     (void)elem;
     return (d == 64 || d == 128) && (G == 1 || G == 2 || G == 4 || G == 8);
@@ -676,6 +733,7 @@ bool use_fast(const cf_decode_attn_args_t* a) {
 }
 
 int g_stages = 0;   // tuning override of the fp16 ring depth (2..4; 0 = kDecodeStages)
+int g_merge_rows = 0;   // 1: use the workgroup-per-row merge for every head size (tests)
 
 int f16_stages() { return g_stages >= 2 && g_stages <= 4 ? g_stages : kDecodeStages; }
 
@@ -721,6 +779,8 @@ extern "C" int32_t cf_decode_attn_chunk_quantum(int32_t elem, int32_t d, int32_t
 
 extern "C" void cf_decode_attn_set_stages(int32_t stages) { g_stages = stages; }
 
+extern "C" void cf_decode_attn_set_merge_rows(int32_t on) { g_merge_rows = on != 0; }
+
 extern "C" int32_t cf_decode_attn_wgs_per_cu(int32_t elem, int32_t d, int32_t group) {
     if (elem != CF_ELEM_F16 || !fast_supported(elem, d, group)) return 0;
     const int n = kLdsPerCu / f16_lds_bytes(d, group, f16_stages());
@@ -765,6 +825,18 @@ extern "C" int cf_launch_decode_attn_merge(const cf_decode_attn_args_t* a, void*
     const bool fast = use_fast(a);
     const int Gx = fast ? a->H_q / a->H_kv : 1;
     const int units_per_b = fast ? a->H_kv : a->H_q;
+    const int rows = a->B * units_per_b * Gx;
+    if ((a->d == 64 || a->d == 128) && !g_merge_rows) {
+        const dim3 grid((unsigned)((rows + 3) / 4)), blk(256);
+        if (a->elem == CF_ELEM_F16) {
+            if (a->d == 64) hipLaunchKernelGGL((merge_wave<_Float16, 1>), grid, blk, 0, s, *a, Gx, units_per_b, rows);
+            else hipLaunchKernelGGL((merge_wave<_Float16, 2>), grid, blk, 0, s, *a, Gx, units_per_b, rows);
+        } else {
+            if (a->d == 64) hipLaunchKernelGGL((merge_wave<float, 1>), grid, blk, 0, s, *a, Gx, units_per_b, rows);
+            else hipLaunchKernelGGL((merge_wave<float, 2>), grid, blk, 0, s, *a, Gx, units_per_b, rows);
+        }
+        return (int)hipGetLastError();
+    }
     if (a->d % 4 == 0 && a->d / 4 <= kMergeThreads) {
         dim3 grid((unsigned)((size_t)a->B * units_per_b * Gx));
         if (a->elem == CF_ELEM_F16)

@@ -49,6 +49,9 @@ int32_t cf_decode_attn_chunk_max(int32_t elem, int32_t d, int32_t group);
 int32_t cf_decode_attn_wgs_per_cu(int32_t elem, int32_t d, int32_t group);
 /* Tuning override of the fp16 split kernel's LDS ring depth (2..4; 0 = default 3). */
 void    cf_decode_attn_set_stages(int32_t stages);
+/* Tests: 1 selects the workgroup-per-row merge for every head size (0 = the one-wave
+ * merge for d = 64 / 128). */
+void    cf_decode_attn_set_merge_rows(int32_t on);
 /* Workspace floats needed for the partials of a launch. */
 size_t  cf_decode_attn_partials_floats(int32_t B, int32_t H_q, int32_t H_kv, int32_t d,
                                        int32_t n_split, int32_t elem);

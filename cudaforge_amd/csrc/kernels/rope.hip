@@ -32,18 +32,18 @@ __device__ __forceinline__ void rotate(const T* in, T* out, float2 cs) {
     st(out + 1, c + e);
 }
 
-// (rows, H, d): pair index -> (row = position, head, i).
-template <typename T>
+// (rows, H, d): pair index -> (row = position, head, i).  I is the index type: 32-bit
+// when the pair count fits (integer division is far cheaper), else 64-bit.
+template <typename T, typename I>
 __global__ __launch_bounds__(kThreads) void rope_rows(cf_rope_args_t a) {
-    const int half = a.d >> 1;
-    const int64_t total = a.rows * a.H * half;
-    for (int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x; idx < total;
-         idx += (int64_t)gridDim.x * kThreads) {
-        const int i = (int)(idx % half);
-        const int64_t rh = idx / half;              // row * H + h
-        const int64_t pos = rh / a.H;
+    const I half = (I)(a.d >> 1), H = (I)a.H;
+    const I total = (I)a.rows * H * half;
+    for (I idx = (I)blockIdx.x * kThreads + threadIdx.x; idx < total; idx += (I)gridDim.x * kThreads) {
+        const I i = idx % half;
+        const I rh = idx / half;                    // row * H + h
+        const I pos = rh / H;
         const size_t off = (size_t)rh * a.d + 2 * i;
-        rotate((const T*)a.in + off, (T*)a.out + off, ((const float2*)a.table)[pos * half + i]);
+        rotate((const T*)a.in + off, (T*)a.out + off, ((const float2*)a.table)[(size_t)pos * half + i]);
     }
 }
 
@@ -51,12 +51,11 @@ __global__ __launch_bounds__(kThreads) void rope_rows(cf_rope_args_t a) {
 template <typename T>
 __global__ __launch_bounds__(kThreads) void rope_decode(cf_rope_decode_args_t a) {
     const int half = a.d >> 1, heads = a.H_q + a.H_kv;
-    const int64_t total = (int64_t)a.B * heads * half;
-    for (int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x; idx < total;
-         idx += (int64_t)gridDim.x * kThreads) {
-        const int i = (int)(idx % half);
-        const int64_t bh = idx / half;
-        const int h = (int)(bh % heads), b = (int)(bh / heads);
+    const int total = a.B * heads * half;           // < 2^31: checked by the launcher
+    for (int idx = blockIdx.x * kThreads + threadIdx.x; idx < total; idx += gridDim.x * kThreads) {
+        const int i = idx % half;
+        const int bh = idx / half;
+        const int h = bh % heads, b = bh / heads;
         const int64_t pos = a.lens ? (int64_t)a.lens[b] : a.pos_uniform;
         if (pos < 0 || pos >= a.max_seq) continue;
         T* p = h < a.H_q ? (T*)a.q + ((size_t)b * a.H_q + h) * a.d
@@ -78,10 +77,15 @@ extern "C" int cf_launch_rope(const cf_rope_args_t* a, void* stream) {
     const int64_t total = a->rows * a->H * (a->d / 2);
     if (total == 0) return 0;
     hipStream_t s = (hipStream_t)stream;
-    if (a->elem == CF_ELEM_F16)
-        hipLaunchKernelGGL(rope_rows<_Float16>, dim3(grid_for(total)), dim3(kThreads), 0, s, *a);
-    else
-        hipLaunchKernelGGL(rope_rows<float>, dim3(grid_for(total)), dim3(kThreads), 0, s, *a);
+    const dim3 g(grid_for(total)), b(kThreads);
+    const bool narrow = total < (1LL << 31) - 65536LL * kThreads;
+    if (a->elem == CF_ELEM_F16) {
+        if (narrow) hipLaunchKernelGGL((rope_rows<_Float16, int32_t>), g, b, 0, s, *a);
+        else hipLaunchKernelGGL((rope_rows<_Float16, int64_t>), g, b, 0, s, *a);
+    } else {
+        if (narrow) hipLaunchKernelGGL((rope_rows<float, int32_t>), g, b, 0, s, *a);
+        else hipLaunchKernelGGL((rope_rows<float, int64_t>), g, b, 0, s, *a);
+    }
     return (int)hipGetLastError();
 }
 
@@ -90,6 +94,7 @@ extern "C" int cf_launch_rope_decode(const cf_rope_decode_args_t* a, void* strea
         (a->d & 1) || a->max_seq <= 0)
         return (int)hipErrorInvalidValue;
     const int64_t total = (int64_t)a->B * (a->H_q + a->H_kv) * (a->d / 2);
+    if (total >= (1LL << 31) - 65536LL * kThreads) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
     if (a->elem == CF_ELEM_F16)
         hipLaunchKernelGGL(rope_decode<_Float16>, dim3(grid_for(total)), dim3(kThreads), 0, s, *a);

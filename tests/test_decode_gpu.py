@@ -381,3 +381,26 @@ def test_split_chunks_longer_than_4096(gpu, native):
         native.mha_decode_set_split_chunk(0)
     want = O.decode_attn(Q, K, V, np.full(B, T, np.int32), float(1 / np.sqrt(d)), H_kv)
     assert max_abs(want, got) <= TOL16
+
+
+@pytest.mark.parametrize("f16,d,G", [(True, 128, 4), (True, 64, 2), (False, 64, 1), (False, 128, 8)])
+def test_merge_kernels_agree(gpu, native, f16, d, G):
+    """The one-wave merge (d = 64 / 128) and the workgroup-per-row merge on the same
+    partials: both within the bound of the oracle, and close to each other."""
+    B, H_kv, T = 3, 2, 3000
+    H = H_kv * G
+    r = O.round_f16 if f16 else (lambda a: a)
+    Q, K, V = (r(O.normal(s, 140 + i)) for i, s in enumerate([(B, H, d), (B, T, H_kv, d), (B, T, H_kv, d)]))
+    lens = [2999, 17, 1500]
+    want = O.decode_attn(Q, K, V, np.asarray([l + 1 for l in lens], np.int32), float(1 / np.sqrt(d)), H_kv)
+    outs = []
+    try:
+        for rows in (0, 1):
+            native.cf_decode_attn_set_merge_rows(rows)
+            outs.append(run_decode_attn_gpu(Q, K, V, None, H_kv, f16, seq_lens=lens))
+    finally:
+        native.cf_decode_attn_set_merge_rows(0)
+    tol = TOL16 if f16 else TOL32
+    for got in outs:
+        assert max_abs(want, got) <= tol
+    assert max_abs(outs[0], outs[1]) <= tol
