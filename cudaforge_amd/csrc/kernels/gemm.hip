@@ -310,63 +310,94 @@ void gemm_f16(cf_gemm_args_t a, Tiling t) {
 }
 
 // Epilogues of the pipelined kernel, straight from the accumulators (no LDS pass).
-// Full tiles only, with the 8-byte alignment the launcher's epi_vec check implies.
-//
+// Full tiles only, with the alignment the launcher's epi_vec check implies (16 bytes).
+// Each lane first holds four consecutive outputs of one 16x16 MFMA tile; a row swap
+// with the lane 16 apart (v_permlane16_swap) between two neighbouring tiles gives each
+// lane eight consecutive outputs, so the stores are 16 bytes (measured: 16-row x 32-byte
+// 8-byte stores take ~1.7x as long as 16-row x 64-byte 16-byte ones for this output).
+// After swap(a = tile B, b = tile A), even lane rows (lq = 0, 2) hold tile B's four
+// values then the partner's next four, odd rows the partner's tile-A four then their own.
+__device__ __forceinline__ uint2 pack4(float x0, float x1, float x2, float x3) {
+    return __builtin_bit_cast(uint2, h4_t{(_Float16)x0, (_Float16)x1, (_Float16)x2, (_Float16)x3});
+}
+
+__device__ __forceinline__ void pair_swap(uint2& tb, uint2& ta) {
+    float a0 = __builtin_bit_cast(float, tb.x), b0 = __builtin_bit_cast(float, ta.x);
+    float a1 = __builtin_bit_cast(float, tb.y), b1 = __builtin_bit_cast(float, ta.y);
+    swap_xor16(a0, b0);
+    swap_xor16(a1, b1);
+    tb = uint2{__builtin_bit_cast(uint32_t, a0), __builtin_bit_cast(uint32_t, a1)};
+    ta = uint2{__builtin_bit_cast(uint32_t, b0), __builtin_bit_cast(uint32_t, b1)};
+}
+
 // Columns-contiguous destinations (row-major C, head-major q and k): the main loop
 // accumulates C^T (MFMA operands swapped), so acc[i][j][e] = C[m][n + e] with
-// m = m0 + wm + 16i + lr and n = n0 + wn + 16j + 4lq: four consecutive columns of one
-// row, one 8-byte store.  Bias, then the residual, are added in fp32 before the single
-// rounding to fp16.
+// m = m0 + wm + 16i + lr and n = n0 + wn + 16j + 4lq.  Tiles j = 2p, 2p+1 pair up; the
+// lane then stores C[m][n0 + wn + 32p + 16 * (lq even) + 8 * (lq / 2) .. +7].  Bias, then
+// the residual, are added in fp32 before the single rounding to fp16.
 __device__ __forceinline__ void store_ct_f16(const cf_gemm_args_t& a, int seg, int m0, int n0, int wm, int wn,
                                              int lr, int lq, const f4_t (&acc)[4][4]) {
     const _Float16* __restrict__ bias = (const _Float16*)a.bias[seg];
     const _Float16* __restrict__ res = a.out_kind == CF_GEMM_OUT_ROWMAJOR ? (const _Float16*)a.residual : nullptr;
     _Float16* __restrict__ out = (_Float16*)a.out[seg];
+    const bool odd = lq & 1;
     float bv[4][4];
-    size_t cp[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int n = n0 + wn + 16 * j + 4 * lq;
-        cp[j] = col_part(a, seg, n);
 #pragma unroll
         for (int e = 0; e < 4; e++) bv[j][e] = bias ? (float)bias[n + e] : 0.0f;
     }
+    size_t cp[2];
+#pragma unroll
+    for (int p = 0; p < 2; p++) cp[p] = col_part(a, seg, n0 + wn + 32 * p + (odd ? 0 : 16) + 8 * (lq >> 1));
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const size_t rp = row_part(a, seg, m0 + wm + 16 * i + lr);
+        const int m = m0 + wm + 16 * i + lr;
+        const size_t rp = row_part(a, seg, m);
+        uint2 t[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const size_t off = rp + cp[j];
             float f[4];
 #pragma unroll
             for (int e = 0; e < 4; e++) f[e] = acc[i][j][e] + bv[j][e];
             if (res) {
-                const h4_t r = *(const h4_t*)(res + off);
+                const h4_t r = *(const h4_t*)(res + rp + col_part(a, seg, n0 + wn + 16 * j + 4 * lq));
 #pragma unroll
                 for (int e = 0; e < 4; e++) f[e] += (float)r[e];
             }
-            *(h4_t*)(out + off) = h4_t{(_Float16)f[0], (_Float16)f[1], (_Float16)f[2], (_Float16)f[3]};
+            t[j] = pack4(f[0], f[1], f[2], f[3]);
+        }
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            pair_swap(t[2 * p + 1], t[2 * p]);
+            *(uint4*)(out + rp + cp[p]) = uint4{t[2 * p + 1].x, t[2 * p + 1].y, t[2 * p].x, t[2 * p].y};
         }
     }
 }
 
 // Rows-contiguous destination (v^T, (B, H_kv, d, S)): the main loop accumulates C, so
-// acc[i][j][e] = C[m + e][n] with m = m0 + wm + 16i + 4lq and n = n0 + wn + 16j + lr:
-// four consecutive positions s of one (head, dim) row of v^T, one 8-byte store.
+// acc[i][j][e] = C[m + e][n] with m = m0 + wm + 16i + 4lq and n = n0 + wn + 16j + lr: four
+// consecutive positions s of one (head, dim) row of v^T.  Tiles i = 2p, 2p+1 pair up the
+// same way, and the lane stores positions m0 + wm + 32p + 16 * (lq even) + 8 * (lq / 2) .. +7.
 __device__ __forceinline__ void store_cn_f16(const cf_gemm_args_t& a, int seg, int m0, int n0, int wm, int wn,
                                              int lr, int lq, const f4_t (&acc)[4][4]) {
     const _Float16* __restrict__ bias = (const _Float16*)a.bias[seg];
     _Float16* __restrict__ out = (_Float16*)a.out[seg];
+    const bool odd = lq & 1;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int n = n0 + wn + 16 * j + lr;
         const size_t cp = col_part(a, seg, n);
         const float bv = bias ? (float)bias[n] : 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const size_t off = row_part(a, seg, m0 + wm + 16 * i + 4 * lq) + cp;
-            *(h4_t*)(out + off) = h4_t{(_Float16)(acc[i][j][0] + bv), (_Float16)(acc[i][j][1] + bv),
-                                       (_Float16)(acc[i][j][2] + bv), (_Float16)(acc[i][j][3] + bv)};
+        for (int p = 0; p < 2; p++) {
+            uint2 ta = pack4(acc[2 * p][j][0] + bv, acc[2 * p][j][1] + bv, acc[2 * p][j][2] + bv, acc[2 * p][j][3] + bv);
+            uint2 tb = pack4(acc[2 * p + 1][j][0] + bv, acc[2 * p + 1][j][1] + bv, acc[2 * p + 1][j][2] + bv,
+                             acc[2 * p + 1][j][3] + bv);
+            pair_swap(tb, ta);
+            const int m = m0 + wm + 32 * p + (odd ? 0 : 16) + 8 * (lq >> 1);
+            *(uint4*)(out + row_part(a, seg, m) + cp) = uint4{tb.x, tb.y, ta.x, ta.y};
         }
     }
 }
