@@ -421,18 +421,31 @@ void flash_f16_dma64(cf_flash_args_t a) {
                     acc[j][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[j][s2], acc[j][u], 0, 0, 0);
             }
     }
+    // Lane (lr, lq) holds O[query][16u + 4lq .. +3].  A row swap with the lane 16 apart
+    // between dim blocks u = 2p and 2p+1 gives each lane eight consecutive dims (even lane
+    // rows: block 2p+1 from 4lq; odd rows: block 2p from 4(lq-1)), stored as 16 bytes.  The
+    // swaps run on every lane; only the store is predicated.
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
-        const float l_tot = add_xor32(add_xor16(l_run[j]));
-        if (query[j] < S) {
-            const float inv = 1.0f / l_tot;
-            _Float16* op = (_Float16*)a.o + (((size_t)b * S + query[j]) * a.H_q + h) * D;
+        const float inv = 1.0f / add_xor32(add_xor16(l_run[j]));
+        _Float16* op = (_Float16*)a.o + (((size_t)b * S + min(query[j], S - 1)) * a.H_q + h) * D;
 #pragma unroll
-            for (int u = 0; u < UT; u++) {
-                const h4_t ov = {(_Float16)(acc[j][u][0] * inv), (_Float16)(acc[j][u][1] * inv),
-                                 (_Float16)(acc[j][u][2] * inv), (_Float16)(acc[j][u][3] * inv)};
-                *(h4_t*)(op + 16 * u + 4 * lq) = ov;
+        for (int p = 0; p < UT / 2; p++) {
+            const f4_t& x = acc[j][2 * p];
+            const f4_t& y = acc[j][2 * p + 1];
+            float ta[2], tb[2];
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                ta[k] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, h2_t{(_Float16)(x[2 * k] * inv),
+                                                                                   (_Float16)(x[2 * k + 1] * inv)}));
+                tb[k] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, h2_t{(_Float16)(y[2 * k] * inv),
+                                                                                   (_Float16)(y[2 * k + 1] * inv)}));
+                swap_xor16(tb[k], ta[k]);
             }
+            if (query[j] < S)
+                *(uint4*)(op + 32 * p + ((lq & 1) ? 0 : 16) + 8 * (lq >> 1)) =
+                    uint4{__builtin_bit_cast(uint32_t, tb[0]), __builtin_bit_cast(uint32_t, tb[1]),
+                          __builtin_bit_cast(uint32_t, ta[0]), __builtin_bit_cast(uint32_t, ta[1])};
         }
     }
 }
