@@ -658,10 +658,11 @@ void merge_rows(cf_decode_attn_args_t a, int Gx, int units_per_b) {
     }
 }
 
-// Merge, one wave per output row (D = 64 or 128; DPL = D / 64 dims per lane), four rows
-// per workgroup, no LDS: lane s holds (m, l) of splits s, s + 64, ...; the wave reduces
-// M = max m and den = sum 2^(m - M) l with shuffles, then accumulates the splits'
-// accumulator rows weighted by 2^(m_s - M) (broadcast from lane s % 64), eight in flight.
+// Merge, one wave per output row (D = 64 or 128; DPL = D / 64 dims per lane; used up to
+// 16 splits), four rows per workgroup, no LDS: lane s holds (m, l) of splits s, s + 64,
+// ...; the wave reduces M = max m and den = sum 2^(m - M) l with shuffles, then
+// accumulates the splits' accumulator rows weighted by 2^(m_s - M) (broadcast from lane
+// s % 64), eight in flight.
 template <typename T, int DPL>
 __global__ __launch_bounds__(256)
 void merge_wave(cf_decode_attn_args_t a, int Gx, int units_per_b, int rows) {
@@ -826,7 +827,9 @@ extern "C" int cf_launch_decode_attn_merge(const cf_decode_attn_args_t* a, void*
     const int Gx = fast ? a->H_q / a->H_kv : 1;
     const int units_per_b = fast ? a->H_kv : a->H_q;
     const int rows = a->B * units_per_b * Gx;
-    if ((a->d == 64 || a->d == 128) && !g_merge_rows) {
+    // One wave per row while the splits fit a few rounds of eight loads; with many
+    // splits (long or ragged caches) a whole workgroup per row keeps more in flight.
+    if ((a->d == 64 || a->d == 128) && a->n_split <= 16 && !g_merge_rows) {
         const dim3 grid((unsigned)((rows + 3) / 4)), blk(256);
         if (a->elem == CF_ELEM_F16) {
             if (a->d == 64) hipLaunchKernelGGL((merge_wave<_Float16, 1>), grid, blk, 0, s, *a, Gx, units_per_b, rows);

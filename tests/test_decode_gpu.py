@@ -385,8 +385,8 @@ def test_split_chunks_longer_than_4096(gpu, native):
 
 @pytest.mark.parametrize("f16,d,G", [(True, 128, 4), (True, 64, 2), (False, 64, 1), (False, 128, 8)])
 def test_merge_kernels_agree(gpu, native, f16, d, G):
-    """The one-wave merge (d = 64 / 128) and the workgroup-per-row merge on the same
-    partials: both within the bound of the oracle, and close to each other."""
+    """The one-wave merge (d = 64 / 128, up to 16 splits) and the workgroup-per-row merge
+    on the same partials: both within the bound of the oracle, and close to each other."""
     B, H_kv, T = 3, 2, 3000
     H = H_kv * G
     r = O.round_f16 if f16 else (lambda a: a)
@@ -395,11 +395,13 @@ def test_merge_kernels_agree(gpu, native, f16, d, G):
     want = O.decode_attn(Q, K, V, np.asarray([l + 1 for l in lens], np.int32), float(1 / np.sqrt(d)), H_kv)
     outs = []
     try:
+        native.mha_decode_set_split_chunk(256)         # <= 12 splits: the one-wave merge applies
         for rows in (0, 1):
             native.cf_decode_attn_set_merge_rows(rows)
             outs.append(run_decode_attn_gpu(Q, K, V, None, H_kv, f16, seq_lens=lens))
     finally:
         native.cf_decode_attn_set_merge_rows(0)
+        native.mha_decode_set_split_chunk(0)
     tol = TOL16 if f16 else TOL32
     for got in outs:
         assert max_abs(want, got) <= tol
