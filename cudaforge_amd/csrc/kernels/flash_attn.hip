@@ -232,10 +232,17 @@ void flash_f16(cf_flash_args_t a) {
 // (row / 2 ^ row / 16) % 8) are bank-conflict free.  The V^T term in row / 16 makes the
 // reads of row blocks u and u+1 differ by more than a constant, so the compiler keeps
 // them as separate ds_read_b64 instead of pairing them into ds_read2st64_b64, which
-// measured four times the LDS cycles (SQ_LDS_BANK_CONFLICT) on gfx950.  Rows and chunks past the sequence end are clamped to the last
-// valid ones (S % 8 == 0 keeps every 8-key chunk whole) and get p = 0.  The row max is
-// reduced with the gfx950 row swaps, and the running max only moves when a block
-// exceeds it by more than kLazy (log2 units), so the accumulators are rarely rescaled.
+// measured four times the LDS cycles (SQ_LDS_BANK_CONFLICT) on gfx950.  Rows and chunks
+// past the sequence end are clamped to the last valid ones (S % 8 == 0 keeps every 8-key
+// chunk whole) and get p = 0.  The row max is reduced with the gfx950 row swaps, and the
+// running max only moves when a block exceeds it by more than kLazy (log2 units), so the
+// accumulators are rarely rescaled.
+// The kernel is bound by its VALU work per score (the exponential and its neighbours),
+// so everything else is kept off the VALU: the loop is unrolled by ring stage (LDS
+// addresses become immediates), full blocks are loaded as a uniform base plus per-lane
+// offsets fixed for the whole loop, and the row sum of p comes out of the matrix core:
+// one more MFMA per 32 keys with an all-ones A operand gives every lane the full sum
+// over the block's keys for its query, from the same fp16 p that weights V.
 constexpr int kFlashStages = 3;
 constexpr float kLazy = 8.0f;
 
@@ -252,6 +259,7 @@ void flash_f16_dma64(cf_flash_args_t a) {
     constexpr int UT = D / 16;                    // 16-dim tiles of O^T
     constexpr int TILE = kKB * D;                 // halves per block per tensor (8 KB)
     constexpr int NS = kFlashStages;
+    static_assert(NS == 3, "the prologue issues two blocks");
     __shared__ __attribute__((aligned(16))) _Float16 ring[NS * 2 * TILE];
 
     const int nqb = (a.S + QB - 1) / QB;
@@ -287,22 +295,41 @@ void flash_f16_dma64(cf_flash_args_t a) {
     wait_vm<0>();
 
     // DMA: each wave fills K rows 16w .. 16w+15 and V^T rows 16w .. 16w+15 of a stage,
-    // 8 rows per instruction; lane L writes physical chunk L % 8 of row 8u + L / 8.
+    // 8 rows per instruction; lane L writes physical chunk L % 8 of row 8u + L / 8.  A
+    // full block is a uniform base (its first key) plus these per-lane byte offsets
+    // (V^T rows are S keys apart: the launcher keeps 64 * S * 2 bytes below 2^32).
     const uint32_t ring_base = lds_offset(ring);
+    const uint32_t wave_lds = __builtin_amdgcn_readfirstlane(ring_base + (uint32_t)(16 * wave) * 128u);
     const int drow0 = 16 * wave + (lane >> 3), dch = lane & 7;
-    auto issue = [&](int blk) {
-        const int k0 = blk * kKB;
-        const uint32_t kb = ring_base + (uint32_t)((blk % NS) * 2 * TILE) * 2u;
-        const uint32_t vb = kb + (uint32_t)TILE * 2u;
+    uint32_t koff[2], voff[2];
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int row = drow0 + 8 * u;
-            const int kc = dch ^ fswz(row);
-            lds_dma16(kp + (size_t)min(k0 + row, S - 1) * D + 8 * kc,
-                      __builtin_amdgcn_readfirstlane(kb + (uint32_t)(16 * wave + 8 * u) * 128u));
-            const int vcol = min(k0 + 8 * (dch ^ vswz(row)), S - 8);
-            lds_dma16(vp + (size_t)row * S + vcol,
-                      __builtin_amdgcn_readfirstlane(vb + (uint32_t)(16 * wave + 8 * u) * 128u));
+    for (int u = 0; u < 2; u++) {
+        const int row = drow0 + 8 * u;
+        koff[u] = (uint32_t)(row * D + 8 * (dch ^ fswz(row))) * 2u;
+        voff[u] = ((uint32_t)row * (uint32_t)S + 8u * (uint32_t)(dch ^ vswz(row))) * 2u;
+    }
+    auto issue = [&](int blk, auto stage_c) {
+        constexpr int stage = decltype(stage_c)::value;
+        const int k0 = blk * kKB;
+        const uint32_t kb = wave_lds + (uint32_t)(stage * 2 * TILE) * 2u;
+        const uint32_t vb = kb + (uint32_t)TILE * 2u;
+        if (k0 + kKB <= S) {
+            const _Float16* kblk = kp + (size_t)k0 * D;
+            const _Float16* vblk = vp + k0;
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                lds_dma16_s(koff[u], kblk, kb + (uint32_t)(8 * u) * 128u);
+                lds_dma16_s(voff[u], vblk, vb + (uint32_t)(8 * u) * 128u);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int row = drow0 + 8 * u;
+                const int kc = dch ^ fswz(row);
+                lds_dma16(kp + (size_t)min(k0 + row, S - 1) * D + 8 * kc, kb + (uint32_t)(8 * u) * 128u);
+                const int vcol = min(k0 + 8 * (dch ^ vswz(row)), S - 8);
+                lds_dma16(vp + (size_t)row * S + vcol, vb + (uint32_t)(8 * u) * 128u);
+            }
         }
     };
     // Per-lane LDS read offsets (halves) inside a stage.
@@ -327,12 +354,13 @@ void flash_f16_dma64(cf_flash_args_t a) {
             }
 
     const float c = a.scale * kLog2e;
-    float m_run[NJ], l_run[NJ];
-    f4_t acc[NJ][UT];
+    const h8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
+    float m_run[NJ];
+    f4_t acc[NJ][UT], lsum[NJ];                    // lsum: every element is the query's sum of p
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
         m_run[j] = -INFINITY;
-        l_run[j] = 0.0f;
+        lsum[j] = f4_t{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
     for (int j = 0; j < NJ; j++)
@@ -341,18 +369,17 @@ void flash_f16_dma64(cf_flash_args_t a) {
 
     const int k_end = a.causal ? min(S, q0 + QB) : S;
     const int nblk = (k_end + kKB - 1) / kKB;
-#pragma unroll
-    for (int st = 0; st < NS - 1; st++)
-        if (st < nblk) issue(st);
-    for (int bi = 0; bi < nblk; bi++) {
+    if (0 < nblk) issue(0, std::integral_constant<int, 0>{});
+    if (1 < nblk) issue(1, std::integral_constant<int, 1>{});
+    auto step = [&](int bi, auto stage_c) {
+        constexpr int stage = decltype(stage_c)::value;
         // Blocks issued after this one that may still be in flight (4 loads each).
-        if (min(NS - 2, nblk - 1 - bi) >= 1) wait_vm<4>();
-        else wait_vm<0>();
+        wait_ahead<4, NS - 2>(nblk - 1 - bi);
         ring_barrier();                            // every wave's part of block bi landed;
                                                    // block bi-1's stage is free again
-        if (bi + NS - 1 < nblk) issue(bi + NS - 1);
+        if (bi + NS - 1 < nblk) issue(bi + NS - 1, std::integral_constant<int, (stage + NS - 1) % NS>{});
         const int k0 = bi * kKB;
-        const _Float16* st = ring + (bi % NS) * 2 * TILE;
+        const _Float16* st = ring + stage * 2 * TILE;
 
         // S^T tiles: sc[j][t][i] = score(key k0 + 16t + 4*lq + i, query[j]).
         f4_t sc[NJ][4];
@@ -390,22 +417,17 @@ void flash_f16_dma64(cf_flash_args_t a) {
                 const float m_new = mloc > m_run[j] + kLazy ? mloc : m_run[j];
                 const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_new);   // 0 on the first move
                 m_run[j] = m_new;
-                l_run[j] *= alpha;
+                lsum[j] *= alpha;
 #pragma unroll
                 for (int u = 0; u < UT; u++) acc[j][u] *= alpha;
             }
             // Rows with nothing visible yet keep m = -inf: use 0 so p = 2^-inf = 0.
             const float m_use = m_run[j] == -INFINITY ? 0.0f : m_run[j];
-            float psum = 0.0f;
 #pragma unroll
             for (int t = 0; t < 4; t++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][t][i], c, -m_use));
-                    psum += p;
-                    pf[j][t >> 1][(t & 1) * 4 + i] = (_Float16)p;
-                }
-            l_run[j] += psum;
+                for (int i = 0; i < 4; i++)
+                    pf[j][t >> 1][(t & 1) * 4 + i] = (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][t][i], c, -m_use));
         }
         // O^T[16u + 4*lq + i][query] += V^T . P^T; in 32-key step s, k-slot e of lane group
         // lq is key 32s + 16*(e/4) + 4*lq + (e%4).
@@ -420,14 +442,21 @@ void flash_f16_dma64(cf_flash_args_t a) {
                 for (int j = 0; j < NJ; j++)
                     acc[j][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[j][s2], acc[j][u], 0, 0, 0);
             }
-    }
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int s2 = 0; s2 < 2; s2++)
+                lsum[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf[j][s2], lsum[j], 0, 0, 0);
+    };
+    for_each_stage<NS>(nblk, step);
+
     // Lane (lr, lq) holds O[query][16u + 4lq .. +3].  A row swap with the lane 16 apart
     // between dim blocks u = 2p and 2p+1 gives each lane eight consecutive dims (even lane
     // rows: block 2p+1 from 4lq; odd rows: block 2p from 4(lq-1)), stored as 16 bytes.  The
     // swaps run on every lane; only the store is predicated.
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
-        const float inv = 1.0f / add_xor32(add_xor16(l_run[j]));
+        const float inv = 1.0f / lsum[j][0];
         _Float16* op = (_Float16*)a.o + (((size_t)b * S + min(query[j], S - 1)) * a.H_q + h) * D;
 #pragma unroll
         for (int p = 0; p < UT / 2; p++) {
@@ -521,7 +550,8 @@ extern "C" int cf_launch_flash_attn(const cf_flash_args_t* a, void* stream) {
         const long long groups = ((long long)a->B * a->H_q + 7) / 8;
         if (groups * nqb * 8 > 0x7fffffffLL) return (int)hipErrorInvalidValue;
         dim3 grid((unsigned)(groups * nqb * 8));
-        if (a->d == 64 && a->S % 8 == 0 && g_flash_mode != 0) {
+        // The DMA kernel addresses V^T rows with 32-bit byte offsets: 64 * S * 2 < 2^32.
+        if (a->d == 64 && a->S % 8 == 0 && a->S <= (1 << 24) && g_flash_mode != 0) {
             // 16 queries per wave (64 per workgroup) doubles the workgroups, and with
             // them the waves per SIMD that hide each block's latency chain; 32 per wave
             // halves the LDS traffic per query (every wave reads the whole K/V^T block),

@@ -497,10 +497,7 @@ void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
         for (int kt = 0; kt < nk; kt++) {
             // Tiles issued after kt that may still be in flight: min(STAGES-2, nk-1-kt), 4
             // load instructions each.
-            const int ahead = min(STAGES - 2, nk - 1 - kt);
-            if (ahead >= 2) wait_vm<8>();
-            else if (ahead == 1) wait_vm<4>();
-            else wait_vm<0>();
+            wait_ahead<4, STAGES - 2>(nk - 1 - kt);
             ring_barrier();
             if (kt + STAGES - 1 < nk) issue((kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BKA);
             const _Float16* As = smem + (kt % STAGES) * ST;

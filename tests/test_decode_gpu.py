@@ -383,7 +383,8 @@ def test_split_chunks_longer_than_4096(gpu, native):
     assert max_abs(want, got) <= TOL16
 
 
-@pytest.mark.parametrize("f16,d,G", [(True, 128, 4), (True, 64, 2), (False, 64, 1), (False, 128, 8)])
+@pytest.mark.parametrize("f16,d,G", [(True, 128, 4), (True, 64, 2), (True, 64, 8), (True, 128, 1),
+                                     (False, 64, 1), (False, 128, 8)])
 def test_merge_kernels_agree(gpu, native, f16, d, G):
     """The one-wave merge (d = 64 / 128, up to 16 splits) and the workgroup-per-row merge
     on the same partials: both within the bound of the oracle, and close to each other."""
