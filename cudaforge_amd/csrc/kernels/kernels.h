@@ -134,6 +134,9 @@ int cf_launch_gemm(const cf_gemm_args_t* a, void* stream);
 void cf_gemm_set_stages(int32_t stages);
 /* Tuning override of the tile order's group height (M tiles per group; 0 = default). */
 void cf_gemm_set_group_m(int32_t group_m);
+/* Tuning/test override of the fp16 direct-to-LDS GEMM's tile width (96 or 128 columns;
+ * 0 = automatic: the width that balances the tiles over the CUs). */
+void cf_gemm_set_bn(int32_t bn);
 
 /* ---------------------------------------------------------------------------------
  * Prefill attention (flash style, online softmax): q (B, H_q, S, d), k (B, H_kv, S, d),

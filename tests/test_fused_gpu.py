@@ -147,6 +147,27 @@ def test_flash_kernel_variants_agree(gpu, native, causal):
         assert max_abs(outs[0], o) <= 1e-2
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_gemm_tile_widths_agree(gpu, native, causal):
+    """The fp16 projection GEMM with 128-column and 96-column tiles on a shape both fit
+    (D = 384 = 3 x 128 = 4 x 96; QKV with head-major and V^T scatter, WO with bias and
+    residual): each within the FP16 bound of the oracle, and bit-identical to each other
+    (every output element sums the same k-steps in the same order)."""
+    c = FusedCase(2, 128, 6, 6, 64, seed=96, f16=True, causal=causal, residual=True, bias_std=0.02)
+    want = c.oracle()
+    outs = []
+    try:
+        for bn in (128, 96, 0):
+            native.cf_gemm_set_bn(bn)
+            outs.append(run_fused_gpu(c))
+    finally:
+        native.cf_gemm_set_bn(0)
+    for o in outs:
+        assert max_abs(want, o) <= TOL16
+    assert np.array_equal(outs[0], outs[1])
+    assert np.array_equal(outs[0], outs[2])
+
+
 @pytest.mark.parametrize("f16,causal", [(False, False), (True, False), (True, True)])
 def test_graph_runs_unfused_attention_as_one_fused_op(gpu, native, f16, causal):
     """An unfused self-attention block (MatMul/Add/Reshape/Transpose/Mul/[CausalMask]/
