@@ -281,18 +281,9 @@ void flash_f16_dma64(cf_flash_args_t a) {
     const _Float16* __restrict__ kp = (const _Float16*)a.k + (((size_t)b * a.H_kv + kvh) * S) * D;
     const _Float16* __restrict__ vp = (const _Float16*)a.vt + (((size_t)b * a.H_kv + kvh) * D) * (size_t)S;
 
-    // Q fragments first, waited for before the ring starts (the DMA loads are invisible
-    // to the compiler's wait counting).
     int query[NJ];
-    h8_t qf[NJ][KT];
 #pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        query[j] = qw + 16 * j + lr;
-        const _Float16* qr = qp + (size_t)min(query[j], S - 1) * D + 8 * lq;
-#pragma unroll
-        for (int kt = 0; kt < KT; kt++) qf[j][kt] = *(const h8_t*)(qr + 32 * kt);
-    }
-    wait_vm<0>();
+    for (int j = 0; j < NJ; j++) query[j] = qw + 16 * j + lr;
 
     // DMA: each wave fills K rows 16w .. 16w+15 and V^T rows 16w .. 16w+15 of a stage,
     // 8 rows per instruction; lane L writes physical chunk L % 8 of row 8u + L / 8.  A
@@ -369,8 +360,37 @@ void flash_f16_dma64(cf_flash_args_t a) {
 
     const int k_end = a.causal ? min(S, q0 + QB) : S;
     const int nblk = (k_end + kKB - 1) / kKB;
+    // The workgroup's Q rows (QB x 128 B, swizzled like K) go by DMA into ring stage
+    // NS-1, which the first blocks leave free, ahead of blocks 0 and 1: the Q and K/V
+    // latencies overlap.  Wave w loads rows 8u .. 8u+7 for u = QB/32 * w + v.
+    constexpr int QI = QB / 32;                   // Q DMA instructions per wave
+    {
+        const uint32_t qb_lds = ring_base + (uint32_t)((NS - 1) * 2 * TILE) * 2u;
+#pragma unroll
+        for (int v = 0; v < QI; v++) {
+            const int u = QI * wave + v, row = 8 * u + (lane >> 3);
+            lds_dma16(qp + (size_t)min(q0 + row, S - 1) * D + 8 * (dch ^ fswz(row)),
+                      __builtin_amdgcn_readfirstlane(qb_lds + (uint32_t)u * 1024u));
+        }
+    }
     if (0 < nblk) issue(0, std::integral_constant<int, 0>{});
     if (1 < nblk) issue(1, std::integral_constant<int, 1>{});
+    // Q landed when at most the blocks' loads (4 per block) are outstanding.
+    if (nblk >= 2) wait_vm<8>();
+    else wait_vm<4>();
+    ring_barrier();
+    // B operand Q^T: lane (lr, lq) holds Q[query][32kt + 8lq .. +7].
+    h8_t qf[NJ][KT];
+    {
+        const _Float16* qs = ring + (NS - 1) * 2 * TILE;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const int row = QW * wave + 16 * j + lr;
+#pragma unroll
+            for (int kt = 0; kt < KT; kt++) qf[j][kt] = *(const h8_t*)(qs + row * D + 8 * ((4 * kt + lq) ^ fswz(row)));
+        }
+    }
+    wait_lds_reads();                              // stage NS-1 is refilled after the next barrier
     auto step = [&](int bi, auto stage_c) {
         constexpr int stage = decltype(stage_c)::value;
         // Blocks issued after this one that may still be in flight (4 loads each).
