@@ -388,15 +388,17 @@ int dma_bn(const cf_gemv_args_t* a) {
 
 // Reduce for the DMA path (tile widths are multiples of 64): a thread owns 4 adjacent
 // columns of one row and issues all of its K-chunk loads (16-byte) before summing, so
-// the whole reduction is one round trip to memory.
-__global__ __launch_bounds__(256)
+// the whole reduction is one round trip to memory.  One-wave workgroups spread the
+// partials over every CU (16 rows x 6144 columns is 384 of them).
+constexpr int kReduceThreads = 64;
+__global__ __launch_bounds__(kReduceThreads)
 void gemv_reduce4(cf_gemv_args_t a, Tiles t) {
     constexpr int MAXKS = 32;
     const int ncols = t.start[a.nseg] * t.bn;
     const int Mp = (a.M + kMTile - 1) / kMTile * kMTile;
     const size_t plane = (size_t)Mp * ncols;
     const size_t total = (size_t)a.M * (ncols / 4);
-    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t idx = (size_t)blockIdx.x * kReduceThreads + threadIdx.x;
     if (idx >= total) return;
     const int m = (int)(idx / (ncols / 4));
     const int col = (int)(idx - (size_t)m * (ncols / 4)) * 4;
@@ -496,7 +498,8 @@ extern "C" int cf_launch_gemv(const cf_gemv_args_t* a, void* stream) {
     if (e != hipSuccess || t.ks == 1) return (int)e;
     if (t.dma) {
         const size_t total4 = (size_t)a->M * t.start[a->nseg] * t.bn / 4;
-        hipLaunchKernelGGL(gemv_reduce4, dim3((unsigned)((total4 + 255) / 256)), dim3(256), 0, s, args, t);
+        hipLaunchKernelGGL(gemv_reduce4, dim3((unsigned)((total4 + kReduceThreads - 1) / kReduceThreads)),
+                           dim3(kReduceThreads), 0, s, args, t);
         return (int)hipGetLastError();
     }
     const size_t total = (size_t)a->M * t.start[a->nseg] * t.bn;
