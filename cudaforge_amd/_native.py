@@ -128,6 +128,8 @@ def _proto(lib):
         "graph_set_input": (c_int, [c_void_p, c_int]),
         "graph_set_output": (c_int, [c_void_p, c_int]),
         "graph_build": (c_int, [c_void_p]),
+        "graph_set_replay": (None, [c_void_p, c_int]),
+        "graph_replay_state": (c_int, [c_void_p]),
         "graph_destroy": (None, [c_void_p]),
         "graph_set_kv_cache": (None, [c_void_p, c_int, c_int]),
         "graph_update_cache_len": (None, [c_void_p, c_int64]),

@@ -17,6 +17,12 @@
  * executions run each self-attention subgraph that graph_detect_mha finds (graph_fuse.c,
  * the reference's detect_and_fuse_mha, graph.c:347-665) as one OP_MHA_FUSED node, without
  * rewriting the graph.
+ * GPU executions run on a non-blocking stream the graph owns and, once an execution has
+ * run every node on the GPU, are recorded into a HIP graph and replayed (the reference's
+ * CUDA-graph path, graph.c:681-742, which it left disabled because every launch went to
+ * the legacy stream).  Host copies stay synchronous on the legacy stream: graph inputs are
+ * uploaded before any node that reads them runs, and the graph stream is synchronised
+ * before any device-to-host copy.
  */
 #include "graph.h"
 #include "gpu_ops.h"
@@ -25,6 +31,21 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+
+/* Drops the recorded execution; the next all-GPU execution starts over. */
+static void replay_reset(inference_graph_t* g) {
+    if (g->hip_graph_exec) gpu_graph_exec_destroy(g->hip_graph_exec);
+    g->hip_graph_exec = NULL;
+    g->hip_graph_state = 0;
+}
+
+void graph_set_replay(inference_graph_t* g, int enable) {
+    if (!g) return;
+    g->replay_off = !enable;
+    replay_reset(g);
+}
+
+int graph_replay_state(const inference_graph_t* g) { return g ? g->hip_graph_state : 0; }
 
 inference_graph_t* graph_create(void) {
     inference_graph_t* g = (inference_graph_t*)calloc(1, sizeof(inference_graph_t));
@@ -36,6 +57,7 @@ inference_graph_t* graph_create(void) {
 
 int graph_add_tensor(inference_graph_t* g, tensor_t* t) {
     if (!g || !t) return -1;
+    replay_reset(g);
     graph_tensor_t* p = (graph_tensor_t*)realloc(g->tensors, (size_t)(g->num_tensors + 1) * sizeof(graph_tensor_t));
     if (!p) return -1;
     g->tensors = p;
@@ -53,6 +75,7 @@ int graph_add_node(inference_graph_t* g, op_type_t type,
                    void* params, size_t params_size) {
     if (!g || num_inputs < 0 || num_outputs < 0 || num_weights < 0) return -1;
     if ((num_inputs > 0 && !input_tensors) || (num_outputs > 0 && !output_tensors)) return -1;
+    replay_reset(g);
     graph_node_t* p = (graph_node_t*)realloc(g->nodes, (size_t)(g->num_nodes + 1) * sizeof(graph_node_t));
     if (!p) return -1;
     g->nodes = p;
@@ -120,6 +143,7 @@ int graph_set_output(inference_graph_t* g, int node_id) {
 
 void graph_set_kv_cache(inference_graph_t* g, int K_tensor_id, int V_tensor_id) {
     if (!g) return;
+    replay_reset(g);
     g->kv_cache_K_tid = K_tensor_id;
     g->kv_cache_V_tid = V_tensor_id;
 }
@@ -128,8 +152,11 @@ void graph_update_cache_len(inference_graph_t* g, int64_t new_cache_len) {
     if (!g) return;
     for (int i = 0; i < g->num_nodes; i++) {
         graph_node_t* n = &g->nodes[i];
-        if (n->type == OP_MHA_DECODE && n->params && n->params_size >= sizeof(mha_decode_params_t))
+        if (n->type == OP_MHA_DECODE && n->params && n->params_size >= sizeof(mha_decode_params_t) &&
+            ((mha_decode_params_t*)n->params)->cache_len != new_cache_len) {
             ((mha_decode_params_t*)n->params)->cache_len = new_cache_len;
+            replay_reset(g);                  /* the recorded launches hold the old length */
+        }
     }
 }
 
@@ -140,6 +167,7 @@ void graph_set_permanent_fusion(inference_graph_t* g, int enable) {
 /* Kahn's algorithm (graph.c:158-220): a node depends on the producers of its inputs. */
 int graph_build(inference_graph_t* g) {
     if (!g) return -1;
+    replay_reset(g);
     const int n = g->num_nodes;
     int* indeg = (int*)calloc((size_t)(n > 0 ? n : 1), sizeof(int));
     int* queue = (int*)malloc((size_t)(n > 0 ? n : 1) * sizeof(int));
@@ -178,7 +206,11 @@ int graph_build(inference_graph_t* g) {
 
 void graph_destroy(inference_graph_t* g) {
     if (!g) return;
-    if (g->hip_graph) gpu_stream_destroy(g->hip_graph);
+    replay_reset(g);
+    if (g->hip_graph) {
+        (void)gpu_stream_synchronize(g->hip_graph);
+        gpu_stream_destroy(g->hip_graph);
+    }
     for (int i = 0; i < g->num_nodes; i++) {
         free(g->nodes[i].input_tensors);
         free(g->nodes[i].output_tensors);
@@ -293,12 +325,17 @@ static int op_produced(const inference_graph_t* g, int tid) {
 
 /* Runs one node: resolves its operator, moves its tensors to where the operator runs,
  * calls it (graph.c:820-1030). */
-static int run_node(inference_graph_t* g, const graph_node_t* n, bool use_cuda, unsigned char* fresh) {
+static int run_node(inference_graph_t* g, const graph_node_t* n, bool use_cuda, unsigned char* fresh,
+                    int* ran_on_gpu) {
     int ret = 0;
     char name[64];
     const operator_registry_t* op = resolve_node(g, n, use_cuda, name, sizeof(name));
     if (!op) return -2;
     const int on_gpu = use_cuda && strstr(name, "_cuda") != NULL;
+    if (ran_on_gpu) *ran_on_gpu = on_gpu;
+    /* A CPU operator reads host copies of device data: let the graph's stream finish. */
+    if (use_cuda && !on_gpu && g->hip_graph && (ret = gpu_stream_synchronize(g->hip_graph)) != 0) return ret;
+    int copied = 0;                 /* a host-to-device copy was issued for this node */
 
     /* Input slots: tensor inputs, then weights, padded with NULLs to the count some ops
      * always read (graph.c:886-895: activations 2, Conv/MatMul 3 for the optional bias,
@@ -326,8 +363,10 @@ static int run_node(inference_graph_t* g, const graph_node_t* n, bool use_cuda, 
         tensor_t* t = g->tensors[tid].tensor;
         if (on_gpu) {
             if (is_kv(g, tid) || op_produced(g, tid)) {
+                copied |= !t->data_device;
                 if (tensor_copy_to_device(t) != 0) ret = -1;
             } else if (!fresh[tid]) {
+                copied = 1;
                 if (tensor_upload(t) != 0) ret = -1;
                 fresh[tid] = 1;
             }
@@ -343,6 +382,7 @@ static int run_node(inference_graph_t* g, const graph_node_t* n, bool use_cuda, 
         slots[n->num_inputs + w] = NULL;
         if (!t) continue;
         if (on_gpu) {
+            copied |= !t->data_device;
             if (tensor_copy_to_device(t) != 0) ret = -1;
             slots[n->num_inputs + w] = t->data_device;
         } else {
@@ -364,8 +404,11 @@ static int run_node(inference_graph_t* g, const graph_node_t* n, bool use_cuda, 
             outs[i] = t->data;
         }
     }
+    /* Host copies go on the legacy stream, which the graph's non-blocking stream does not
+     * wait for: let them land before the operator's launches. */
+    if (ret == 0 && copied) ret = gpu_stream_synchronize(NULL);
     if (ret == 0) {
-        stream_t stream = {NULL};
+        stream_t stream = {g->hip_graph};
         ret = op->func(slots, outs, (const operator_params_t*)n->params, use_cuda ? &stream : NULL);
     }
     if (ret == 0 && use_cuda && !on_gpu) {
@@ -377,7 +420,7 @@ static int run_node(inference_graph_t* g, const graph_node_t* n, bool use_cuda, 
             tensor_t* t = g->tensors[tid].tensor;
             if (!t->data_device) continue;
             if (is_kv(g, tid)) {
-                if (tensor_upload(t) != 0) ret = -1;
+                if (tensor_upload(t) != 0 || gpu_stream_synchronize(NULL) != 0) ret = -1;
             } else {
                 gpu_device_free(t->data_device);
                 t->data_device = NULL;
@@ -388,10 +431,93 @@ static int run_node(inference_graph_t* g, const graph_node_t* n, bool use_cuda, 
     return ret;
 }
 
+/* Uploads every tensor a GPU execution reads from the host that is neither a KV cache nor
+ * produced by an operator (the graph inputs and constant inputs), marking it fresh, and
+ * makes sure the KV caches and weights are on the device: a recorded execution may not
+ * copy from the host. */
+static int preload_inputs(inference_graph_t* g, unsigned char* fresh) {
+    for (int i = 0; i < g->num_nodes; i++) {
+        const graph_node_t* n = &g->nodes[i];
+        for (int k = 0; k < n->num_inputs; k++) {
+            const int tid = n->input_tensors[k];
+            if (tid < 0 || tid >= g->num_tensors || fresh[tid]) continue;
+            tensor_t* t = g->tensors[tid].tensor;
+            if (is_kv(g, tid) || op_produced(g, tid)) {
+                if (is_kv(g, tid) && tensor_copy_to_device(t) != 0) return -1;
+                continue;
+            }
+            if (tensor_upload(t) != 0) return -1;
+            fresh[tid] = 1;
+        }
+        for (int w = 0; w < n->num_weights; w++)
+            if (n->weights[w] && tensor_copy_to_device(n->weights[w]) != 0) return -1;
+    }
+    /* The copies ran on the legacy stream; the graph's stream does not wait for it. */
+    return gpu_stream_synchronize(NULL);
+}
+
+/* Runs every node once, in topological order, with MHA subgraph fusion on GPU
+ * executions.  *all_gpu tells whether every node ran on the GPU. */
+static int run_nodes(inference_graph_t* g, bool use_cuda, unsigned char* fresh, int* all_gpu) {
+    /* MHA subgraph fusion (graph.c:766-815, GPU executions only): each match runs as one
+     * OP_MHA_FUSED node in place of its last node; its other nodes are skipped. */
+    graph_mha_match_t* fz = NULL;
+    int* fused_at = NULL;
+    int n_fused = 0;
+    *all_gpu = use_cuda;
+    if (use_cuda && g->num_nodes > 0) {
+        const int cap = g->num_nodes / 8 + 1;
+        fz = (graph_mha_match_t*)malloc((size_t)cap * sizeof(*fz));
+        fused_at = (int*)malloc((size_t)g->num_nodes * sizeof(int));
+        if (!fz || !fused_at) { free(fz); free(fused_at); return -1; }
+        n_fused = graph_detect_mha(g, fz, cap);
+        for (int i = 0; i < g->num_nodes; i++) fused_at[i] = -1;
+        for (int k = 0; k < n_fused; k++)
+            for (int i = 0; i < fz[k].num_nodes; i++)
+                fused_at[fz[k].nodes[i]] = fz[k].nodes[i] == fz[k].out_node ? k : -2;
+    }
+
+    int ret = 0;
+    for (int oi = 0; oi < g->num_nodes && ret == 0; oi++) {
+        const int nid = g->topo_order[oi];
+        graph_node_t* n = &g->nodes[nid];
+        if (n->type == OP_INPUT || n->type == OP_OUTPUT) continue;
+        if (fused_at && fused_at[nid] == -2) continue;
+        int gpu = 0;
+        if (fused_at && fused_at[nid] >= 0) {
+            graph_mha_match_t* m = &fz[fused_at[nid]];
+            int fin[2] = {m->input_tid, m->residual_tid};
+            int fout[1] = {m->output_tid};
+            graph_node_t fn;
+            memset(&fn, 0, sizeof(fn));
+            fn.type = OP_MHA_FUSED;
+            fn.num_inputs = 2;
+            fn.input_tensors = fin;
+            fn.num_outputs = 1;
+            fn.output_tensors = fout;
+            fn.num_weights = 8;
+            fn.weights = m->weights;
+            fn.params = &m->params;
+            fn.params_size = sizeof(m->params);
+            ret = run_node(g, &fn, use_cuda, fresh, &gpu);
+        } else {
+            ret = run_node(g, n, use_cuda, fresh, &gpu);
+        }
+        if (!gpu) *all_gpu = 0;
+    }
+    free(fz);
+    free(fused_at);
+    return ret;
+}
+
 int graph_execute(inference_graph_t* g, tensor_t* inputs[], tensor_t* outputs[], bool use_cuda) {
     if (!g || !g->topo_order) return -1;
     if (g->num_inputs > 0 && !inputs) return -1;
     if (g->num_outputs > 0 && !outputs) return -1;
+    if (use_cuda && !g->hip_graph && gpu_stream_create(&g->hip_graph) != 0) {
+        g->hip_graph = NULL;
+        return -1;
+    }
 
     /* Graph inputs -> input-node tensors (host). */
     for (int i = 0; i < g->num_inputs; i++) {
@@ -410,56 +536,43 @@ int graph_execute(inference_graph_t* g, tensor_t* inputs[], tensor_t* outputs[],
     unsigned char* fresh = (unsigned char*)calloc((size_t)(g->num_tensors > 0 ? g->num_tensors : 1), 1);
     if (!fresh) return -1;
 
-    /* MHA subgraph fusion (graph.c:766-815, GPU executions only): each match runs as one
-     * OP_MHA_FUSED node in place of its last node; its other nodes are skipped. */
-    graph_mha_match_t* fz = NULL;
-    int* fused_at = NULL;
-    int n_fused = 0;
-    if (use_cuda && g->num_nodes > 0) {
-        const int cap = g->num_nodes / 8 + 1;
-        fz = (graph_mha_match_t*)malloc((size_t)cap * sizeof(*fz));
-        fused_at = (int*)malloc((size_t)g->num_nodes * sizeof(int));
-        if (!fz || !fused_at) { free(fz); free(fused_at); free(fresh); return -1; }
-        n_fused = graph_detect_mha(g, fz, cap);
-        for (int i = 0; i < g->num_nodes; i++) fused_at[i] = -1;
-        for (int k = 0; k < n_fused; k++)
-            for (int i = 0; i < fz[k].num_nodes; i++)
-                fused_at[fz[k].nodes[i]] = fz[k].nodes[i] == fz[k].out_node ? k : -2;
-    }
-
     int ret = 0;
-    for (int oi = 0; oi < g->num_nodes && ret == 0; oi++) {
-        const int nid = g->topo_order[oi];
-        graph_node_t* n = &g->nodes[nid];
-        if (n->type == OP_INPUT || n->type == OP_OUTPUT) continue;
-        if (fused_at && fused_at[nid] == -2) continue;
-        if (fused_at && fused_at[nid] >= 0) {
-            graph_mha_match_t* m = &fz[fused_at[nid]];
-            int fin[2] = {m->input_tid, m->residual_tid};
-            int fout[1] = {m->output_tid};
-            graph_node_t fn;
-            memset(&fn, 0, sizeof(fn));
-            fn.type = OP_MHA_FUSED;
-            fn.num_inputs = 2;
-            fn.input_tensors = fin;
-            fn.num_outputs = 1;
-            fn.output_tensors = fout;
-            fn.num_weights = 8;
-            fn.weights = m->weights;
-            fn.params = &m->params;
-            fn.params_size = sizeof(m->params);
-            ret = run_node(g, &fn, use_cuda, fresh);
-        } else {
-            ret = run_node(g, n, use_cuda, fresh);
+    const int replay = use_cuda && !g->replay_off;
+    if (replay && g->hip_graph_state == 2 && g->hip_graph_exec) {
+        ret = preload_inputs(g, fresh);
+        if (ret == 0) ret = gpu_graph_launch(g->hip_graph_exec, g->hip_graph);
+    } else if (replay && g->hip_graph_state == 1) {
+        /* Record this execution's launches, then run the recording. */
+        int all_gpu = 0, crc;
+        void* exec = NULL;
+        ret = preload_inputs(g, fresh);
+        if (ret == 0 && (ret = gpu_capture_begin(g->hip_graph)) == 0) {
+            ret = run_nodes(g, use_cuda, fresh, &all_gpu);
+            crc = gpu_capture_end(g->hip_graph, &exec);
+            if (ret == 0 && crc == 0 && all_gpu) {
+                g->hip_graph_exec = exec;
+                g->hip_graph_state = 2;
+                ret = gpu_graph_launch(exec, g->hip_graph);
+            } else {
+                /* Not recordable: run it eagerly, and do not try again until the graph
+                 * or its parameters change. */
+                gpu_graph_exec_destroy(exec);
+                (void)gpu_get_last_error();
+                g->hip_graph_state = -1;
+                memset(fresh, 0, (size_t)(g->num_tensors > 0 ? g->num_tensors : 1));
+                ret = run_nodes(g, use_cuda, fresh, &all_gpu);
+            }
         }
+    } else {
+        int all_gpu = 0;
+        ret = run_nodes(g, use_cuda, fresh, &all_gpu);
+        if (ret == 0 && replay && all_gpu && g->hip_graph_state == 0) g->hip_graph_state = 1;
     }
-    free(fz);
-    free(fused_at);
     free(fresh);
     if (ret != 0) return ret;
 
     if (use_cuda) {
-        const int rc = gpu_stream_synchronize(NULL);
+        const int rc = gpu_stream_synchronize(g->hip_graph);
         if (rc != 0) return rc;
     }
     for (int i = 0; i < g->num_outputs; i++) {

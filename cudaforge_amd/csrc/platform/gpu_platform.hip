@@ -138,6 +138,41 @@ int gpu_stream_synchronize(gpu_stream_t stream) { return rc(hipStreamSynchronize
 int gpu_stream_destroy(gpu_stream_t stream) { return stream ? rc(hipStreamDestroy((hipStream_t)stream)) : 0; }
 int gpu_device_synchronize(void) { return rc(hipDeviceSynchronize()); }
 
+int gpu_capture_begin(gpu_stream_t stream) {
+    if (!stream) return (int)hipErrorInvalidValue;   // the legacy stream cannot be captured
+    return rc(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal));
+}
+
+int gpu_capture_end(gpu_stream_t stream, void** exec) {
+    if (!exec) return (int)hipErrorInvalidValue;
+    *exec = nullptr;
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture((hipStream_t)stream, &graph);
+    if (e != hipSuccess || !graph) {
+        if (graph) (void)hipGraphDestroy(graph);
+        (void)hipGetLastError();
+        return e != hipSuccess ? (int)e : (int)hipErrorStreamCaptureInvalidated;
+    }
+    hipGraphExec_t x = nullptr;
+    e = hipGraphInstantiate(&x, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return (int)e;
+    }
+    *exec = (void*)x;
+    return 0;
+}
+
+int gpu_graph_launch(void* exec, gpu_stream_t stream) {
+    if (!exec) return (int)hipErrorInvalidValue;
+    return rc(hipGraphLaunch((hipGraphExec_t)exec, (hipStream_t)stream));
+}
+
+void gpu_graph_exec_destroy(void* exec) {
+    if (exec) (void)hipGraphExecDestroy((hipGraphExec_t)exec);
+}
+
 int gpu_get_device_count(int* count) {
     if (!count) return (int)hipErrorInvalidValue;
     *count = 0;

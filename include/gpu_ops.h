@@ -84,6 +84,16 @@ int   gpu_memset(void* dst, int value, size_t bytes, gpu_stream_t stream);
 int   gpu_stream_create(gpu_stream_t* stream);
 int   gpu_stream_synchronize(gpu_stream_t stream);
 int   gpu_stream_destroy(gpu_stream_t stream);
+/* Stream capture into a replayable HIP graph (thread-local capture mode): between
+ * gpu_capture_begin and gpu_capture_end, work enqueued on `stream` is recorded, not run.
+ * gpu_capture_end instantiates the recording into *exec (0), or returns the capture's
+ * error and keeps nothing.  gpu_graph_launch replays an instantiated recording on a
+ * stream.  The graph executor uses these for repeated executions
+ * (graph_set_replay in graph.h). */
+int   gpu_capture_begin(gpu_stream_t stream);
+int   gpu_capture_end(gpu_stream_t stream, void** exec);
+int   gpu_graph_launch(void* exec, gpu_stream_t stream);
+void  gpu_graph_exec_destroy(void* exec);
 int   gpu_device_synchronize(void);
 int   gpu_get_device_count(int* count);
 int   gpu_current_device(void);          /* device id HIP calls on this thread go to */

@@ -95,12 +95,16 @@ typedef struct {
     int             kv_cache_K_tid;  /* -1 if unused */
     int             kv_cache_V_tid;
     int             permanent_fusion;
-    /* Stream and graph-replay state (the reference's CUDA-graph slots, graph.h:89-94). */
+    /* Stream and graph-replay state (the reference's CUDA-graph slots, graph.h:89-94):
+     * hip_graph_state 0 = nothing recorded, 1 = one all-GPU execution done (the next
+     * one is captured), 2 = captured (executions replay hip_graph_exec), -1 = not
+     * capturable until the graph or its parameters change. */
     int             hip_graph_state;
-    void*           hip_graph;       /* stream owned by this graph (hipStream_t) */
-    void*           hip_graph_exec;
+    void*           hip_graph;       /* stream owned by this graph (hipStream_t, non-blocking) */
+    void*           hip_graph_exec;  /* instantiated recording of one execution */
     int64_t         graph_cache_B;
     int64_t         graph_cache_S;
+    int             replay_off;      /* graph_set_replay(g, 0) */
 } inference_graph_t;
 
 inference_graph_t* graph_create(void);
@@ -123,6 +127,18 @@ void  graph_set_permanent_fusion(inference_graph_t* g, int enable);
 
 int   graph_execute(inference_graph_t* g, tensor_t* inputs[],
                     tensor_t* outputs[], bool use_cuda);
+
+/* HIP-graph replay of GPU executions (on by default).  GPU executions run on a
+ * non-blocking stream the graph owns.  After one execution in which every node ran on
+ * the GPU, the next execution uploads the graph inputs, records the node launches into a
+ * HIP graph and launches it; later executions only upload the inputs, replay the
+ * recording and download the outputs.  Adding nodes or tensors, graph_build,
+ * graph_set_kv_cache and a changed graph_update_cache_len discard the recording (a
+ * decode loop that moves cache_len every step therefore runs eagerly).  An execution
+ * with a CPU operator, or whose recording fails, stays eager.  graph_set_replay(g, 0)
+ * turns it off; graph_replay_state(g) returns hip_graph_state. */
+void  graph_set_replay(inference_graph_t* g, int enable);
+int   graph_replay_state(const inference_graph_t* g);
 
 /* One self-attention subgraph, the pattern of the reference's detect_and_fuse_mha
  * (graph.c:347-665):

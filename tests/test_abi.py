@@ -242,6 +242,23 @@ def test_graph_execute_cpu_matches_oracle(cpu_ops):
     lib.inference_session_destroy(s)       # owns and destroys the graph
 
 
+def test_graph_replay_state_machine_cpu(cpu_ops):
+    """HIP-graph replay only concerns GPU executions: CPU executions leave the state at 0,
+    graph_set_replay resets it, and the state API accepts NULL."""
+    lib = cpu_ops
+    c = FusedCase(1, 4, 2, 2, 8, fill="lcg", residual=True)
+    g, nid, tX, tY = build_fused_graph(lib, c)
+    ins, outs = (c_void_p * 1)(tX), (c_void_p * 1)(tY)
+    for _ in range(3):
+        assert lib.graph_execute(g.g, ins, outs, False) == 0
+        assert lib.graph_replay_state(g.g) == 0
+    assert np.array_equal(g.read(tY, c.X.shape), c.oracle())
+    lib.graph_set_replay(g.g, 0)
+    assert lib.graph_replay_state(g.g) == 0
+    assert lib.graph_replay_state(None) == 0
+    g.destroy()
+
+
 def test_graph_decode_kv_cache_steps_cpu(cpu_ops):
     """OP_MHA_DECODE with in-place caches and graph_update_cache_len over two steps."""
     lib = cpu_ops

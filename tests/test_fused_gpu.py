@@ -200,6 +200,61 @@ def test_graph_runs_unfused_attention_as_one_fused_op(gpu, native, f16, causal):
         g.destroy()
 
 
+@pytest.mark.parametrize("f16", [False, True])
+def test_graph_replay_matches_eager(gpu, native, f16):
+    """GPU executions of an unchanged graph are recorded into a HIP graph on the second
+    run and replayed after it.  Five executions with a new input each, with eager work
+    (a direct operator call on the legacy stream) and synchronisations between them: every
+    replayed result equals, bit for bit, the same graph run with replay off, and is
+    within the bound of the oracle.  Changing the graph discards the recording."""
+    import cudaforge_amd as cf
+    from helpers import DT_F16, DT_F32, OP_INPUT, OP_OUTPUT, Graph, build_attention_subgraph
+    import oracle as O
+    c = FusedCase(2, 64, 4, 4, 32, seed=41, f16=f16, residual=True, bias_std=0.02)
+    dt, npdt = (DT_F16, np.float16) if f16 else (DT_F32, np.float32)
+    conv = (lambda a: O.to_f16(a)) if f16 else (lambda a: np.asarray(a, np.float32))
+    graphs = []
+    try:
+        for replay in (1, 0):
+            g = Graph(native)
+            graphs.append(g)
+            tX, iX = g.tensor(conv(c.X), dt)
+            tR, iR = g.tensor(conv(c.R), dt)
+            ids = build_attention_subgraph(g, c, iX, iR)
+            native.graph_set_input(g.g, g.node(OP_INPUT, [], [iX]))
+            native.graph_set_output(g.g, g.node(OP_OUTPUT, [ids["out"]], []))
+            assert native.graph_build(g.g) == 0
+            native.graph_set_replay(g.g, replay)
+            g.tX = tX
+            g.tY = g.tensor(np.zeros(c.X.shape, npdt), dt)[0]
+        side_in = cf.DeviceBuffer.from_numpy(np.ones(4096, np.float32))
+        side_out = cf.DeviceBuffer.empty((64, 64), np.float32)
+        states = []
+        for it in range(5):
+            X = conv(O.normal(c.X.shape, 900 + it))
+            outs = []
+            for g in graphs:
+                g.write(g.tX, X)
+                ins, os_ = (ctypes.c_void_p * 1)(g.tX), (ctypes.c_void_p * 1)(g.tY)
+                assert native.graph_execute(g.g, ins, os_, True) == 0
+                outs.append(g.read(g.tY, c.X.shape, npdt).astype(np.float32))
+            states.append(native.graph_replay_state(graphs[0].g))
+            assert np.array_equal(outs[0], outs[1]), f"execution {it}"
+            want = O.mha_fused(np.asarray(X, np.float32), c.R, c.WQ, c.bQ, c.WK, c.bK, c.WV, c.bV, c.WO, c.bO,
+                               O.fused_params(c.B, c.S, c.D, c.H, c.H_kv, c.d, True, False))
+            assert max_abs(want, outs[0]) <= (TOL16 if f16 else TOL32)
+            # Eager work on the legacy stream between replays.
+            assert cf.call_op("causal_mask_f32_cuda", [side_in], [side_out], cf.CausalMaskParams(64)) == 0
+            native.gpu_stream_synchronize(None)
+        assert states == [1, 2, 2, 2, 2]
+        assert native.graph_replay_state(graphs[1].g) == 0
+        graphs[0].tensor(np.zeros(4, npdt), dt)          # changing the graph drops the recording
+        assert native.graph_replay_state(graphs[0].g) == 0
+    finally:
+        for g in graphs:
+            g.destroy()
+
+
 def test_graph_fuses_every_layer(gpu, native):
     """Two stacked attention blocks, each with the residual from its own input (BERT's
     wiring): both run fused; the reference fused only the first (graph.c:655)."""
