@@ -543,25 +543,27 @@ int graph_execute(inference_graph_t* g, tensor_t* inputs[], tensor_t* outputs[],
         if (ret == 0) ret = gpu_graph_launch(g->hip_graph_exec, g->hip_graph);
     } else if (replay && g->hip_graph_state == 1) {
         /* Record this execution's launches, then run the recording. */
-        int all_gpu = 0, crc;
+        int all_gpu = 0, recorded = 0;
         void* exec = NULL;
         ret = preload_inputs(g, fresh);
-        if (ret == 0 && (ret = gpu_capture_begin(g->hip_graph)) == 0) {
-            ret = run_nodes(g, use_cuda, fresh, &all_gpu);
-            crc = gpu_capture_end(g->hip_graph, &exec);
-            if (ret == 0 && crc == 0 && all_gpu) {
+        if (ret == 0 && gpu_capture_begin(g->hip_graph) == 0) {
+            const int rrc = run_nodes(g, use_cuda, fresh, &all_gpu);
+            const int crc = gpu_capture_end(g->hip_graph, &exec);
+            if (rrc == 0 && crc == 0 && all_gpu) {
                 g->hip_graph_exec = exec;
                 g->hip_graph_state = 2;
+                recorded = 1;
                 ret = gpu_graph_launch(exec, g->hip_graph);
-            } else {
-                /* Not recordable: run it eagerly, and do not try again until the graph
-                 * or its parameters change. */
-                gpu_graph_exec_destroy(exec);
-                (void)gpu_get_last_error();
-                g->hip_graph_state = -1;
-                memset(fresh, 0, (size_t)(g->num_tensors > 0 ? g->num_tensors : 1));
-                ret = run_nodes(g, use_cuda, fresh, &all_gpu);
             }
+        }
+        if (ret == 0 && !recorded) {
+            /* Not recordable: run it eagerly, and do not try again until the graph or
+             * its parameters change. */
+            gpu_graph_exec_destroy(exec);
+            (void)gpu_get_last_error();
+            g->hip_graph_state = -1;
+            memset(fresh, 0, (size_t)(g->num_tensors > 0 ? g->num_tensors : 1));
+            ret = run_nodes(g, use_cuda, fresh, &all_gpu);
         }
     } else {
         int all_gpu = 0;

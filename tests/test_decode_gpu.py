@@ -308,6 +308,50 @@ def test_graph_decode_two_steps_on_gpu(gpu, native, f16):
         g.destroy()
 
 
+@pytest.mark.parametrize("f16", [False, True])
+def test_graph_decode_replay(gpu, native, f16):
+    """A decode graph executed repeatedly at one cache_len (each execution rewrites row
+    cache_len) is recorded on its second execution and replayed after; a length change
+    drops the recording.  Every execution equals, bit for bit, the same graph with replay
+    off, and the oracle."""
+    from helpers import build_decode_graph
+    dt = np.float16 if f16 else np.float32
+    tol = TOL16 if f16 else TOL32
+    c = DecodeCase(2, 8, 2, 64, 16, cache_len=5, seed=61, f16=f16, wstd=0.1)
+    graphs = [build_decode_graph(native, c) for _ in range(2)]
+    native.graph_set_replay(graphs[1][0].g, 0)
+    try:
+        states = []
+        for it, cl in enumerate([5, 5, 5, 5, 6, 6, 6]):
+            X = O.normal(c.X.shape, 700 + it)
+            if f16:
+                X = O.round_f16(X)
+            outs = []
+            for g, t in graphs:
+                g.write(t["X"], O.to_f16(X) if f16 else X)
+                native.graph_update_cache_len(g.g, cl)
+                ins, os_ = (ctypes.c_void_p * 1)(t["X"]), (ctypes.c_void_p * 1)(t["Y"])
+                assert native.graph_execute(g.g, ins, os_, True) == 0
+                outs.append(g.read(t["Y"], c.X.shape, dt).astype(np.float32))
+            states.append(native.graph_replay_state(graphs[0][0].g))
+            assert np.array_equal(outs[0], outs[1]), f"execution {it}"
+            # Each execution rewrites row cl and attends rows 0..cl: rows below 5 are the
+            # initial history, row 5 (for cl = 6) holds the last execution at cl = 5.
+            want_case = DecodeCase(2, 8, 2, 64, 16, cache_len=cl, seed=61, f16=f16, wstd=0.1)
+            want_case.X = X
+            if cl == 5:
+                last_x5 = X
+            else:
+                prev = DecodeCase(2, 8, 2, 64, 16, cache_len=5, seed=61, f16=f16, wstd=0.1)
+                prev.X = last_x5
+                _, want_case.Kc, want_case.Vc = prev.oracle()
+            assert max_abs(want_case.oracle()[0], outs[0]) <= tol
+        assert states == [1, 2, 2, 2, 1, 2, 2]
+    finally:
+        for g, _ in graphs:
+            g.destroy()
+
+
 @pytest.mark.parametrize("bn", [64, 128, 256])
 def test_projection_tile_widths(gpu, native, bn):
     """The fp16 projection kernel at each column-tile width (64/128/256) gives the same
