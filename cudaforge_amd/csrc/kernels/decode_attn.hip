@@ -46,6 +46,7 @@ constexpr int kF32Threads = 256;
 constexpr int kF32Unroll = 4;
 constexpr int kGenericThreads = 128;
 constexpr int kMergeThreads = 256;
+constexpr int kMergeWaveSplits = 16;       // merge_wave holds every split in registers
 
 __device__ __forceinline__ float to_f(float x) { return x; }
 __device__ __forceinline__ float to_f(_Float16 x) { return (float)x; }
@@ -86,11 +87,19 @@ __device__ __forceinline__ int kswz(int row) { return (row / (128 / D)) % (D / 8
 template <int D>
 __device__ __forceinline__ int vswz(int row) { return 2 * ((row / (128 / D)) % (D / 16)); }
 
-template <int D, int G, int NS>
-__global__ __launch_bounds__(64)
+// WIDE: one workgroup per (split, b) with one wave per KV head (H_kv <= 8 waves), each
+// wave streaming its head's 16-position blocks through its own 2-stage ring.  The waves
+// of a workgroup read the same cache rows at about the same time, so the DRAM sees whole
+// rows (all KV heads) instead of one head's slice at a time: a streaming probe with the
+// config-2 layout reads 6.1 TB/s this way against 5.5-5.9 TB/s with one workgroup per
+// (split, KV head).  With 16 positions per block, P.V runs on v_mfma_f32_16x16x16_f16,
+// whose B operand is exactly the four probabilities a score lane holds.
+template <int D, int G, int NS, bool WIDE = false>
+__global__ __launch_bounds__(WIDE ? 512 : 64)
 void split_f16(cf_decode_attn_args_t a) {
     constexpr int KT = D / 32;          // 32-dim MFMA steps per 16 positions
-    constexpr int BP = 32;              // positions per block
+    constexpr int BP = WIDE ? 16 : 32;  // positions per block
+    constexpr int NH = BP / 16;         // 16-position row blocks per block
     constexpr int CPR = D / 8;          // 16-byte chunks per row
     constexpr int RPI = 64 / CPR;       // rows per DMA instruction (1 KB)
     constexpr int NI = BP / RPI;        // DMA instructions per block per tensor
@@ -100,16 +109,20 @@ void split_f16(cf_decode_attn_args_t a) {
     constexpr int HDR = part_hdr(G);
     static_assert((NS - 1) * NL < 64, "vmcnt range");
     constexpr int QH = (G * D * 2 + 1023) / 1024 * 512;   // halves of the Q area (whole DMA KBs)
-    __shared__ __attribute__((aligned(16))) _Float16 ring[NS * 2 * TILE + QH];
+    constexpr int WAVE_LDS = NS * 2 * TILE + QH;          // halves of one wave's ring + Q area
+    __shared__ __attribute__((aligned(16))) _Float16 ring_all[(WIDE ? 8 : 1) * WAVE_LDS];
 
-    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int split = blockIdx.x;
+    const int kvh = WIDE ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : (int)blockIdx.y;   // wave-uniform
+    const int b = WIDE ? (int)blockIdx.y : (int)blockIdx.z;
+    _Float16* ring = ring_all + (WIDE ? kvh * WAVE_LDS : 0);
     const int T_b = attended(a, b);
     const int t0 = split * a.chunk;
     if (t0 >= T_b) return;
     const int t1 = min(t0 + a.chunk, T_b);
     const int nblk = (t1 - t0 + BP - 1) / BP;
     const int nsplit_b = (T_b + a.chunk - 1) / a.chunk;
-    const int lane = threadIdx.x, lr = lane & 15, lq = lane >> 4;
+    const int lane = threadIdx.x & 63, lr = lane & 15, lq = lane >> 4;
 
     const size_t row_stride = (size_t)a.H_kv * D;
     const size_t unit_off = ((size_t)b * a.max_seq * a.H_kv + kvh) * D;
@@ -158,19 +171,19 @@ void split_f16(cf_decode_attn_args_t a) {
     };
 
     // Per-lane LDS read offsets (halves) inside a stage.
-    int k_rd[2][KT];
+    int k_rd[NH][KT];
 #pragma unroll
-    for (int h = 0; h < 2; h++)
+    for (int h = 0; h < NH; h++)
 #pragma unroll
         for (int kt = 0; kt < KT; kt++) {
             const int row = 16 * h + lr;
             k_rd[h][kt] = row * D + 8 * ((4 * kt + lq) ^ kswz<D>(row));
         }
-    int v_rd[NT][2];
+    int v_rd[NT][NH];
 #pragma unroll
     for (int n = 0; n < NT; n++)
 #pragma unroll
-        for (int hh = 0; hh < 2; hh++) {
+        for (int hh = 0; hh < NH; hh++) {
             const int row = 16 * hh + 4 * lq + (lr >> 2);
             const int col = 16 * n + 4 * (lr & 3);                  // halves
             v_rd[n][hh] = TILE + row * D + 8 * ((col >> 3) ^ vswz<D>(row)) + (col & 7);
@@ -216,9 +229,9 @@ void split_f16(cf_decode_attn_args_t a) {
         }
 
         const _Float16* st = ring + stage * 2 * TILE;
-        f4_t s[2];
+        f4_t s[NH];
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
+        for (int h = 0; h < NH; h++) {
             s[h] = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kt = 0; kt < KT; kt++)
@@ -227,21 +240,21 @@ void split_f16(cf_decode_attn_args_t a) {
         // Raw scores; positions past t1 (last block only) -> -inf.  scale > 0, so the
         // max of the raw scores times scale*log2(e) is the max of the scaled ones.
         const int p0 = t0 + blk * BP;
-        float x[8];
+        float x[4 * NH];
 #pragma unroll
-        for (int h = 0; h < 2; h++)
+        for (int h = 0; h < NH; h++)
 #pragma unroll
             for (int j = 0; j < 4; j++) x[4 * h + j] = s[h][j];
         if (p0 + BP > t1) {
 #pragma unroll
-            for (int h = 0; h < 2; h++)
+            for (int h = 0; h < NH; h++)
 #pragma unroll
                 for (int j = 0; j < 4; j++)
                     if (p0 + 16 * h + 4 * lq + j >= t1) x[4 * h + j] = -INFINITY;
         }
         float mb = x[0];
 #pragma unroll
-        for (int i = 1; i < 8; i++) mb = fmaxf(mb, x[i]);
+        for (int i = 1; i < 4 * NH; i++) mb = fmaxf(mb, x[i]);
         mb = max_xor32(max_xor16(mb)) * qk_scale;                   // finite: p0 < t1
         // The running max moves only when a block exceeds it by more than kLazyMax (log2
         // units): until then p = 2^(s - m) <= 2^kLazyMax, exact enough in fp16 and far
@@ -258,18 +271,26 @@ void split_f16(cf_decode_attn_args_t a) {
             for (int n = 0; n < NT; n++) acc[n] *= alpha;
         }
         float ps = 0.0f;
-        h8_t pf;
+        _Float16 pv[4 * NH];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
+        for (int i = 0; i < 4 * NH; i++) {
             const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(x[i], qk_scale, -m_run));
             ps += p;
-            pf[i] = (_Float16)p;
+            pv[i] = (_Float16)p;
         }
         l_run += ps;
+        if constexpr (NH == 2) {
+            const h8_t pf = {pv[0], pv[1], pv[2], pv[3], pv[4], pv[5], pv[6], pv[7]};
 #pragma unroll
-        for (int n = 0; n < NT; n++) {
-            const h8_t vf = cat8(ds_read_tr4(st + v_rd[n][0]), ds_read_tr4(st + v_rd[n][1]));
-            acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, acc[n], 0, 0, 0);
+            for (int n = 0; n < NT; n++) {
+                const h8_t vf = cat8(ds_read_tr4(st + v_rd[n][0]), ds_read_tr4(st + v_rd[n][1]));
+                acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, acc[n], 0, 0, 0);
+            }
+        } else {
+            const h4_t pf = {pv[0], pv[1], pv[2], pv[3]};
+#pragma unroll
+            for (int n = 0; n < NT; n++)
+                acc[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(ds_read_tr4(st + v_rd[n][0]), pf, acc[n], 0, 0, 0);
         }
     };
     for_each_stage<NS>(nblk, step);
@@ -667,6 +688,7 @@ template <typename T, int DPL>
 __global__ __launch_bounds__(256)
 void merge_wave(cf_decode_attn_args_t a, int Gx, int units_per_b, int rows) {
     constexpr int D = 64 * DPL;
+    constexpr int MAXS = kMergeWaveSplits;
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
@@ -675,41 +697,37 @@ void merge_wave(cf_decode_attn_args_t a, int Gx, int units_per_b, int rows) {
     if (nsplit <= 1) return;                       // finished by the split kernel
     const int stride = part_stride(Gx, D), hdr = part_hdr(Gx);
     const float* part = a.partials + (size_t)unit * a.n_split * stride;
-    float M = -INFINITY;
-    for (int sp = lane; sp < nsplit; sp += 64) M = fmaxf(M, part[(size_t)sp * stride + g]);
+    // Every load first (one round trip): lane s < nsplit holds split s's (m, l), and each
+    // lane the DPL accumulator values of every split for its dims.
+    float mv = -INFINITY, lv = 0.0f;
+    if (lane < nsplit) {
+        mv = part[(size_t)lane * stride + g];
+        lv = part[(size_t)lane * stride + Gx + g];
+    }
+    float av[MAXS][DPL];
+#pragma unroll
+    for (int j = 0; j < MAXS; j++) {
+        const bool ok = j < nsplit;
+        const float* ps = part + (size_t)(ok ? j : 0) * stride + hdr + g * D + DPL * lane;
+#pragma unroll
+        for (int e = 0; e < DPL; e++) av[j][e] = ok ? ps[e] : 0.0f;
+    }
+    float M = mv;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-    float den = 0.0f;
+    const float w = lane < nsplit ? exp2f(mv - M) : 0.0f;
+    float den = w * lv;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) den += __shfl_xor(den, off, 64);
     float num[DPL];
 #pragma unroll
     for (int e = 0; e < DPL; e++) num[e] = 0.0f;
-    for (int s0 = 0; s0 < nsplit; s0 += 64) {
-        const int sp = s0 + lane;
-        float w = 0.0f;
-        if (sp < nsplit) {
-            w = exp2f(part[(size_t)sp * stride + g] - M);
-            den = __builtin_fmaf(w, part[(size_t)sp * stride + Gx + g], den);
-        }
-        const int n = min(64, nsplit - s0);
-        for (int j0 = 0; j0 < n; j0 += 8) {
-            float ws[8];
-            float av[8][DPL];
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                ws[j] = __shfl(w, j0 + j, 64);
-                const bool ok = j0 + j < n;
-                const float* ps = part + (size_t)(s0 + (ok ? j0 + j : 0)) * stride + hdr + g * D + DPL * lane;
+    for (int j = 0; j < MAXS; j++) {
+        const float wj = __shfl(w, j, 64);        // 0 for j >= nsplit
 #pragma unroll
-                for (int e = 0; e < DPL; e++) av[j][e] = ok ? ps[e] : 0.0f;
-            }
-#pragma unroll
-            for (int j = 0; j < 8; j++)
-#pragma unroll
-                for (int e = 0; e < DPL; e++) num[e] = __builtin_fmaf(ws[j], av[j][e], num[e]);
-        }
+        for (int e = 0; e < DPL; e++) num[e] = __builtin_fmaf(wj, av[j][e], num[e]);
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) den += __shfl_xor(den, off, 64);
     const float inv = 1.0f / den;
     T* out = (T*)a.o + (size_t)row * D + DPL * lane;
 #pragma unroll
@@ -736,6 +754,8 @@ bool use_fast(const cf_decode_attn_args_t* a) {
 int g_stages = 0;   // tuning override of the fp16 ring depth (2..4; 0 = kDecodeStages)
 int g_merge_rows = 0;   // 1: use the workgroup-per-row merge for every head size (tests)
 
+int g_wide = 1;     // 0: one workgroup per (split, KV head) even where the grouped kernel applies
+
 int f16_stages() { return g_stages >= 2 && g_stages <= 4 ? g_stages : kDecodeStages; }
 
 // Static LDS of split_f16<D, G, NS>: the ring plus the Q area.
@@ -744,10 +764,27 @@ int f16_lds_bytes(int d, int G, int NS) {
     return (NS * 2 * 32 * d + qh) * 2;
 }
 
+// The grouped (WIDE) fp16 split kernel: 2-stage rings of 16-position blocks, one wave per
+// KV head, static LDS for 8 waves.
+constexpr int kWideStages = 2;
+constexpr int kWideMaxHeads = 8;
+int wide_lds_bytes(int d, int G) {
+    const int qh = (G * d * 2 + 1023) / 1024 * 512;
+    return kWideMaxHeads * (kWideStages * 2 * 16 * d + qh) * 2;
+}
+// Uniform lengths only: with ragged lengths the grouped kernel's whole-row workgroups
+// leave a partial last round (config 4: 67 us against 64.6 us one wave per KV head).
+bool use_wide(const cf_decode_attn_args_t* a) {
+    return g_wide && a->elem == CF_ELEM_F16 && !a->seq_lens && a->H_kv <= kWideMaxHeads && use_fast(a);
+}
+
 template <int D, int G>
 hipError_t launch_split_fast(const cf_decode_attn_args_t& a, hipStream_t s) {
     dim3 grid((unsigned)a.n_split, (unsigned)a.H_kv, (unsigned)a.B);
-    if (a.elem == CF_ELEM_F16) {
+    if (use_wide(&a)) {
+        hipLaunchKernelGGL((split_f16<D, G, kWideStages, true>), dim3((unsigned)a.n_split, (unsigned)a.B),
+                           dim3(64 * (unsigned)a.H_kv), 0, s, a);
+    } else if (a.elem == CF_ELEM_F16) {
         switch (f16_stages()) {
             case 2: hipLaunchKernelGGL((split_f16<D, G, 2>), grid, dim3(64), 0, s, a); break;
             case 3: hipLaunchKernelGGL((split_f16<D, G, 3>), grid, dim3(64), 0, s, a); break;
@@ -781,6 +818,14 @@ extern "C" int32_t cf_decode_attn_chunk_quantum(int32_t elem, int32_t d, int32_t
 extern "C" void cf_decode_attn_set_stages(int32_t stages) { g_stages = stages; }
 
 extern "C" void cf_decode_attn_set_merge_rows(int32_t on) { g_merge_rows = on != 0; }
+
+extern "C" void cf_decode_attn_set_wide(int32_t on) { g_wide = on != 0; }
+
+extern "C" int32_t cf_decode_attn_wide_wgs_per_cu(int32_t elem, int32_t d, int32_t group, int32_t h_kv) {
+    if (!g_wide || elem != CF_ELEM_F16 || h_kv > kWideMaxHeads || !fast_supported(elem, d, group)) return 0;
+    const int n = kLdsPerCu / wide_lds_bytes(d, group);
+    return n < 1 ? 1 : n;
+}
 
 extern "C" int32_t cf_decode_attn_wgs_per_cu(int32_t elem, int32_t d, int32_t group) {
     if (elem != CF_ELEM_F16 || !fast_supported(elem, d, group)) return 0;
@@ -829,7 +874,7 @@ extern "C" int cf_launch_decode_attn_merge(const cf_decode_attn_args_t* a, void*
     const int rows = a->B * units_per_b * Gx;
     // One wave per row while the splits fit a few rounds of eight loads; with many
     // splits (long or ragged caches) a whole workgroup per row keeps more in flight.
-    if ((a->d == 64 || a->d == 128) && a->n_split <= 16 && !g_merge_rows) {
+    if ((a->d == 64 || a->d == 128) && a->n_split <= kMergeWaveSplits && !g_merge_rows) {
         const dim3 grid((unsigned)((rows + 3) / 4)), blk(256);
         if (a->elem == CF_ELEM_F16) {
             if (a->d == 64) hipLaunchKernelGGL((merge_wave<_Float16, 1>), grid, blk, 0, s, *a, Gx, units_per_b, rows);

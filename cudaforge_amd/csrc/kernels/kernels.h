@@ -49,6 +49,12 @@ int32_t cf_decode_attn_chunk_max(int32_t elem, int32_t d, int32_t group);
 int32_t cf_decode_attn_wgs_per_cu(int32_t elem, int32_t d, int32_t group);
 /* Tuning override of the fp16 split kernel's LDS ring depth (2..4; 0 = default 3). */
 void    cf_decode_attn_set_stages(int32_t stages);
+/* The grouped fp16 split kernel (one workgroup per (split, b), one wave per KV head,
+ * H_kv <= 8): workgroups per CU, or 0 where it does not apply.  The chunk planner sizes
+ * the split count by it.  cf_decode_attn_set_wide(0) selects the one-wave-per-(split, KV
+ * head) kernel everywhere (tests and measurements; default 1). */
+int32_t cf_decode_attn_wide_wgs_per_cu(int32_t elem, int32_t d, int32_t group, int32_t h_kv);
+void    cf_decode_attn_set_wide(int32_t on);
 /* Tests: 1 selects the workgroup-per-row merge for every head size (0 = the one-wave
  * merge for d = 64 / 128). */
 void    cf_decode_attn_set_merge_rows(int32_t on);

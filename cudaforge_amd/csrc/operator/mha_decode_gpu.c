@@ -61,11 +61,13 @@ static void plan_split(int elem, const decode_shape_t* s, int64_t t_max, int64_t
     if (g_chunk_override > 0) {
         c = cf_ceil_div(g_chunk_override, q) * q;
     } else {
-        /* Enough workgroups to keep every CU's memory pipeline full.  The fp16 kernel
-         * is one wave with an LDS ring, as many per CU as the ring allows; the others
-         * are 2-4 waves with registers as their only buffer. */
-        const int64_t units = s->B * (fast ? s->H_kv : s->H);
-        const int32_t ring_cu = cf_decode_attn_wgs_per_cu(elem, (int)s->d, G);
+        /* Enough workgroups to keep every CU's memory pipeline full.  The grouped fp16
+         * kernel is one workgroup per (split, b) covering every KV head, the other fp16
+         * kernel one wave per (split, b, KV head), each as many per CU as its LDS rings
+         * allow; the others are 2-4 waves with registers as their only buffer. */
+        const int32_t wide_cu = s->ragged ? 0 : cf_decode_attn_wide_wgs_per_cu(elem, (int)s->d, G, (int)s->H_kv);
+        const int64_t units = wide_cu > 0 ? s->B : s->B * (fast ? s->H_kv : s->H);
+        const int32_t ring_cu = wide_cu > 0 ? wide_cu : cf_decode_attn_wgs_per_cu(elem, (int)s->d, G);
         const int64_t per_cu = ring_cu > 0 ? ring_cu : 4;
         int64_t target = per_cu * (int64_t)cf_cu_count();
         /* Ragged: the grid spans max_seq, but a sequence only runs the splits its length
