@@ -442,7 +442,7 @@ def main() -> int:
                                "(split kernel + merge kernel per step)", **cfg},
         "roofline": {"bound": "hbm", "achieved": round(gbs_split, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs_split / HBM_PEAK_GBS, 4), "traffic": read_traffic("split_f16"),
-                     "kernel": "split_f16<128,4,3> (decode_attn.hip)", "alg_bytes_per_launch": alg_bytes,
+                     "kernel": "split_f16<128,4,2,wide> (decode_attn.hip; a workgroup per (split, batch row), a wave per KV head)", "alg_bytes_per_launch": alg_bytes,
                      "kernel_us": round(ms_split * 1e3, 2), "merge_kernel_us": round(ms_merge * 1e3, 2)},
         "cpu_baseline": cpu,
         "extra": extra,
