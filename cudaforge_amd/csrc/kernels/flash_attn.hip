@@ -18,8 +18,9 @@
 // O^T += V^T·P^T; the key order inside each 32-key MFMA step is permuted so that the
 // registers a lane already holds are exactly its B operand (the V^T reads follow the
 // same permutation).  No score or probability goes through LDS.  Masks are evaluated
-// only on blocks that cross the sequence end or the causal diagonal; causal workgroups
-// are issued heaviest-first.
+// only on blocks that cross the sequence end or the causal diagonal.  Causal workgroups
+// of this kernel are issued heaviest-first; the DMA kernel below pairs each causal query
+// block with its mirror so every workgroup has the same work.
 //
 // Generic path (fp32, or other head sizes): one thread per query, online softmax in
 // fp32 with Q and the accumulator in LDS.
@@ -262,16 +263,20 @@ void flash_f16_dma64(cf_flash_args_t a) {
     static_assert(NS == 3, "the prologue issues two blocks");
     __shared__ __attribute__((aligned(16))) _Float16 ring[NS * 2 * TILE];
 
+    // Causal: workgroup slot qi runs query block nqb-1-qi and then its mirror qi, so
+    // every workgroup does nqb+1 key blocks whatever the order the CUs receive them in
+    // (one block per slot when the two meet).
     const int nqb = (a.S + QB - 1) / QB;
+    const int nslot = a.causal ? (nqb + 1) / 2 : nqb;
     const int HB = a.B * a.H_q;
     const int w = blockIdx.x, r8 = w & 7, rest = w >> 3;
-    const int qi = rest % nqb, grp = rest / nqb;
+    const int qi = rest % nslot, grp = rest / nslot;
     const int hb = grp * 8 + r8;
     if (hb >= HB) return;                          // padding of the last group of 8
-    const int qb = a.causal ? (nqb - 1 - qi) : qi;
     const int h = hb % a.H_q, b = hb / a.H_q;
     const int S = a.S;
     const int kvh = h / (a.H_q / a.H_kv);
+  auto run = [&](int qb) {
     const int q0 = qb * QB;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 15, lq = lane >> 4;
@@ -497,6 +502,18 @@ void flash_f16_dma64(cf_flash_args_t a) {
                           __builtin_bit_cast(uint32_t, ta[0]), __builtin_bit_cast(uint32_t, ta[1])};
         }
     }
+  };
+    if (!a.causal) {
+        run(qi);
+        return;
+    }
+    const int heavy = nqb - 1 - qi;
+    run(heavy);
+    if (qi < heavy) {
+        wait_vm<0>();                              // the first block's output stores
+        ring_barrier();                            // every wave is done with the ring
+        run(qi);
+    }
 }
 
 __device__ __forceinline__ float to_f(float x) { return x; }
@@ -576,9 +593,12 @@ extern "C" int cf_launch_flash_attn(const cf_flash_args_t* a, void* stream) {
             // them the waves per SIMD that hide each block's latency chain; 32 per wave
             // halves the LDS traffic per query (every wave reads the whole K/V^T block),
             // better once there are two 128-query workgroups per CU.
-            const int nj = g_flash_mode == 1 ? 2 : g_flash_mode == 2 ? 1 : (groups * nqb * 8 < 2LL * cu_count() ? 1 : 2);
-            const long long nqb2 = (a->S + 64 * nj - 1) / (64 * nj);
-            dim3 grid2((unsigned)(groups * nqb2 * 8));
+            auto slots = [&](int nj) {                 // causal pairs query blocks
+                const long long n = (a->S + 64 * nj - 1) / (64 * nj);
+                return a->causal ? (n + 1) / 2 : n;
+            };
+            const int nj = g_flash_mode == 1 ? 2 : g_flash_mode == 2 ? 1 : (groups * slots(2) * 8 < 2LL * cu_count() ? 1 : 2);
+            dim3 grid2((unsigned)(groups * slots(nj) * 8));
             if (nj == 1) hipLaunchKernelGGL(flash_f16_dma64<1>, grid2, dim3(kThreads), 0, s, *a);
             else hipLaunchKernelGGL(flash_f16_dma64<2>, grid2, dim3(kThreads), 0, s, *a);
         } else if (a->d == 64) hipLaunchKernelGGL(flash_f16<64>, grid, dim3(kThreads), 0, s, *a);
