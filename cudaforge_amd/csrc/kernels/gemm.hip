@@ -461,31 +461,32 @@ void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
     // Wave w fills A slices u = 2w, 2w+1 (rows 16u .. 16u+15; lane L owns physical chunk
     // L%4) and W instructions u = w and w + 4 (when < W_INSTR) of every stage; W
     // instruction u covers the stage's chunks 64u .. 64u+63 in row-major order.
+    // Loads are a uniform base (the k-step's first column of A, first row of W) plus
+    // per-lane byte offsets fixed for the whole loop (the launcher keeps M*K*2 and K*N*2
+    // below 2^32), so issuing them is scalar work.
     const int nw = (wave + 4 < W_INSTR) ? 2 : 1;   // W instructions of this wave
-    size_t a_off[2], w_off[2];
+    uint32_t a_off[2], w_off[2];
 #pragma unroll
     for (int v = 0; v < 2; v++) {
         const int u = 2 * wave + v;
         const int ra = 16 * u + (lane >> 2), ca = (lane & 3) ^ swz_a(ra);
-        a_off[v] = (size_t)(m0 + ra) * K + 8 * ca;
+        a_off[v] = ((uint32_t)(m0 + ra) * (uint32_t)K + 8u * (uint32_t)ca) * 2u;
         const int q = 64 * (wave + 4 * v) + lane;  // W chunk index in the stage
         const int rw = q / CPR, cw = (q % CPR) ^ swz_w<BNT>(rw);
-        w_off[v] = (size_t)rw * N + n0 + 8 * cw;
+        w_off[v] = ((uint32_t)rw * (uint32_t)N + (uint32_t)(n0 + 8 * cw)) * 2u;
     }
-    const uint32_t smem_base = lds_offset(smem);
-    auto issue = [&](int stage, int k0) {
-        const uint32_t base = smem_base + (uint32_t)(stage * ST) * 2u;
+    const uint32_t wave_lds = __builtin_amdgcn_readfirstlane(lds_offset(smem) + (uint32_t)(2 * wave) * 1024u);
+    const uint32_t wave_lds_w = __builtin_amdgcn_readfirstlane(lds_offset(smem) + (uint32_t)(A_ST * 2 + wave * 1024));
+    auto issue = [&](int k0, auto stage_c) {
+        constexpr int stage = decltype(stage_c)::value;
+        const _Float16* ab = A + k0;
+        const _Float16* wb = W + (size_t)k0 * N;
 #pragma unroll
-        for (int v = 0; v < 2; v++) {
-            const int u = 2 * wave + v;
-            lds_dma16(A + a_off[v] + k0, __builtin_amdgcn_readfirstlane(base + (uint32_t)u * 1024u));
-        }
+        for (int v = 0; v < 2; v++)
+            lds_dma16_s(a_off[v], ab, wave_lds + (uint32_t)(stage * ST * 2 + v * 1024));
 #pragma unroll
-        for (int v = 0; v < 2; v++) {
-            if (v < nw)
-                lds_dma16(W + w_off[v] + (size_t)k0 * N,
-                          __builtin_amdgcn_readfirstlane(base + (uint32_t)(A_ST * 2 + (wave + 4 * v) * 1024)));
-        }
+        for (int v = 0; v < 2; v++)
+            if (v < nw) lds_dma16_s(w_off[v], wb, wave_lds_w + (uint32_t)(stage * ST * 2 + 4 * v * 1024));
     };
 
     f4_t acc[4][NJ];
@@ -511,20 +512,24 @@ void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
         }
 
     const int nk = K / BKA;
-#pragma unroll
-    for (int s = 0; s < STAGES - 1; s++)
-        if (s < nk) issue(s, s * BKA);
+    if (0 < nk) issue(0, std::integral_constant<int, 0>{});
+    if (1 < nk) issue(BKA, std::integral_constant<int, 1>{});
+    if constexpr (STAGES > 3)
+        if (2 < nk) issue(2 * BKA, std::integral_constant<int, 2>{});
+    static_assert(STAGES == 3 || STAGES == 4, "the prologue issues STAGES - 1 tiles");
     // CT: accumulate C^T (operands swapped) for destinations contiguous along n.
     auto main_loop = [&](auto ct_c) {
         constexpr bool CT = decltype(ct_c)::value;
-        for (int kt = 0; kt < nk; kt++) {
+        for_each_stage<STAGES>(nk, [&](int kt, auto stage_c) {
+            constexpr int stage = decltype(stage_c)::value;        // kt % STAGES
             // Tiles issued after kt that may still be in flight: min(STAGES-2, nk-1-kt),
             // 2 + nw load instructions each.
             if (nw == 2) wait_ahead<4, STAGES - 2>(nk - 1 - kt);
             else wait_ahead<3, STAGES - 2>(nk - 1 - kt);
             ring_barrier();
-            if (kt + STAGES - 1 < nk) issue((kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BKA);
-            const _Float16* As = smem + (kt % STAGES) * ST;
+            if (kt + STAGES - 1 < nk)
+                issue((kt + STAGES - 1) * BKA, std::integral_constant<int, (stage + STAGES - 1) % STAGES>{});
+            const _Float16* As = smem + stage * ST;
             const _Float16* Ws = As + A_ST;
             h8_t af[4], bf[NJ];
 #pragma unroll
@@ -537,7 +542,7 @@ void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
                 for (int j = 0; j < NJ; j++)
                     acc[i][j] = CT ? __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[j], af[i], acc[i][j], 0, 0, 0)
                                    : __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
+        });
     };
     // Every DMA load was waited for in the last step, and the epilogue does not touch LDS.
     if (a.out_kind == CF_GEMM_OUT_ROWMAJOR || seg < 2) {
@@ -677,7 +682,9 @@ extern "C" int cf_launch_gemm(const cf_gemm_args_t* a, void* stream) {
     // the balance they buy measured slower (the 4096 x 2304 QKV product: 27.4 us at 96
     // columns, three tiles per CU, vs 26.6 us at 128, 2.25 per CU).
     const long long tiles_m = (a->M + BM - 1) / BM;
-    bool full = a->elem == CF_ELEM_F16 && t.epi_vec && a->M % BM == 0 && a->K % BKA == 0 && t.a_vec;
+    bool full = a->elem == CF_ELEM_F16 && t.epi_vec && a->M % BM == 0 && a->K % BKA == 0 && t.a_vec &&
+                (long long)a->M * a->K * 2 < (1LL << 32);
+    for (int s = 0; s < a->nseg; s++) full = full && (long long)a->K * a->n[s] * 2 < (1LL << 32);
     for (int s = 0; s < a->nseg; s++) full = full && t.w_vec[s];
     auto fits = [&](int bn) {
         for (int s = 0; s < a->nseg; s++)
