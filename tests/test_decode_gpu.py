@@ -309,6 +309,29 @@ def test_graph_decode_two_steps_on_gpu(gpu, native, f16):
         g.destroy()
 
 
+@pytest.mark.parametrize("d,G,H_kv,T", [(128, 4, 8, 3000), (64, 2, 4, 777), (128, 8, 2, 1500), (64, 1, 8, 64),
+                                         (128, 1, 1, 33)])
+def test_grouped_and_one_wave_split_kernels_agree(gpu, native, d, G, H_kv, T):
+    """Uniform lengths take the grouped fp16 split kernel (a workgroup per (split, b), a
+    wave per KV head, 16-position blocks); cf_decode_attn_set_wide(0) forces the one-wave
+    kernel (32-position blocks).  Both within the FP16 bound of the oracle and close to
+    each other, including lengths that end inside a block and a single split."""
+    B = 3
+    H = H_kv * G
+    Q, K, V = (O.round_f16(O.normal(s, 170 + i)) for i, s in enumerate([(B, H, d), (B, T, H_kv, d), (B, T, H_kv, d)]))
+    want = O.decode_attn(Q, K, V, np.full(B, T, np.int32), float(1 / np.sqrt(d)), H_kv)
+    outs = []
+    try:
+        for wide in (1, 0):
+            native.cf_decode_attn_set_wide(wide)
+            outs.append(run_decode_attn_gpu(Q, K, V, T - 1, H_kv, True))
+    finally:
+        native.cf_decode_attn_set_wide(1)
+    for got in outs:
+        assert max_abs(want, got) <= TOL16
+    assert max_abs(outs[0], outs[1]) <= TOL16
+
+
 @pytest.mark.parametrize("f16", [False, True])
 def test_graph_decode_replay(gpu, native, f16):
     """A decode graph executed repeatedly at one cache_len (each execution rewrites row
