@@ -324,6 +324,21 @@ def vendor_comparison(reps: int = 50) -> dict:
     return out
 
 
+def bench_prefill(cf, stream, steps, warmup) -> dict:
+    """Configs 3 and 5 through mha_fused_f16_cuda: TFLOP/s over the algorithmic FLOPs."""
+    out = {}
+    for key, (B, S, H, d, causal, seed) in {
+            "prefill_config3_bert_base_f16": (8, 512, 12, 64, False, 300),
+            "prefill_config5_causal_gpt2_medium_f16": (4, 1024, 16, 64, True, 500)}.items():
+        log(key)
+        ms_p, fl = bench_fused(cf, stream, max(steps // 4, 10), max(warmup // 2, 3), B, S, H, d, causal, seed)
+        tf = fl / (ms_p * 1e-3) / 1e12
+        out[key] = {"us_per_step": round(ms_p * 1e3, 2), "TFLOP_s": round(tf, 1), "alg_flop": fl,
+                    "mfma_frac": round(tf / FP16_PEAK_TFLOPS, 4)}
+        log(f"  {ms_p * 1e3:.1f} us/step {tf:.1f} TFLOP/s")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -332,6 +347,8 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU oracle timing")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-core", action="store_true", help="time only the headline kernel (for profiling)")
+    ap.add_argument("--only-prefill", action="store_true",
+                    help="time only the two prefill configs and print their figures (for counter runs)")
     ap.add_argument("--vendor", action="store_true",
                     help="only time the prefill shapes through torch (hipBLASLt matmul, SDPA) for comparison")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -363,6 +380,10 @@ def main() -> int:
                 raise RuntimeError("calibration copy failed")
         stream.synchronize()
         log(f"calibration: 5 copies of {n} bytes")
+
+    if args.only_prefill:
+        print(json.dumps({"prefill": bench_prefill(cf, stream, steps, warmup)}), flush=True)
+        return 0
 
     log("decode core, config 2")
     ms, ms_split, ms_merge, alg_bytes, cfg = bench_decode_core(cf, stream, steps, warmup)
@@ -401,15 +422,7 @@ def main() -> int:
                                                "GB_s": round(alg_r / (ms_r * 1e-3) / 1e9, 1),
                                                "alg_bytes": alg_r, "lengths": lens,
                                                "hbm_frac": round(alg_r / (ms_r * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-        for key, (B, S, H, d, causal, seed) in {
-                "prefill_config3_bert_base_f16": (8, 512, 12, 64, False, 300),
-                "prefill_config5_causal_gpt2_medium_f16": (4, 1024, 16, 64, True, 500)}.items():
-            log(key)
-            ms_p, fl = bench_fused(cf, stream, max(steps // 4, 10), max(warmup // 2, 3), B, S, H, d, causal, seed)
-            tf = fl / (ms_p * 1e-3) / 1e12
-            extra[key] = {"us_per_step": round(ms_p * 1e3, 2), "TFLOP_s": round(tf, 1), "alg_flop": fl,
-                          "mfma_frac": round(tf / FP16_PEAK_TFLOPS, 4)}
-            log(f"  {ms_p * 1e3:.1f} us/step {tf:.1f} TFLOP/s")
+        extra.update(bench_prefill(cf, stream, steps, warmup))
         log("layer neighbours: LayerNorm F16 (4096 x 768), FFN MatMul F16 (4096 x 768 -> 3072)")
         ms_ln, by_ln, ms_mm, fl_mm = bench_layer_neighbours(cf, stream, max(steps // 4, 10), max(warmup // 2, 3))
         extra["layernorm_f16_4096x768"] = {"us_per_step": round(ms_ln * 1e3, 2),
