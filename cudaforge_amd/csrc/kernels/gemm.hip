@@ -407,41 +407,56 @@ __device__ __forceinline__ void store_cn_f16(const cf_gemm_args_t& a, int seg, i
     }
 }
 
-// ---- pipelined kernel: full tiles only (M % 128, N % BNT, K % 32 == 0, aligned).
-// STAGES LDS stages of 32 k, filled by global_load_lds_dwordx4 (global -> LDS without
+// ---- pipelined kernel: full tiles only (M % 128, N % BNT, K % BK == 0, aligned).
+// STAGES LDS stages of BK k, filled by global_load_lds_dwordx4 (global -> LDS without
 // VGPRs): STAGES-1 k-tiles are in flight while one is multiplied.  A lane-contiguous
 // 1 KB of LDS per load instruction fixes the LDS layout, so the global side is
 // permuted instead: the 16-byte chunk c of row r is stored at chunk c ^ swz(r), which
 // makes the MFMA A reads (16 rows x one chunk) and the W transpose reads (4 rows x 32 B
 // per 16-lane group) hit distinct banks.
-// BNT = 128 or 96 output columns per tile (waves 2 x 2, each 64 rows x BNT/2 columns).
-// The launcher takes 96 where it balances the tiles over the CUs better: BERT-base's
-// 4096 x 2304 QKV product is 768 tiles of 128 x 96 (three per CU) instead of 576 of
-// 128 x 128, and its 4096 x 768 output projection 256 tiles (one per CU) instead of 192.
+// BNT = 128 or 96 output columns per tile (waves 2 x 2, each 64 rows x BNT/2 columns);
+// the launcher takes 96 only where 128 leaves CUs idle.
+// BK = 32 or 64 k per stage.  An A row of a stage is BK * 2 bytes of one 128-byte line:
+// at BK = 32 each load instruction reads half lines of 16 rows, and direct-to-LDS loads
+// of half lines measured ~68 GB/s per CU from L2 against ~118 GB/s for whole lines (three
+// workgroups per CU, 3-deep rings of 16 KB).  BK = 64 reads whole lines at twice the LDS
+// per stage: 2 stages of 32 KB, two workgroups per CU.
 constexpr int BKA = 32;
-constexpr int A_ST = BM * BKA;          // halves per stage: A [128][32]
 
-// A rows are 64 B (4 chunks).  (row >> 1) & 3 is the permutation under which the
-// fragment reads (ds_read_b128, 16 rows x one chunk) measure conflict-free on gfx950
-// (SQ_LDS_BANK_CONFLICT); (row >> 2) & 3 and row & 3 both measure two-way conflicts.
-__device__ __forceinline__ int swz_a(int row) { return (row >> 1) & 3; }
+// A rows are BK * 2 bytes: 4 chunks (BK 32) or 8 (BK 64).  (row >> 1) & (chunks - 1) is
+// the permutation under which the fragment reads (ds_read_b128, 16 rows x one chunk)
+// measure conflict-free on gfx950 (SQ_LDS_BANK_CONFLICT) at BK 32; (row >> 2) & 3 and
+// row & 3 both measure two-way conflicts.  At BK 64 the 16 rows of a read cover all
+// (row & 1, chunk) pairs, i.e. the 16 distinct 16-byte bank slots of a 256-byte row.
+template <int BK>
+__device__ __forceinline__ int swz_a(int row) { return (row >> 1) & (BK / 8 - 1); }
 // W rows are BNT * 2 bytes: 16 chunks (BNT = 128) or 12 (BNT = 96).  The 96-column
 // permutation only flips chunk bit 1, so it stays inside the row's 12 chunks; rows
-// 8 apart (read by the same half-wave) then sit 32 bytes apart in the banks.
+// 8 apart (read by the same half-wave) then sit 32 bytes apart in the banks.  Both
+// depend on row bits 0..3 only, so the rows of the second 32-k half of a BK = 64 stage
+// (row + 32) are permuted like the first.
 template <int BNT>
 __device__ __forceinline__ int swz_w(int row) {
     if constexpr (BNT == 128) return ((row & 3) << 1) ^ (((row >> 3) & 1) << 3);
     else return ((row >> 3) & 1) << 1;
 }
 
-template <int STAGES, int BNT>
+template <int STAGES, int BNT, int BK>
 __global__ __launch_bounds__(kThreads, 2)
 void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
-    constexpr int W_ST = BKA * BNT;                 // halves per stage: W [32][BNT]
-    constexpr int ST = A_ST + W_ST;                 // 16 KB (BNT 128) or 14 KB (BNT 96) per stage
+    constexpr int A_ST = BM * BK;                   // halves per stage: A [128][BK]
+    constexpr int W_ST = BK * BNT;                  // halves per stage: W [BK][BNT]
+    constexpr int ST = A_ST + W_ST;
     constexpr int NJ = BNT / 32;                    // 16-column MFMA blocks per wave
-    constexpr int W_INSTR = W_ST * 2 / 1024;        // 1 KB DMA instructions per W stage: 8 or 6
+    constexpr int KS = BK / 32;                     // MFMA k-steps per stage
+    constexpr int A_CPR = BK / 8;                   // 16-byte chunks per A row
+    constexpr int A_RPI = 64 / A_CPR;               // A rows per 1 KB load instruction
+    constexpr int A_PW = BM * BK * 2 / 1024 / 4;    // A load instructions per wave per stage
+    constexpr int W_INSTR = W_ST * 2 / 1024;        // W load instructions per stage
+    constexpr int W_PW = (W_INSTR + 3) / 4;         // ... per wave, at most
     constexpr int CPR = BNT / 8;                    // 16-byte chunks per W row
+    static_assert(BK == 32 || BK == 64, "stages are 32 or 64 k deep");
+    static_assert(STAGES >= 2 && STAGES <= 4, "2 to 4 stages");
     __shared__ __attribute__((aligned(16))) _Float16 smem[STAGES * ST];
 
     int tile_m, tile_n;
@@ -458,34 +473,39 @@ void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
     const int wm = (wave & 1) * 64, wn = (wave >> 1) * (BNT / 2);
     const int lr = lane & 15, lq = lane >> 4;
 
-    // Wave w fills A slices u = 2w, 2w+1 (rows 16u .. 16u+15; lane L owns physical chunk
-    // L%4) and W instructions u = w and w + 4 (when < W_INSTR) of every stage; W
-    // instruction u covers the stage's chunks 64u .. 64u+63 in row-major order.
-    // Loads are a uniform base (the k-step's first column of A, first row of W) plus
-    // per-lane byte offsets fixed for the whole loop (the launcher keeps M*K*2 and K*N*2
-    // below 2^32), so issuing them is scalar work.
-    const int nw = (wave + 4 < W_INSTR) ? 2 : 1;   // W instructions of this wave
-    uint32_t a_off[2], w_off[2];
+    // Wave w fills A instructions u = A_PW*w .. A_PW*w + A_PW-1 (rows A_RPI*u ..; lane L
+    // owns physical chunk L % A_CPR) and W instructions u = w, w + 4, ... (< W_INSTR) of
+    // every stage; W instruction u covers the stage's chunks 64u .. 64u+63 in row-major
+    // order.  Loads are a uniform base (the k-step's first column of A, first row of W)
+    // plus per-lane byte offsets fixed for the whole loop (the launcher keeps M*K*2 and
+    // K*N*2 below 2^32), so issuing them is scalar work.
+    int nw = 0;                                     // W instructions of this wave
 #pragma unroll
-    for (int v = 0; v < 2; v++) {
-        const int u = 2 * wave + v;
-        const int ra = 16 * u + (lane >> 2), ca = (lane & 3) ^ swz_a(ra);
+    for (int v = 0; v < W_PW; v++) nw += (wave + 4 * v < W_INSTR) ? 1 : 0;
+    uint32_t a_off[A_PW], w_off[W_PW];
+#pragma unroll
+    for (int v = 0; v < A_PW; v++) {
+        const int u = A_PW * wave + v;
+        const int ra = A_RPI * u + lane / A_CPR, ca = (lane % A_CPR) ^ swz_a<BK>(ra);
         a_off[v] = ((uint32_t)(m0 + ra) * (uint32_t)K + 8u * (uint32_t)ca) * 2u;
+    }
+#pragma unroll
+    for (int v = 0; v < W_PW; v++) {
         const int q = 64 * (wave + 4 * v) + lane;  // W chunk index in the stage
         const int rw = q / CPR, cw = (q % CPR) ^ swz_w<BNT>(rw);
         w_off[v] = ((uint32_t)rw * (uint32_t)N + (uint32_t)(n0 + 8 * cw)) * 2u;
     }
-    const uint32_t wave_lds = __builtin_amdgcn_readfirstlane(lds_offset(smem) + (uint32_t)(2 * wave) * 1024u);
+    const uint32_t wave_lds = __builtin_amdgcn_readfirstlane(lds_offset(smem) + (uint32_t)(A_PW * wave) * 1024u);
     const uint32_t wave_lds_w = __builtin_amdgcn_readfirstlane(lds_offset(smem) + (uint32_t)(A_ST * 2 + wave * 1024));
     auto issue = [&](int k0, auto stage_c) {
         constexpr int stage = decltype(stage_c)::value;
         const _Float16* ab = A + k0;
         const _Float16* wb = W + (size_t)k0 * N;
 #pragma unroll
-        for (int v = 0; v < 2; v++)
+        for (int v = 0; v < A_PW; v++)
             lds_dma16_s(a_off[v], ab, wave_lds + (uint32_t)(stage * ST * 2 + v * 1024));
 #pragma unroll
-        for (int v = 0; v < 2; v++)
+        for (int v = 0; v < W_PW; v++)
             if (v < nw) lds_dma16_s(w_off[v], wb, wave_lds_w + (uint32_t)(stage * ST * 2 + 4 * v * 1024));
     };
 
@@ -495,13 +515,15 @@ void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-    // Per-lane LDS read offsets inside a stage.
-    int a_rd[4], w_rd[NJ][2];
+    // Per-lane LDS read offsets inside a stage, for its k-step s (32 k each).
+    int a_rd[KS][4], w_rd[NJ][2];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int row = wm + 16 * i + lr;
-        a_rd[i] = row * BKA + 8 * (lq ^ swz_a(row));
-    }
+    for (int s = 0; s < KS; s++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int row = wm + 16 * i + lr;
+            a_rd[s][i] = row * BK + 8 * ((4 * s + lq) ^ swz_a<BK>(row));
+        }
 #pragma unroll
     for (int j = 0; j < NJ; j++)
 #pragma unroll
@@ -511,37 +533,41 @@ void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
             w_rd[j][h] = row * BNT + 8 * ((col >> 3) ^ swz_w<BNT>(row)) + (col & 7);
         }
 
-    const int nk = K / BKA;
+    const int nk = K / BK;
     if (0 < nk) issue(0, std::integral_constant<int, 0>{});
-    if (1 < nk) issue(BKA, std::integral_constant<int, 1>{});
+    if constexpr (STAGES > 2)
+        if (1 < nk) issue(BK, std::integral_constant<int, 1>{});
     if constexpr (STAGES > 3)
-        if (2 < nk) issue(2 * BKA, std::integral_constant<int, 2>{});
-    static_assert(STAGES == 3 || STAGES == 4, "the prologue issues STAGES - 1 tiles");
+        if (2 < nk) issue(2 * BK, std::integral_constant<int, 2>{});
     // CT: accumulate C^T (operands swapped) for destinations contiguous along n.
     auto main_loop = [&](auto ct_c) {
         constexpr bool CT = decltype(ct_c)::value;
         for_each_stage<STAGES>(nk, [&](int kt, auto stage_c) {
             constexpr int stage = decltype(stage_c)::value;        // kt % STAGES
             // Tiles issued after kt that may still be in flight: min(STAGES-2, nk-1-kt),
-            // 2 + nw load instructions each.
-            if (nw == 2) wait_ahead<4, STAGES - 2>(nk - 1 - kt);
-            else wait_ahead<3, STAGES - 2>(nk - 1 - kt);
+            // A_PW + nw load instructions each.
+            if (nw == W_PW) wait_ahead<A_PW + W_PW, STAGES - 2>(nk - 1 - kt);
+            else wait_ahead<A_PW + W_PW - 1, STAGES - 2>(nk - 1 - kt);
             ring_barrier();
             if (kt + STAGES - 1 < nk)
-                issue((kt + STAGES - 1) * BKA, std::integral_constant<int, (stage + STAGES - 1) % STAGES>{});
+                issue((kt + STAGES - 1) * BK, std::integral_constant<int, (stage + STAGES - 1) % STAGES>{});
             const _Float16* As = smem + stage * ST;
             const _Float16* Ws = As + A_ST;
-            h8_t af[4], bf[NJ];
 #pragma unroll
-            for (int i = 0; i < 4; i++) af[i] = *(const h8_t*)&As[a_rd[i]];
+            for (int s = 0; s < KS; s++) {
+                h8_t af[4], bf[NJ];
 #pragma unroll
-            for (int j = 0; j < NJ; j++) bf[j] = b_frag_tr(Ws + w_rd[j][0], Ws + w_rd[j][1]);
-#pragma unroll
-            for (int i = 0; i < 4; i++)
+                for (int i = 0; i < 4; i++) af[i] = *(const h8_t*)&As[a_rd[s][i]];
 #pragma unroll
                 for (int j = 0; j < NJ; j++)
-                    acc[i][j] = CT ? __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[j], af[i], acc[i][j], 0, 0, 0)
-                                   : __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                    bf[j] = b_frag_tr(Ws + 32 * s * BNT + w_rd[j][0], Ws + 32 * s * BNT + w_rd[j][1]);
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int j = 0; j < NJ; j++)
+                        acc[i][j] = CT ? __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[j], af[i], acc[i][j], 0, 0, 0)
+                                       : __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+            }
         });
     };
     // Every DMA load was waited for in the last step, and the epilogue does not touch LDS.
@@ -642,15 +668,19 @@ void gemm_f32(cf_gemm_args_t a, Tiling t) {
 int g_gemm_stages = 0;   // tuning override of the direct-to-LDS kernel's ring depth (3, 4; 0 = automatic)
 int g_gemm_bn = 0;       // tuning override of its tile width (96, 128; 0 = automatic)
 
-template <int STAGES>
+int g_gemm_bk = 0;       // tuning override of its stage depth in k (32, 64; 0 = automatic)
+
+template <int STAGES, int BK>
 void launch_async(int bn, dim3 grid, hipStream_t s, const cf_gemm_args_t& a, const Tiling& t) {
-    if (bn == 96) hipLaunchKernelGGL((gemm_f16_async<STAGES, 96>), grid, dim3(kThreads), 0, s, a, t);
-    else hipLaunchKernelGGL((gemm_f16_async<STAGES, 128>), grid, dim3(kThreads), 0, s, a, t);
+    if (bn == 96) hipLaunchKernelGGL((gemm_f16_async<STAGES, 96, BK>), grid, dim3(kThreads), 0, s, a, t);
+    else hipLaunchKernelGGL((gemm_f16_async<STAGES, 128, BK>), grid, dim3(kThreads), 0, s, a, t);
 }
 
 }  // namespace
 
 extern "C" void cf_gemm_set_stages(int32_t stages) { g_gemm_stages = stages; }
+
+extern "C" void cf_gemm_set_bk(int32_t bk) { g_gemm_bk = bk == 32 || bk == 64 ? bk : 0; }
 
 extern "C" void cf_gemm_set_bn(int32_t bn) { g_gemm_bn = bn == 96 || bn == 128 ? bn : 0; }
 
@@ -715,10 +745,18 @@ extern "C" int cf_launch_gemm(const cf_gemm_args_t* a, void* stream) {
     dim3 grid((unsigned)blocks);
     hipStream_t st = (hipStream_t)stream;
     if (full) {
-        int stages = blocks > 2LL * cu_count() ? 3 : 4;
+        // Up to two tiles per CU: two workgroups per CU, each with 64 KB of ring, as 2
+        // stages of 64 k (whole 128-byte A lines; 10.2 vs 11.0 us on BERT-base's output
+        // projection) rather than 4 of 32.  More tiles: three workgroups per CU on
+        // 3 stages of 32 k, since 160 KB of LDS holds no third 64 KB ring.
+        const bool two_per_cu = blocks <= 2LL * cu_count();
+        int bk = two_per_cu && a->K % 64 == 0 ? 64 : 32;
+        if (g_gemm_bk == 32 || (g_gemm_bk == 64 && a->K % 64 == 0)) bk = g_gemm_bk;
+        int stages = two_per_cu ? 4 : 3;
         if (g_gemm_stages == 3 || g_gemm_stages == 4) stages = g_gemm_stages;
-        if (stages == 3) launch_async<3>(bn, grid, st, *a, t);
-        else launch_async<4>(bn, grid, st, *a, t);
+        if (bk == 64) launch_async<2, 64>(bn, grid, st, *a, t);
+        else if (stages == 3) launch_async<3, 32>(bn, grid, st, *a, t);
+        else launch_async<4, 32>(bn, grid, st, *a, t);
     } else if (a->elem == CF_ELEM_F16) {
         hipLaunchKernelGGL(gemm_f16, grid, dim3(kThreads), 0, st, *a, t);
     } else {

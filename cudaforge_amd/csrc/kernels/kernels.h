@@ -143,6 +143,9 @@ void cf_gemm_set_group_m(int32_t group_m);
 /* Tuning/test override of the fp16 direct-to-LDS GEMM's tile width (96 or 128 columns;
  * 0 = automatic: the width that balances the tiles over the CUs). */
 void cf_gemm_set_bn(int32_t bn);
+/* Tuning/test override of its stage depth in k (32: 3-4 stages of 16 KB; 64: 2 stages of
+ * 32 KB; 0 = automatic). */
+void cf_gemm_set_bk(int32_t bk);
 
 /* ---------------------------------------------------------------------------------
  * Prefill attention (flash style, online softmax): q (B, H_q, S, d), k (B, H_kv, S, d),

@@ -168,6 +168,28 @@ def test_gemm_tile_widths_agree(gpu, native, causal):
     assert np.array_equal(outs[0], outs[2])
 
 
+def test_gemm_stage_depths_agree(gpu, native):
+    """The fp16 projection GEMM's ring as 3 or 4 stages of 32 k and as 2 stages of 64 k
+    (K = 384, both QKV with its head-major and V^T scatter and WO with bias and residual):
+    within the FP16 bound of the oracle, and bit-identical to each other (every output
+    element sums the same 32-k MFMA steps in the same order)."""
+    c = FusedCase(2, 128, 6, 6, 64, seed=97, f16=True, causal=False, residual=True, bias_std=0.02)
+    want = c.oracle()
+    outs = []
+    try:
+        for bk, stages in ((32, 3), (32, 4), (64, 0), (0, 0)):
+            native.cf_gemm_set_bk(bk)
+            native.cf_gemm_set_stages(stages)
+            outs.append(run_fused_gpu(c))
+    finally:
+        native.cf_gemm_set_bk(0)
+        native.cf_gemm_set_stages(0)
+    for o in outs:
+        assert max_abs(want, o) <= TOL16
+    for o in outs[1:]:
+        assert np.array_equal(outs[0], o)
+
+
 @pytest.mark.parametrize("f16,causal", [(False, False), (True, False), (True, True)])
 def test_graph_runs_unfused_attention_as_one_fused_op(gpu, native, f16, causal):
     """An unfused self-attention block (MatMul/Add/Reshape/Transpose/Mul/[CausalMask]/
