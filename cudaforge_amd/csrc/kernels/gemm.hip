@@ -12,11 +12,13 @@
 //       k of one column per lane; it comes from W[k][n] with two ds_read_b64_tr_b16
 //       (gfx950 LDS transpose reads): in each 16-lane group, lane j addresses
 //       W[kb + j/4][nb + 4(j%4)] and lane i receives W[kb..kb+3][nb + i].
-//       Full tiles use a 3- or 4-stage ring filled by global_load_lds_dwordx4 (no VGPR
-//       staging; 3 stages, i.e. three workgroups per CU, when there are more tiles than
-//       two per CU); edge shapes use a 2-stage register-staged kernel.  The output tile
-//       goes through LDS (fp16 in one pass without a residual, fp32 in two with one) so
-//       stores are 16 bytes along the destination's contiguous direction.
+//       Full tiles use an LDS ring filled by global_load_lds_dwordx4 (no VGPR staging):
+//       3 stages of 32 k, i.e. three workgroups per CU, when there are more tiles than
+//       two per CU, else 2 stages of 64 k; it stores straight from the accumulators,
+//       16 bytes per lane after a permlane swap between neighbouring tiles.  Edge shapes
+//       use a 2-stage register-staged kernel whose output tile goes through LDS (fp16 in
+//       one pass without a residual, fp32 in two with one) so stores are 16 bytes along
+//       the destination's contiguous direction.
 // fp32: 128x128x16 tile with v_mfma_f32_16x16x4_f32, both tiles staged k-major so each
 //       operand is one conflict-free ds_read_b32 (the FP32 operator's parity path).
 // Tile edges are zero-filled on load and masked on store.
