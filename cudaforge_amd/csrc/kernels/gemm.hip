@@ -416,8 +416,9 @@ __device__ __forceinline__ void store_cn_f16(const cf_gemm_args_t& a, int seg, i
 // permuted instead: the 16-byte chunk c of row r is stored at chunk c ^ swz(r), which
 // makes the MFMA A reads (16 rows x one chunk) and the W transpose reads (4 rows x 32 B
 // per 16-lane group) hit distinct banks.
-// BNT = 128 or 96 output columns per tile (waves 2 x 2, each 64 rows x BNT/2 columns);
-// the launcher takes 96 only where 128 leaves CUs idle.
+// BNT = 128, 96 or 192 output columns per tile (waves 2 x 2, each 64 rows x BNT/2
+// columns); the launcher takes 96 only where 128 leaves CUs idle, and 192 where it
+// brings three tiles per CU down to two (fewer bytes loaded per flop on the busiest CU).
 // BK = 32 or 64 k per stage.  An A row of a stage is BK * 2 bytes of one 128-byte line:
 // at BK = 32 each load instruction reads half lines of 16 rows, and direct-to-LDS loads
 // of half lines measured ~68 GB/s per CU from L2 against ~118 GB/s for whole lines (three
@@ -432,14 +433,19 @@ constexpr int BKA = 32;
 // (row & 1, chunk) pairs, i.e. the 16 distinct 16-byte bank slots of a 256-byte row.
 template <int BK>
 __device__ __forceinline__ int swz_a(int row) { return (row >> 1) & (BK / 8 - 1); }
-// W rows are BNT * 2 bytes: 16 chunks (BNT = 128) or 12 (BNT = 96).  The 96-column
-// permutation only flips chunk bit 1, so it stays inside the row's 12 chunks; rows
-// 8 apart (read by the same half-wave) then sit 32 bytes apart in the banks.  Both
-// depend on row bits 0..3 only, so the rows of the second 32-k half of a BK = 64 stage
+// W rows are BNT * 2 bytes: 16 chunks (BNT = 128), 12 (96) or 24 (192).  The 96- and
+// 192-column permutations flip chunk bits 1-2 only, so they stay inside the row's
+// chunks.  At 96, rows 8 apart (read by the same half-wave) then sit 32 bytes apart in
+// the banks.  At 192 a row is 384 bytes, so rows of one parity start at the same bank;
+// a transpose read takes 32 bytes from each of 16 rows (8 even, 8 odd: 8r + 4h + 0..3
+// for r < 4), and ((row >> 1) ^ (row >> 3)) & 3 gives each parity's 8 rows every
+// 32-byte bank slot of its half twice, the 2-cycle minimum for 512 bytes.  All three
+// depend on row bits 0..4 only, so the rows of the second 32-k half of a BK = 64 stage
 // (row + 32) are permuted like the first.
 template <int BNT>
 __device__ __forceinline__ int swz_w(int row) {
     if constexpr (BNT == 128) return ((row & 3) << 1) ^ (((row >> 3) & 1) << 3);
+    else if constexpr (BNT == 192) return (((row >> 1) ^ (row >> 3)) & 3) << 1;
     else return ((row >> 3) & 1) << 1;
 }
 
@@ -678,13 +684,18 @@ void launch_async(int bn, dim3 grid, hipStream_t s, const cf_gemm_args_t& a, con
     else hipLaunchKernelGGL((gemm_f16_async<STAGES, 128, BK>), grid, dim3(kThreads), 0, s, a, t);
 }
 
+// 192-column tiles: 3 stages of 32 k (60 KB of LDS; two workgroups per CU).
+void launch_async_192(dim3 grid, hipStream_t s, const cf_gemm_args_t& a, const Tiling& t) {
+    hipLaunchKernelGGL((gemm_f16_async<3, 192, 32>), grid, dim3(kThreads), 0, s, a, t);
+}
+
 }  // namespace
 
 extern "C" void cf_gemm_set_stages(int32_t stages) { g_gemm_stages = stages; }
 
 extern "C" void cf_gemm_set_bk(int32_t bk) { g_gemm_bk = bk == 32 || bk == 64 ? bk : 0; }
 
-extern "C" void cf_gemm_set_bn(int32_t bn) { g_gemm_bn = bn == 96 || bn == 128 ? bn : 0; }
+extern "C" void cf_gemm_set_bn(int32_t bn) { g_gemm_bn = bn == 96 || bn == 128 || bn == 192 ? bn : 0; }
 
 int g_gemm_group_m = 0;  // tuning override of the tile-order group height (0 = kGroupM)
 
@@ -730,10 +741,12 @@ extern "C" int cf_launch_gemm(const cf_gemm_args_t* a, void* stream) {
     };
     int bn = BN;
     if (full) {
-        const bool f128 = fits(128), f96 = fits(96);
-        if (!f128 && !f96) full = false;
+        const bool f128 = fits(128), f96 = fits(96), f192 = fits(192);
+        if (!f128 && !f96 && !f192) full = false;
         else if (g_gemm_bn && fits(g_gemm_bn)) bn = g_gemm_bn;
+        else if (f128 && f192 && tiles(128) > 2LL * cu_count() && tiles(192) <= 2LL * cu_count()) bn = 192;
         else if (f96 && (!f128 || (tiles(128) < cu_count() && tiles(96) > tiles(128)))) bn = 96;
+        else if (!f128) bn = 192;
     }
     t.n_tiles_m = (int)tiles_m;
     int acc = 0;
@@ -756,7 +769,8 @@ extern "C" int cf_launch_gemm(const cf_gemm_args_t* a, void* stream) {
         if (g_gemm_bk == 32 || (g_gemm_bk == 64 && a->K % 64 == 0)) bk = g_gemm_bk;
         int stages = two_per_cu ? 4 : 3;
         if (g_gemm_stages == 3 || g_gemm_stages == 4) stages = g_gemm_stages;
-        if (bk == 64) launch_async<2, 64>(bn, grid, st, *a, t);
+        if (bn == 192) launch_async_192(grid, st, *a, t);
+        else if (bk == 64) launch_async<2, 64>(bn, grid, st, *a, t);
         else if (stages == 3) launch_async<3, 32>(bn, grid, st, *a, t);
         else launch_async<4, 32>(bn, grid, st, *a, t);
     } else if (a->elem == CF_ELEM_F16) {
