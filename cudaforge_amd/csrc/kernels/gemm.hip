@@ -449,8 +449,12 @@ __device__ __forceinline__ int swz_w(int row) {
     else return ((row >> 3) & 1) << 1;
 }
 
-template <int STAGES, int BNT, int BK>
-__global__ __launch_bounds__(kThreads, 2)
+// KSPLIT = 2: two groups of 4 waves split the k-loop of one tile, each with its own ring
+// (dynamic LDS), and the second group's accumulators are added to the first's through
+// LDS before the epilogue.  For grids of at most one tile per CU, where one 4-wave
+// workgroup per CU leaves each SIMD a single wave to hide load and LDS latency.
+template <int STAGES, int BNT, int BK, int KSPLIT = 1>
+__global__ __launch_bounds__(kThreads * KSPLIT, 2 / KSPLIT)
 void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
     constexpr int A_ST = BM * BK;                   // halves per stage: A [128][BK]
     constexpr int W_ST = BK * BNT;                  // halves per stage: W [BK][BNT]
@@ -465,7 +469,11 @@ void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
     constexpr int CPR = BNT / 8;                    // 16-byte chunks per W row
     static_assert(BK == 32 || BK == 64, "stages are 32 or 64 k deep");
     static_assert(STAGES >= 2 && STAGES <= 4, "2 to 4 stages");
-    __shared__ __attribute__((aligned(16))) _Float16 smem[STAGES * ST];
+    static_assert(KSPLIT == 1 || KSPLIT == 2, "one or two k groups");
+    __shared__ __attribute__((aligned(16))) _Float16 smem_s[KSPLIT == 1 ? STAGES * ST : 8];
+    extern __shared__ __attribute__((aligned(16))) _Float16 smem_dyn[];
+    const int kg = KSPLIT == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8));   // k group
+    _Float16* const smem = (KSPLIT == 1 ? smem_s : smem_dyn) + kg * STAGES * ST;
 
     int tile_m, tile_n;
     tile_of_block(blockIdx.x, t.n_tiles_m, t.seg_start[3], t.group_m, tile_m, tile_n);
@@ -474,10 +482,13 @@ void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
     const int K = a.K;
     const int m0 = tile_m * BM;
     const int n0 = (tile_n - t.seg_start[seg]) * BNT;
-    const _Float16* __restrict__ A = (const _Float16*)a.a;
-    const _Float16* __restrict__ W = (const _Float16*)a.w[seg];
+    // Group kg multiplies k in [kg * K / KSPLIT, (kg + 1) * K / KSPLIT) (the launcher
+    // keeps K / BK a multiple of KSPLIT, so both groups run the same steps and barriers).
+    const int k_begin = kg * (K / KSPLIT);
+    const _Float16* __restrict__ A = (const _Float16*)a.a + k_begin;
+    const _Float16* __restrict__ W = (const _Float16*)a.w[seg] + (size_t)k_begin * N;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x & (kThreads - 1), lane = tid & 63, wave = tid >> 6;
     const int wm = (wave & 1) * 64, wn = (wave >> 1) * (BNT / 2);
     const int lr = lane & 15, lq = lane >> 4;
 
@@ -541,7 +552,7 @@ void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
             w_rd[j][h] = row * BNT + 8 * ((col >> 3) ^ swz_w<BNT>(row)) + (col & 7);
         }
 
-    const int nk = K / BK;
+    const int nk = K / BK / KSPLIT;
     if (0 < nk) issue(0, std::integral_constant<int, 0>{});
     if constexpr (STAGES > 2)
         if (1 < nk) issue(BK, std::integral_constant<int, 1>{});
@@ -579,12 +590,37 @@ void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
         });
     };
     // Every DMA load was waited for in the last step, and the epilogue does not touch LDS.
+    // With two k groups, group 1 hands its accumulators to group 0 through the (then
+    // idle) rings: [wave][i][j][lane] as f4, 16 KB x NJ in all.
+    auto reduce_groups = [&]() {
+        if constexpr (KSPLIT == 2) {
+            static_assert(4 * 4 * NJ * 64 * 16 <= 2 * STAGES * ST * 2, "the rings hold the partial tile");
+            f4_t* red = (f4_t*)smem_dyn;
+            ring_barrier();                                // every wave is done with both rings
+            if (kg == 1) {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int j = 0; j < NJ; j++) red[((wave * 4 + i) * NJ + j) * 64 + lane] = acc[i][j];
+                wait_lds_reads();                          // lgkmcnt(0): the writes are done
+            }
+            ring_barrier();
+            if (kg == 0) {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int j = 0; j < NJ; j++) acc[i][j] += red[((wave * 4 + i) * NJ + j) * 64 + lane];
+            }
+        }
+    };
     if (a.out_kind == CF_GEMM_OUT_ROWMAJOR || seg < 2) {
         main_loop(std::true_type{});
-        store_ct_f16<NJ>(a, seg, m0, n0, wm, wn, lr, lq, acc);
+        reduce_groups();
+        if (kg == 0) store_ct_f16<NJ>(a, seg, m0, n0, wm, wn, lr, lq, acc);
     } else {
         main_loop(std::false_type{});
-        store_cn_f16<NJ>(a, seg, m0, n0, wm, wn, lr, lq, acc);
+        reduce_groups();
+        if (kg == 0) store_cn_f16<NJ>(a, seg, m0, n0, wm, wn, lr, lq, acc);
     }
 }
 
@@ -684,6 +720,19 @@ void launch_async(int bn, dim3 grid, hipStream_t s, const cf_gemm_args_t& a, con
     else hipLaunchKernelGGL((gemm_f16_async<STAGES, 128, BK>), grid, dim3(kThreads), 0, s, a, t);
 }
 
+// Two k groups (8 waves) per tile: 2 stages of 64 k per group, 112 KB (96 columns) or
+// 128 KB (128 columns) of dynamic LDS, one workgroup per CU.
+int g_gemm_ksplit = 0;   // tuning/test override: 1 = one k group, 2 = two where K allows, 0 = automatic
+
+template <int BNT>
+void launch_ksplit2(dim3 grid, hipStream_t s, const cf_gemm_args_t& a, const Tiling& t) {
+    constexpr unsigned lds = 2u * 2u * (128u * 64u + 64u * BNT) * 2u;
+    static const hipError_t attr = hipFuncSetAttribute((const void*)gemm_f16_async<2, BNT, 64, 2>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    (void)attr;
+    hipLaunchKernelGGL((gemm_f16_async<2, BNT, 64, 2>), grid, dim3(2 * kThreads), lds, s, a, t);
+}
+
 // 192-column tiles: 3 stages of 32 k (60 KB of LDS; two workgroups per CU).
 void launch_async_192(dim3 grid, hipStream_t s, const cf_gemm_args_t& a, const Tiling& t) {
     hipLaunchKernelGGL((gemm_f16_async<3, 192, 32>), grid, dim3(kThreads), 0, s, a, t);
@@ -694,6 +743,8 @@ void launch_async_192(dim3 grid, hipStream_t s, const cf_gemm_args_t& a, const T
 extern "C" void cf_gemm_set_stages(int32_t stages) { g_gemm_stages = stages; }
 
 extern "C" void cf_gemm_set_bk(int32_t bk) { g_gemm_bk = bk == 32 || bk == 64 ? bk : 0; }
+
+extern "C" void cf_gemm_set_ksplit(int32_t ks) { g_gemm_ksplit = ks == 1 || ks == 2 ? ks : 0; }
 
 extern "C" void cf_gemm_set_bn(int32_t bn) { g_gemm_bn = bn == 96 || bn == 128 || bn == 192 ? bn : 0; }
 
@@ -772,7 +823,13 @@ extern "C" int cf_launch_gemm(const cf_gemm_args_t* a, void* stream) {
         if (g_gemm_bk == 32 || (g_gemm_bk == 64 && a->K % 64 == 0)) bk = g_gemm_bk;
         int stages = two_per_cu ? 4 : 3;
         if (g_gemm_stages == 3 || g_gemm_stages == 4) stages = g_gemm_stages;
+        // At most one tile per CU: two k groups of 4 waves per tile (K a multiple of 128).
+        bool ks2 = blocks <= (long long)cu_count() && bn != 192 && a->K % 128 == 0;
+        if (g_gemm_ksplit == 1) ks2 = false;
+        if (g_gemm_ksplit == 2) ks2 = bn != 192 && a->K % 128 == 0;
         if (bn == 192) launch_async_192(grid, st, *a, t);
+        else if (ks2 && bn == 96) launch_ksplit2<96>(grid, st, *a, t);
+        else if (ks2) launch_ksplit2<128>(grid, st, *a, t);
         else if (bk == 64) launch_async<2, 64>(bn, grid, st, *a, t);
         else if (stages == 3) launch_async<3, 32>(bn, grid, st, *a, t);
         else launch_async<4, 32>(bn, grid, st, *a, t);

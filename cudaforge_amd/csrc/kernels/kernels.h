@@ -146,6 +146,10 @@ void cf_gemm_set_bn(int32_t bn);
 /* Tuning/test override of its stage depth in k (32: 3-4 stages of 16 KB; 64: 2 stages of
  * 32 KB; 0 = automatic). */
 void cf_gemm_set_bk(int32_t bk);
+/* Tuning/test override of its k split inside a workgroup (1: one group of 4 waves per
+ * tile; 2: two groups of 4 waves, each over half of K, where K % 128 == 0; 0 = automatic:
+ * two groups when the grid has at most one tile per CU). */
+void cf_gemm_set_ksplit(int32_t ks);
 
 /* ---------------------------------------------------------------------------------
  * Prefill attention (flash style, online softmax): q (B, H_q, S, d), k (B, H_kv, S, d),

@@ -157,11 +157,13 @@ def test_gemm_tile_widths_agree(gpu, native, causal):
     want = c.oracle()
     outs = []
     try:
+        native.cf_gemm_set_ksplit(1)   # one k group everywhere, so the sums match bit for bit
         for bn in (128, 96, 192, 0):
             native.cf_gemm_set_bn(bn)
             outs.append(run_fused_gpu(c))
     finally:
         native.cf_gemm_set_bn(0)
+        native.cf_gemm_set_ksplit(0)
     for o in outs:
         assert max_abs(want, o) <= TOL16
     for o in outs[1:]:
@@ -177,6 +179,7 @@ def test_gemm_stage_depths_agree(gpu, native):
     want = c.oracle()
     outs = []
     try:
+        native.cf_gemm_set_ksplit(1)
         for bk, stages in ((32, 3), (32, 4), (64, 0), (0, 0)):
             native.cf_gemm_set_bk(bk)
             native.cf_gemm_set_stages(stages)
@@ -184,10 +187,34 @@ def test_gemm_stage_depths_agree(gpu, native):
     finally:
         native.cf_gemm_set_bk(0)
         native.cf_gemm_set_stages(0)
+        native.cf_gemm_set_ksplit(0)
     for o in outs:
         assert max_abs(want, o) <= TOL16
     for o in outs[1:]:
         assert np.array_equal(outs[0], o)
+
+
+@pytest.mark.parametrize("bn", [128, 96])
+def test_gemm_two_k_groups(gpu, native, bn):
+    """The fp16 projection GEMM with each tile's k-loop split between two groups of 4
+    waves (K = 384 and 768; QKV with its scatter, WO with bias and residual): within the
+    FP16 bound of the oracle, and within a few fp16 ulps of the one-group kernel (the two
+    halves of K are summed separately in fp32 and then added, so roundings differ)."""
+    for case in (FusedCase(2, 128, 6, 6, 64, seed=98, f16=True, residual=True, bias_std=0.02),
+                 FusedCase(1, 256, 12, 12, 64, seed=99, f16=True, causal=True, residual=True, bias_std=0.02)):
+        want = case.oracle()
+        outs = []
+        try:
+            native.cf_gemm_set_bn(bn)
+            for ks in (1, 2):
+                native.cf_gemm_set_ksplit(ks)
+                outs.append(run_fused_gpu(case))
+        finally:
+            native.cf_gemm_set_ksplit(0)
+            native.cf_gemm_set_bn(0)
+        for o in outs:
+            assert max_abs(want, o) <= TOL16
+        assert max_abs(outs[0], outs[1]) <= 1e-2
 
 
 @pytest.mark.parametrize("f16,causal", [(False, False), (True, False), (True, True)])
