@@ -26,6 +26,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "kernels.h"
 #include "cdna4.h"
 
@@ -724,13 +726,23 @@ void launch_async(int bn, dim3 grid, hipStream_t s, const cf_gemm_args_t& a, con
 // 128 KB (128 columns) of dynamic LDS, one workgroup per CU.
 int g_gemm_ksplit = 0;   // tuning/test override: 1 = one k group, 2 = two where K allows, 0 = automatic
 
+// The dynamic-LDS limit is raised once per device (a bit per device id below 64, every
+// launch above); a failure is returned to the caller rather than left to the launch.
 template <int BNT>
-void launch_ksplit2(dim3 grid, hipStream_t s, const cf_gemm_args_t& a, const Tiling& t) {
+hipError_t launch_ksplit2(dim3 grid, hipStream_t s, const cf_gemm_args_t& a, const Tiling& t) {
     constexpr unsigned lds = 2u * 2u * (128u * 64u + 64u * BNT) * 2u;
-    static const hipError_t attr = hipFuncSetAttribute((const void*)gemm_f16_async<2, BNT, 64, 2>,
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    (void)attr;
+    static std::atomic<uint64_t> raised{0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev >= 64 || !((raised.load(std::memory_order_acquire) >> dev) & 1u)) {
+        e = hipFuncSetAttribute((const void*)gemm_f16_async<2, BNT, 64, 2>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        if (dev < 64) raised.fetch_or(1ull << dev, std::memory_order_release);
+    }
     hipLaunchKernelGGL((gemm_f16_async<2, BNT, 64, 2>), grid, dim3(2 * kThreads), lds, s, a, t);
+    return hipSuccess;
 }
 
 // 192-column tiles: 3 stages of 32 k (60 KB of LDS; two workgroups per CU).
@@ -827,12 +839,14 @@ extern "C" int cf_launch_gemm(const cf_gemm_args_t* a, void* stream) {
         bool ks2 = blocks <= (long long)cu_count() && bn != 192 && a->K % 128 == 0;
         if (g_gemm_ksplit == 1) ks2 = false;
         if (g_gemm_ksplit == 2) ks2 = bn != 192 && a->K % 128 == 0;
+        hipError_t e = hipSuccess;
         if (bn == 192) launch_async_192(grid, st, *a, t);
-        else if (ks2 && bn == 96) launch_ksplit2<96>(grid, st, *a, t);
-        else if (ks2) launch_ksplit2<128>(grid, st, *a, t);
+        else if (ks2 && bn == 96) e = launch_ksplit2<96>(grid, st, *a, t);
+        else if (ks2) e = launch_ksplit2<128>(grid, st, *a, t);
         else if (bk == 64) launch_async<2, 64>(bn, grid, st, *a, t);
         else if (stages == 3) launch_async<3, 32>(bn, grid, st, *a, t);
         else launch_async<4, 32>(bn, grid, st, *a, t);
+        if (e != hipSuccess) return (int)e;
     } else if (a->elem == CF_ELEM_F16) {
         hipLaunchKernelGGL(gemm_f16, grid, dim3(kThreads), 0, st, *a, t);
     } else {
