@@ -433,10 +433,12 @@ void flash_f16_dma64(cf_flash_args_t a) {
                         if (key >= S || (a.causal && key > query[j])) sc[j][t][i] = -INFINITY;
                     }
             }
-            float mloc = fmaxf(fmaxf(sc[j][0][0], sc[j][0][1]), fmaxf(sc[j][0][2], sc[j][0][3]));
+            // A chain of three-input maxima (v_max3_f32): 8 instructions for the 16 scores.
+            float mloc = fmaxf(fmaxf(sc[j][0][0], sc[j][0][1]), sc[j][0][2]);
 #pragma unroll
-            for (int t = 1; t < 4; t++)
-                mloc = fmaxf(mloc, fmaxf(fmaxf(sc[j][t][0], sc[j][t][1]), fmaxf(sc[j][t][2], sc[j][t][3])));
+            for (int e = 3; e < 15; e += 2)
+                mloc = fmaxf(fmaxf(mloc, sc[j][e >> 2][e & 3]), sc[j][(e + 1) >> 2][(e + 1) & 3]);
+            mloc = fmaxf(mloc, sc[j][3][3]);
             mloc = max_xor32(max_xor16(mloc)) * c;     // -inf if the whole row is masked
             if (__builtin_amdgcn_ballot_w64(mloc > m_run[j] + kLazy)) {
                 const float m_new = mloc > m_run[j] + kLazy ? mloc : m_run[j];
