@@ -22,6 +22,7 @@ from .api import (  # noqa: F401
     Stream,
     Event,
     TensorT,
+    call_entry,
     call_op,
     device_caps,
     find_op,
@@ -49,6 +50,7 @@ __all__ = [
     "Stream",
     "Event",
     "TensorT",
+    "call_entry",
     "call_op",
     "device_caps",
     "graph_detect_mha",

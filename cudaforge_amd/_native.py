@@ -112,6 +112,7 @@ def _proto(lib):
         "cf_gemm_set_ksplit": (None, [c_int32]),
         "cf_flash_set_mode": (None, [c_int32]),
         "mha_decode_plan": (c_int, [c_void_p, c_int, POINTER(c_int64), POINTER(c_int64)]),
+        "cf_decode_attn_scratch_bytes": (c_size_t, []),
         # host platform / tensors
         "platform_init": (c_int, []),
         "platform_finalize": (None, []),
@@ -157,7 +158,7 @@ def _proto(lib):
     for name in ("mha_decode_f32_cuda", "mha_decode_f16_cuda", "mha_decode_attn_f32_cuda",
                  "mha_decode_attn_f16_cuda", "mha_fused_f32_cuda", "mha_fused_f16_cuda",
                  "causal_mask_f32_cuda", "rope_f32_cuda", "rope_f16_cuda", "mha_decode_rope_f32_cuda",
-                 "mha_decode_rope_f16_cuda"):
+                 "mha_decode_rope_f16_cuda", "mha_decode_attn_f16_noalloc"):
         fn = getattr(lib, name)
         fn.restype = c_int
         fn.argtypes = [POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_void_p]

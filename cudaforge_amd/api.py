@@ -334,3 +334,15 @@ def call_op(name: str, inputs, outputs, params, stream: Stream | None = None, ex
     st = stream.stream_t() if stream is not None else None
     return entry.func(ctypes.cast(in_arr, POINTER(c_void_p)), ctypes.cast(out_arr, POINTER(c_void_p)),
                       ctypes.cast(ctypes.pointer(params), c_void_p) if params is not None else None, st)
+
+
+def call_entry(name: str, inputs, outputs, params, stream: Stream | None = None) -> int:
+    """Call an exported operator-signature C function by its symbol name (for entry
+    points that are not in the registry, such as mha_decode_attn_f16_noalloc)."""
+    lib = load_library()
+    fn = getattr(lib, name)
+    in_arr = (c_void_p * max(len(inputs), 1))(*[_ptr(x) for x in inputs])
+    out_arr = (c_void_p * max(len(outputs), 1))(*[_ptr(x) for x in outputs])
+    st = stream.stream_t() if stream is not None else None
+    return fn(ctypes.cast(in_arr, POINTER(c_void_p)), ctypes.cast(out_arr, POINTER(c_void_p)),
+              ctypes.cast(ctypes.pointer(params), c_void_p) if params is not None else None, st)

@@ -907,3 +907,41 @@ extern "C" int cf_launch_decode_attn(const cf_decode_attn_args_t* a, void* strea
     if (rc != 0) return rc;
     return cf_launch_decode_attn_merge(a, stream);
 }
+
+// ------------------------------------------------------------ fixed scratch ---
+// Split partials for callers that cannot allocate (mha_decode_attn_f16_noalloc): a
+// file-scope device array, one copy per GPU, held until the process ends.  Host code
+// never passes `scratch` itself to a kernel (on the host the name is only a stand-in for
+// the symbol): it looks up each device's address once, with that device current, and
+// uses that pointer.
+namespace {
+constexpr size_t kScratchBytes = (size_t)16 << 20;
+constexpr int kScratchDevices = 64;
+__device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+float* g_scratch_ptr[kScratchDevices];
+}  // namespace
+
+extern "C" size_t cf_decode_attn_scratch_bytes(void) { return kScratchBytes; }
+
+extern "C" int cf_decode_attn_scratch_init(void) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= kScratchDevices) return (int)hipErrorInvalidDevice;
+    if (g_scratch_ptr[dev]) return 0;
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+        (void)hipGetLastError();
+        return e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol;
+    }
+    g_scratch_ptr[dev] = (float*)p;
+    return 0;
+}
+
+extern "C" float* cf_decode_attn_scratch(void) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices) return nullptr;
+    if (!g_scratch_ptr[dev] && cf_decode_attn_scratch_init() != 0) return nullptr;
+    return g_scratch_ptr[dev];
+}

@@ -61,6 +61,14 @@ void    cf_decode_attn_set_merge_rows(int32_t on);
 /* Workspace floats needed for the partials of a launch. */
 size_t  cf_decode_attn_partials_floats(int32_t B, int32_t H_q, int32_t H_kv, int32_t d,
                                        int32_t n_split, int32_t elem);
+/* Fixed device scratch for the split partials of the allocation-free decode entry: a
+ * file-scope device array of cf_decode_attn_scratch_bytes() bytes, one per GPU.
+ * cf_decode_attn_scratch_init looks up the current device's address of it once
+ * (0 or a hipError_t value); cf_decode_attn_scratch returns that address, looking it up
+ * on first use on a device, or NULL on failure. */
+size_t  cf_decode_attn_scratch_bytes(void);
+int     cf_decode_attn_scratch_init(void);
+float*  cf_decode_attn_scratch(void);
 int     cf_launch_decode_attn_split(const cf_decode_attn_args_t* a, void* stream);
 int     cf_launch_decode_attn_merge(const cf_decode_attn_args_t* a, void* stream);
 int     cf_launch_decode_attn(const cf_decode_attn_args_t* a, void* stream);  /* split + merge */

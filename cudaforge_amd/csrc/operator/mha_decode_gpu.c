@@ -17,6 +17,7 @@
 #include "op_common.h"
 #include "../kernels/kernels.h"
 
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -117,8 +118,12 @@ static size_t attn_args(int elem, const decode_shape_t* s, const int32_t* lens,
     return cf_decode_attn_partials_floats(a->B, a->H_q, a->H_kv, a->d, a->n_split, elem) * sizeof(float);
 }
 
+/* Fill the core's launch arguments.  Partials come from the stream's workspace, or,
+ * when `fixed` is non-NULL, from that buffer of `fixed_bytes` bytes (no allocation);
+ * a plan whose partials exceed it is rejected with -1. */
 static int attn_prepare(int elem, const void* inputs[], void* outputs[],
-                        const operator_params_t* params, void* stream, cf_decode_attn_args_t* a) {
+                        const operator_params_t* params, void* stream, cf_decode_attn_args_t* a,
+                        float* fixed, size_t fixed_bytes) {
     if (!params || !inputs || !outputs) return -1;
     const mha_decode_params_t* p = (const mha_decode_params_t*)params;
     decode_shape_t s;
@@ -131,9 +136,20 @@ static int attn_prepare(int elem, const void* inputs[], void* outputs[],
         if (!lens) return -1;
     }
     const size_t part_bytes = attn_args(elem, &s, lens, a);
-    char* ws = (char*)gpu_workspace_get_stream(stream, part_bytes);
-    if (!ws) return -1;
-    a->partials = (float*)ws;
+    if (fixed) {
+        if (part_bytes > fixed_bytes) {
+            fprintf(stderr,
+                    "mha_decode_attn_f16_noalloc: split partials need %zu bytes, more than the %zu-byte fixed "
+                    "scratch (B=%lld H_q=%lld d=%lld n_split=%d); use mha_decode_attn_f16_cuda\n",
+                    part_bytes, fixed_bytes, (long long)s.B, (long long)s.H, (long long)s.d, a->n_split);
+            return -1;
+        }
+        a->partials = fixed;
+    } else {
+        char* ws = (char*)gpu_workspace_get_stream(stream, part_bytes);
+        if (!ws) return -1;
+        a->partials = (float*)ws;
+    }
     a->q = inputs[0];
     a->k = inputs[1];
     a->v = inputs[2];
@@ -153,7 +169,7 @@ int mha_decode_attn_kernel_times(const void* const* input_sets, int n_inputs, in
     cf_decode_attn_args_t a[16];
     for (int s = 0; s < n_sets; s++) {
         const int rc = attn_prepare(elem, (const void**)&input_sets[s * n_inputs], outputs, params,
-                                    cf_stream_of(stream), &a[s]);
+                                    cf_stream_of(stream), &a[s], NULL, 0);
         if (rc != 0) return rc;
     }
     void* st = cf_stream_of(stream);
@@ -183,7 +199,21 @@ int mha_decode_attn_kernel_times(const void* const* input_sets, int n_inputs, in
 static int attn_core(int elem, const void* inputs[], void* outputs[],
                      const operator_params_t* params, stream_t* stream) {
     cf_decode_attn_args_t a;
-    const int rc = attn_prepare(elem, inputs, outputs, params, cf_stream_of(stream), &a);
+    const int rc = attn_prepare(elem, inputs, outputs, params, cf_stream_of(stream), &a, NULL, 0);
+    if (rc != 0) return rc;
+    return cf_launch_decode_attn(&a, cf_stream_of(stream));
+}
+
+/* mha_decode_attn_f16_cuda with its split partials in the library's fixed per-GPU
+ * scratch instead of the stream workspace: no allocation of any kind.  Same plan, same
+ * kernels, so the same bits.  Calls that overlap on one GPU share the scratch and race. */
+int mha_decode_attn_f16_noalloc(const void* inputs[], void* outputs[],
+                                const operator_params_t* params, stream_t* stream) {
+    float* fixed = cf_decode_attn_scratch();
+    if (!fixed) return -1;
+    cf_decode_attn_args_t a;
+    const int rc = attn_prepare(CF_ELEM_F16, inputs, outputs, params, cf_stream_of(stream), &a, fixed,
+                                cf_decode_attn_scratch_bytes());
     if (rc != 0) return rc;
     return cf_launch_decode_attn(&a, cf_stream_of(stream));
 }

@@ -10,6 +10,7 @@
 #include <string.h>
 
 #include "gpu_ops.h"
+#include "kernels.h"
 
 namespace {
 
@@ -317,8 +318,10 @@ static void gpu_finalize_impl(void) {
 }
 
 int gpu_platform_init(int device_id) {
-    const int e = gpu_init(device_id);
+    int e = gpu_init(device_id);
     if (e != 0) return e;
+    // The allocation-free decode entry's fixed scratch: its address on this device.
+    if ((e = cf_decode_attn_scratch_init()) != 0) return e;
     g_gpu.init = gpu_init;
     g_gpu.finalize = gpu_finalize_impl;
     g_gpu.device_alloc = gpu_device_alloc;

@@ -43,6 +43,17 @@ int mha_decode_attn_f32_cuda(const void* inputs[], void* outputs[],
 int mha_decode_attn_f16_cuda(const void* inputs[], void* outputs[],
                              const operator_params_t* params, stream_t* stream);
 
+/* Allocation-free variant of mha_decode_attn_f16_cuda.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments, plan, kernels
+ * and result bits; the split partials live in a fixed 16 MiB device array per GPU
+ * (cf. cf_decode_attn_scratch_bytes) instead of the stream workspace, and no call
+ * allocates or frees anything.  A plan whose partials exceed that array returns -1 with
+ * a message on stderr.  Every call on one GPU shares the array, so calls that overlap
+ * on one GPU (different streams, or threads) race; order them on one stream. */
+int mha_decode_attn_f16_noalloc(const void* inputs[], void* outputs[],
+                                const operator_params_t* params, stream_t* stream);
+
 /* MHA_Fused, FP32 I/O.  Replaces mha_fused_f32_cuda (src/operator/nn/mha_fused_cuda.cu:938-1189).
  * inputs  [X(B,S,D), R(B,S,D) or NULL, WQ(D,D), bQ, WK(D,H_kv*d), bK, WV(D,H_kv*d), bV, WO(D,D), bO]
  * outputs [Y(B,S,D)]; honours causal and num_kv_heads (the reference CPU op ignores both). */
