@@ -5,25 +5,33 @@
  *
  * Pattern, from the tensor X that exactly three MatMuls read:
  *   each MatMul -> optional bias Add -> Reshape -> Transpose      (Q, K and V chains)
- *   MatMul(Q, K) -> Mul(scale) -> optional CausalMask -> Softmax -> MatMul(probs, V)
+ *   MatMul(Q, K) -> Mul(scale) -> optional Add(mask) -> Softmax -> MatMul(probs, V)
  *   -> Transpose -> Reshape -> MatMul(W_O) -> optional bias Add -> optional residual Add
+ * where the mask Add's second input is the (S, S) output of a CausalMask node.
  * Q is the chain whose output is the first operand of a MatMul, K the chain that is its
  * second operand, V the third (graph.c:431-467).  B, S, D come from X's shape, H and d
  * from Q's transposed shape (B, H, S, d) (graph.c:564-576).
  *
  * Where this differs from the reference, it is stricter or more general, never looser:
- *   - the scale is the Mul's scalar operand when it has one (the reference assumed
- *     1/sqrt(d) whatever the graph multiplied by), else 1/sqrt(d);
- *   - a bias Add is recognised by its operand (a weight, or an input of one projection
- *     row's width) and a residual Add by a (B, S, D) second input, so a missing bias Add
- *     cannot swallow the residual (graph.c:512-540 took the first Add as the bias);
- *   - H_kv is read from K's transposed shape (GQA, H % H_kv == 0), and a CausalMask
- *     between Mul and Softmax gives causal = 1;
+ *   - the scale is the Mul's scalar operand (the reference assumed 1/sqrt(d) whatever
+ *     the graph multiplied by): the scores must be the Mul's first input and its other
+ *     operand a 1-element weight, or a 1-element tensor no node produces, so its host
+ *     value is the one the graph computes with; anything else is not fused;
+ *   - projection weights, their biases and b_O are node weights only; an Add whose second
+ *     operand is a graph tensor is taken as the residual when it is (B, S, D), so a
+ *     missing bias Add cannot swallow the residual (graph.c:512-540 took the first Add as
+ *     the bias) and no graph input is uploaded once as if it were a weight;
+ *   - H_kv is read from K's transposed shape (GQA, H % H_kv == 0);
+ *   - causal = 1 when the scaled scores go through Add(scores, mask) with `mask` the
+ *     output of a CausalMask node of seq_len S (its 0 / -inf pattern is exactly the
+ *     fused op's causal rule, causal_mask.c:17-21); the CausalMask node is part of the
+ *     match when the Add is its only reader, else it still runs;
  *   - weights must be present with the sizes the fused operator reads, and every tensor
  *     must share one dtype (F32 or F16), else the subgraph is left unfused;
  *   - every non-overlapping match is found, not just the first.
  */
 #include "graph.h"
+#include "causal_mask_int.h"
 
 #include <math.h>
 #include <stdint.h>
@@ -77,11 +85,19 @@ static int is(const inference_graph_t* g, int nid, op_type_t type) {
     return nid >= 0 && g->nodes[nid].type == type;
 }
 
-/* Second operand of a binary node: its first weight, else its second input tensor. */
-static tensor_t* operand(const inference_graph_t* g, const graph_node_t* n) {
-    if (n->num_weights >= 1 && n->weights && n->weights[0]) return n->weights[0];
-    if (n->num_inputs >= 2) return tensor_of(g, n->input_tensors[1]);
-    return NULL;
+/* The node's first weight (a MatMul's W, an Add's bias, a Mul's scale), or NULL. */
+static tensor_t* weight_of(const graph_node_t* n) {
+    return (n->num_weights >= 1 && n->weights) ? n->weights[0] : NULL;
+}
+
+/* Node that writes tensor tid, or -1. */
+static int producer_of(const inference_graph_t* g, int tid) {
+    for (int i = 0; i < g->num_nodes; i++) {
+        const graph_node_t* n = &g->nodes[i];
+        for (int j = 0; j < n->num_outputs; j++)
+            if (n->output_tensors[j] == tid) return i;
+    }
+    return -1;
 }
 
 /* MatMul -> (bias Add) -> Reshape -> Transpose from MatMul `mm` (graph.c:391-429).
@@ -90,13 +106,13 @@ static tensor_t* operand(const inference_graph_t* g, const graph_node_t* n) {
 static int proj_chain(const inference_graph_t* g, const unsigned char* used, int mm, node_list_t* l,
                       tensor_t** w, tensor_t** b) {
     const graph_node_t* n = &g->nodes[mm];
-    *w = operand(g, n);
+    *w = weight_of(n);
     *b = NULL;
     take(l, mm);
     int cur = out0(g, mm);
     int nx = sole_reader(g, cur, used);
     if (is(g, nx, OP_ADD) && g->nodes[nx].num_inputs >= 1 && g->nodes[nx].input_tensors[0] == cur) {
-        tensor_t* bias = operand(g, &g->nodes[nx]);
+        tensor_t* bias = weight_of(&g->nodes[nx]);
         const tensor_t* y = tensor_of(g, cur);
         if (!bias || !y || y->ndim < 1 || bias->numel != y->shape[y->ndim - 1]) return -1;
         *b = bias;
@@ -164,15 +180,24 @@ static int match_at(const inference_graph_t* g, const unsigned char* used, int x
 
     int cur = out0(g, attn);
     int nx = sole_reader(g, cur, used);
-    if (!is(g, nx, OP_MUL)) return 0;
-    const tensor_t* scale_t = operand(g, &g->nodes[nx]);
+    if (!is(g, nx, OP_MUL) || g->nodes[nx].num_inputs < 1 || g->nodes[nx].input_tensors[0] != cur) return 0;
+    /* The scale: a 1-element weight, or a 1-element second input that no node produces. */
+    const tensor_t* scale_t = weight_of(&g->nodes[nx]);
+    if (!scale_t && g->nodes[nx].num_inputs >= 2 && producer_of(g, g->nodes[nx].input_tensors[1]) < 0)
+        scale_t = tensor_of(g, g->nodes[nx].input_tensors[1]);
+    if (!scale_t || scale_t->numel != 1 || !scale_t->data) return 0;
     take(&l, nx);
     cur = out0(g, nx);
     nx = sole_reader(g, cur, used);
-    int causal = 0;
-    if (is(g, nx, OP_CAUSAL_MASK)) {
-        causal = 1;
+    /* Causal: Add(scores, mask) with mask the output of a CausalMask node (its seq_len is
+     * checked against S below). */
+    int mask_node = -1;
+    if (is(g, nx, OP_ADD) && g->nodes[nx].num_weights == 0 && g->nodes[nx].num_inputs == 2 &&
+        g->nodes[nx].input_tensors[0] == cur) {
+        mask_node = producer_of(g, g->nodes[nx].input_tensors[1]);
+        if (!is(g, mask_node, OP_CAUSAL_MASK) || used[mask_node]) return 0;
         take(&l, nx);
+        if (sole_reader(g, g->nodes[nx].input_tensors[1], used) == nx) take(&l, mask_node);
         cur = out0(g, nx);
         nx = sole_reader(g, cur, used);
     }
@@ -195,7 +220,7 @@ static int match_at(const inference_graph_t* g, const unsigned char* used, int x
     cur = out0(g, nx);
     nx = sole_reader(g, cur, used);
     if (!is(g, nx, OP_MATMUL)) return 0;
-    tensor_t* wo = operand(g, &g->nodes[nx]);
+    tensor_t* wo = weight_of(&g->nodes[nx]);
     take(&l, nx);
     cur = out0(g, nx);
 
@@ -208,13 +233,20 @@ static int match_at(const inference_graph_t* g, const unsigned char* used, int x
     const int64_t B = x->shape[0], S = x->shape[1], D = x->shape[2];
     const int64_t H = qt->shape[1], d = qt->shape[3], H_kv = kt->shape[1];
     if (B <= 0 || S <= 0 || D <= 0 || H <= 0 || d <= 0 || H_kv <= 0 || H % H_kv != 0 || H * d != D) return 0;
+    if (mask_node >= 0) {
+        const graph_node_t* mn = &g->nodes[mask_node];
+        const tensor_t* mt = tensor_of(g, out0(g, mask_node));
+        if (!mn->params || mn->params_size < sizeof(causal_mask_params_t) ||
+            ((const causal_mask_params_t*)mn->params)->seq_len != S || !mt || mt->numel != S * S)
+            return 0;
+    }
 
     /* Optional bias Add, then optional residual Add (graph.c:512-540). */
     tensor_t* bo = NULL;
     int residual = -1;
     nx = sole_reader(g, cur, used);
     if (is(g, nx, OP_ADD) && g->nodes[nx].num_inputs >= 1 && g->nodes[nx].input_tensors[0] == cur) {
-        tensor_t* op = operand(g, &g->nodes[nx]);
+        tensor_t* op = weight_of(&g->nodes[nx]);
         if (op && op->numel == D) {
             bo = op;
             take(&l, nx);
@@ -266,9 +298,9 @@ static int match_at(const inference_graph_t* g, const unsigned char* used, int x
     p->num_heads = H;
     p->num_kv_heads = H_kv;
     p->head_dim = d;
-    p->scale = (scale_t && scale_t->numel == 1 && scale_t->data) ? scalar_value(scale_t) : 1.0f / sqrtf((float)d);
+    p->scale = scalar_value(scale_t);
     p->has_residual = residual >= 0;
-    p->causal = causal != 0;
+    p->causal = mask_node >= 0;
     return 1;
 }
 

@@ -239,15 +239,24 @@ OP_MATMUL, OP_ADD, OP_RESHAPE, OP_SOFTMAX, OP_MUL, OP_TRANSPOSE = 3, 8, 9, 11, 1
 
 
 def build_attention_subgraph(g: Graph, c: FusedCase, x_id, r_id=None, *, bias=True, causal=False,
-                             scale=None, softmax_op=None, extra_scores_reader=False, wdtype=None):
+                             scale=None, softmax_op=None, extra_scores_reader=False, wdtype=None,
+                             mask_style="add", mask_seq=None, scale_style="weight", bias_style="weight"):
     """Appends the unfused self-attention block the reference's fusion pass recognises
     (graph.c:347-358, the ONNX BERT export's node pattern) reading tensor x_id:
       X -> 3 x [MatMul -> Add(bias) -> Reshape -> Transpose] -> Q, K, V;
-      MatMul(Q, K^T) -> Mul(scale) [-> CausalMask] -> Softmax -> MatMul(., V)
+      MatMul(Q, K^T) -> Mul(scale) [-> Add(CausalMask output)] -> Softmax -> MatMul(., V)
       -> Transpose -> Reshape -> MatMul(W_O) -> Add(b_O) [-> Add(residual r_id)].
     Intermediate tensors get their real shapes (never computed: the pattern runs fused).
     Bias Adds take the bias as their second input and as their weight, as the
-    reference's Add nodes do.  Returns {name: id} for the nodes and tensors."""
+    reference's Add nodes do.  Variants for the matcher's tests:
+      mask_style "add" (CausalMask output added to the scores), "add_shared" (the mask is
+        also read by another node), "passthrough" (CausalMask reading the scores, a
+        pattern whose op-by-op meaning is not masked attention); mask_seq overrides the
+        CausalMask node's seq_len;
+      scale_style "weight", "constant" (second input, no producer), "produced" (second
+        input written by a node), "swapped" (scores as the Mul's second input);
+      bias_style "weight", or "input" (bias Adds read the bias as a graph tensor only).
+    Returns {name: id} for the nodes and tensors."""
     B, S, D, H, H_kv, d = c.B, c.S, c.D, c.H, c.H_kv, c.d
     dt = DT_F16 if c.f16 else DT_F32
     npdt = np.float16 if c.f16 else np.float32
@@ -270,7 +279,7 @@ def build_attention_subgraph(g: Graph, c: FusedCase, x_id, r_id=None, *, bias=Tr
         if bias:
             b_t, b_id = g.tensor(wconv(bvec), wdt)
             _, add_out = t((B, S, width))
-            ids["add_" + name] = g.node(OP_ADD, [cur, b_id], [add_out], [b_t])
+            ids["add_" + name] = g.node(OP_ADD, [cur, b_id], [add_out], [b_t] if bias_style == "weight" else [])
             cur = add_out
         _, rs = t((B, S, heads, d))
         ids["rs_" + name] = g.node(OP_RESHAPE, [cur], [rs])
@@ -282,13 +291,35 @@ def build_attention_subgraph(g: Graph, c: FusedCase, x_id, r_id=None, *, bias=Tr
     if extra_scores_reader:
         _, spare = t((B, H, S, S))
         ids["spare"] = g.node(OP_RELU, [scores], [spare])
-    s_t, _ = g.tensor(np.full((1,), 1.0 / np.sqrt(d) if scale is None else scale, np.float32))
+    s_t, s_id = g.tensor(np.full((1,), 1.0 / np.sqrt(d) if scale is None else scale, np.float32))
     _, scaled = t((B, H, S, S))
-    ids["mul"] = g.node(OP_MUL, [scores], [scaled], [s_t])
+    if scale_style == "weight":
+        ids["mul"] = g.node(OP_MUL, [scores], [scaled], [s_t])
+    elif scale_style == "constant":
+        ids["mul"] = g.node(OP_MUL, [scores, s_id], [scaled])
+    elif scale_style == "swapped":
+        ids["mul"] = g.node(OP_MUL, [s_id, scores], [scaled])
+    else:
+        _, s_src = g.tensor(np.ones((1,), np.float32))
+        ids["scale_src"] = g.node(OP_RELU, [s_src], [s_id])
+        ids["mul"] = g.node(OP_MUL, [scores, s_id], [scaled])
     cur = scaled
     if causal:
+        import cudaforge_amd as cf
         _, masked = t((B, H, S, S))
-        ids["mask"] = g.node(OP_CAUSAL_MASK, [cur], [masked])
+        if mask_style == "passthrough":
+            ids["mask"] = g.node(OP_CAUSAL_MASK, [cur], [masked], params=cf.CausalMaskParams(S))
+        else:
+            # The causal pattern as graphs hold it: CausalMask writes an (S, S) 0 / -inf
+            # mask (its input is a placeholder, causal_mask.c:5-8) that an Add puts on
+            # the scaled scores.
+            _, mask = g.tensor(np.zeros((S, S), np.float32), DT_F32)
+            ms = S if mask_seq is None else mask_seq
+            ids["mask"] = g.node(OP_CAUSAL_MASK, [x_id], [mask], params=cf.CausalMaskParams(ms))
+            ids["add_mask"] = g.node(OP_ADD, [cur, mask], [masked])
+            if mask_style == "add_shared":
+                _, mask2 = g.tensor(np.zeros((S, S), np.float32), DT_F32)
+                ids["mask_reader"] = g.node(OP_RELU, [mask], [mask2])
         cur = masked
     _, probs = t((B, H, S, S))
     ids["softmax"] = g.node(OP_SOFTMAX if softmax_op is None else softmax_op, [cur], [probs])
@@ -305,7 +336,7 @@ def build_attention_subgraph(g: Graph, c: FusedCase, x_id, r_id=None, *, bias=Tr
     if bias:
         bo_t, bo_id = g.tensor(wconv(c.bO), wdt)
         _, projb = t((B, S, D))
-        ids["add_o"] = g.node(OP_ADD, [cur, bo_id], [projb], [bo_t])
+        ids["add_o"] = g.node(OP_ADD, [cur, bo_id], [projb], [bo_t] if bias_style == "weight" else [])
         cur = projb
     if r_id is not None:
         _, out = t((B, S, D))

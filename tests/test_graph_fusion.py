@@ -56,7 +56,8 @@ def test_causal_gqa_and_scale_are_read_from_the_graph(native):
         assert p.causal and not p.has_residual and p.num_kv_heads == 2 and abs(p.scale - 0.2) < 1e-7
         assert m.residual_tid == -1 and m.out_node == ids["mm_o"]
         assert not any(m.weights[i] for i in (1, 3, 5, 7))       # no bias Adds
-        assert m.num_nodes == 3 * 3 + 8
+        assert m.num_nodes == 3 * 3 + 9                          # + CausalMask and its Add
+        assert ids["mask"] in m.nodes[:m.num_nodes] and ids["add_mask"] in m.nodes[:m.num_nodes]
     finally:
         g.destroy()
 
@@ -92,5 +93,89 @@ def test_broken_patterns_are_left_alone(native, breakage):
             assert len(ms) == 1 and not ms[0].params.causal
         else:
             assert ms == []
+    finally:
+        g.destroy()
+
+
+def test_old_passthrough_mask_pattern_is_not_fused(native):
+    """Mul -> CausalMask(scores) -> Softmax computes softmax(mask) op by op (CausalMask
+    ignores its input, causal_mask.c:5-8), so running it as masked attention would change
+    the result: it must stay unfused."""
+    import cudaforge_amd as cf
+    c = FusedCase(1, 12, 4, 2, 8, seed=4, residual=False)
+    g, _, _, _ = _graph(native, c, residual=False, causal=True, mask_style="passthrough")
+    try:
+        assert cf.graph_detect_mha(g.g) == []
+    finally:
+        g.destroy()
+
+
+def test_mask_of_another_length_is_not_fused(native):
+    import cudaforge_amd as cf
+    c = FusedCase(1, 12, 4, 2, 8, seed=4, residual=False)
+    g, _, _, _ = _graph(native, c, residual=False, causal=True, mask_seq=11)
+    try:
+        assert cf.graph_detect_mha(g.g) == []
+    finally:
+        g.destroy()
+
+
+def test_shared_mask_node_still_runs(native):
+    """A mask that another node also reads is not swallowed by the match."""
+    import cudaforge_amd as cf
+    c = FusedCase(1, 12, 4, 2, 8, seed=4, residual=False)
+    g, ids, _, _ = _graph(native, c, residual=False, causal=True, mask_style="add_shared")
+    try:
+        (m,) = cf.graph_detect_mha(g.g)
+        nodes = set(m.nodes[:m.num_nodes])
+        assert m.params.causal and ids["add_mask"] in nodes and ids["mask"] not in nodes
+    finally:
+        g.destroy()
+
+
+@pytest.mark.parametrize("style,fused", [("constant", True), ("produced", False), ("swapped", False)])
+def test_scale_operand_rules(native, style, fused):
+    """The scale is read on the host, so only a weight or a tensor no node writes counts,
+    and the scores must be the Mul's first input."""
+    import cudaforge_amd as cf
+    c = FusedCase(1, 8, 2, 2, 8, seed=6, residual=True)
+    g, _, _, _ = _graph(native, c, scale=0.3, scale_style=style)
+    try:
+        ms = cf.graph_detect_mha(g.g)
+        if fused:
+            assert len(ms) == 1 and abs(ms[0].params.scale - 0.3) < 1e-7
+        else:
+            assert ms == []
+    finally:
+        g.destroy()
+
+
+def test_bias_from_a_graph_tensor_is_not_a_weight(native):
+    """Bias Adds whose bias is only a graph tensor (no node weight) are not fused: the
+    fused op uploads its weights once."""
+    import cudaforge_amd as cf
+    c = FusedCase(1, 8, 2, 2, 8, seed=6, residual=True)
+    g, _, _, _ = _graph(native, c, bias_style="input")
+    try:
+        assert cf.graph_detect_mha(g.g) == []
+    finally:
+        g.destroy()
+
+
+def test_single_token_residual_without_output_bias(native):
+    """B*S == 1: the residual Add has D elements, like b_O; with no bias Add on W_O it is
+    still the residual, because b_O only comes from a node weight."""
+    import cudaforge_amd as cf
+    c = FusedCase(1, 1, 2, 2, 8, seed=8, residual=True)
+    g = Graph(native)
+    try:
+        _, iX = g.tensor(np.asarray(c.X, np.float32))
+        _, iR = g.tensor(np.asarray(c.R, np.float32))
+        ids = build_attention_subgraph(g, c, iX, iR, bias=False)
+        native.graph_set_output(g.g, g.node(OP_OUTPUT, [ids["out"]], []))
+        assert native.graph_build(g.g) == 0
+        (m,) = cf.graph_detect_mha(g.g)
+        assert m.residual_tid == iR and m.params.has_residual and not m.weights[7]
+        assert m.out_node == ids["add_r"]
     finally:
         g.destroy()
