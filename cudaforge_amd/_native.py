@@ -86,6 +86,8 @@ def _proto(lib):
         "gpu_workspace_size": (c_size_t, []),
         "gpu_workspace_release": (None, []),
         "gpu_inject_alloc_failures": (None, [c_int]),
+        "gpu_buffer_generation": (ctypes.c_uint64, []),
+        "gpu_buffer_generation_bump": (None, []),
         # registry
         "operator_init_all": (c_int, []),
         "operator_find": (POINTER(OperatorRegistryEntry), [c_char_p]),

@@ -27,10 +27,72 @@
 #include "graph.h"
 #include "gpu_ops.h"
 #include "mha_decode_int.h"
+#include "../kernels/kernels.h"
 
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+
+/* Device-held length of a uniform-length decode node (GPU executions).  The node runs in
+ * the operator's device-uniform mode (cache_len MHA_DECODE_CACHE_LEN_DEVICE_UNIFORM,
+ * lengths in slot 11), so its launches do not depend on cache_len, and a kernel issued
+ * after it adds one: a recorded execution therefore replays at every length of a decode
+ * loop.  `held` is the value the device array holds after the work issued so far. */
+typedef struct {
+    int32_t* lens;   /* device, B entries; NULL until the node first runs on the GPU */
+    int64_t  B;
+    int64_t  held;   /* -1 = unknown */
+} decode_lens_t;
+
+static decode_lens_t* decode_lens_at(inference_graph_t* g, int nid) {
+    if (nid < 0) return NULL;
+    if (nid >= g->decode_lens_cap) {
+        const int cap = g->num_nodes > nid ? g->num_nodes : nid + 1;
+        decode_lens_t* p = (decode_lens_t*)realloc(g->decode_lens, (size_t)cap * sizeof(decode_lens_t));
+        if (!p) return NULL;
+        memset(p + g->decode_lens_cap, 0, (size_t)(cap - g->decode_lens_cap) * sizeof(decode_lens_t));
+        g->decode_lens = p;
+        g->decode_lens_cap = cap;
+    }
+    return &((decode_lens_t*)g->decode_lens)[nid];
+}
+
+static void decode_lens_free(inference_graph_t* g) {
+    decode_lens_t* v = (decode_lens_t*)g->decode_lens;
+    for (int i = 0; i < g->decode_lens_cap; i++)
+        if (v[i].lens) gpu_device_free(v[i].lens);
+    free(v);
+    g->decode_lens = NULL;
+    g->decode_lens_cap = 0;
+}
+
+/* A decode node whose GPU execution uses a device-held uniform length. */
+static int uniform_decode(const graph_node_t* n) {
+    return n->type == OP_MHA_DECODE && n->params && n->params_size >= sizeof(mha_decode_params_t) &&
+           ((const mha_decode_params_t*)n->params)->cache_len >= 0;
+}
+
+/* Sets the device lengths of node nid to its cache_len (a kernel on the graph's stream)
+ * unless they hold it already.  Not while recording: the recording must advance the
+ * lengths, never set them. */
+static int decode_lens_sync(inference_graph_t* g, int nid) {
+    const graph_node_t* n = &g->nodes[nid];
+    decode_lens_t* dl = decode_lens_at(g, nid);
+    if (!dl) return -1;
+    const mha_decode_params_t* p = (const mha_decode_params_t*)n->params;
+    if (!dl->lens) {
+        if (p->batch_size <= 0 || p->batch_size > 65535) return -1;
+        dl->lens = (int32_t*)gpu_device_alloc((size_t)p->batch_size * sizeof(int32_t));
+        if (!dl->lens) return -1;
+        dl->B = p->batch_size;
+        dl->held = -1;
+    }
+    if (dl->held == p->cache_len) return 0;
+    const int rc = cf_launch_i32_update(dl->lens, (int32_t)dl->B, (int32_t)p->cache_len, 0, g->hip_graph);
+    if (rc != 0) return rc;
+    dl->held = p->cache_len;
+    return 0;
+}
 
 /* Drops the recorded execution; the next all-GPU execution starts over. */
 static void replay_reset(inference_graph_t* g) {
@@ -148,14 +210,17 @@ void graph_set_kv_cache(inference_graph_t* g, int K_tensor_id, int V_tensor_id) 
     g->kv_cache_V_tid = V_tensor_id;
 }
 
+/* (graph.c:139-149.)  GPU executions read a uniform length from the device, so a new
+ * length keeps the recording; only a switch between a uniform and a per-sequence
+ * (ragged, cache_len < 0) length changes the launches and drops it. */
 void graph_update_cache_len(inference_graph_t* g, int64_t new_cache_len) {
     if (!g) return;
     for (int i = 0; i < g->num_nodes; i++) {
         graph_node_t* n = &g->nodes[i];
-        if (n->type == OP_MHA_DECODE && n->params && n->params_size >= sizeof(mha_decode_params_t) &&
-            ((mha_decode_params_t*)n->params)->cache_len != new_cache_len) {
-            ((mha_decode_params_t*)n->params)->cache_len = new_cache_len;
-            replay_reset(g);                  /* the recorded launches hold the old length */
+        if (n->type == OP_MHA_DECODE && n->params && n->params_size >= sizeof(mha_decode_params_t)) {
+            mha_decode_params_t* p = (mha_decode_params_t*)n->params;
+            if ((p->cache_len < 0) != (new_cache_len < 0)) replay_reset(g);
+            p->cache_len = new_cache_len;
         }
     }
 }
@@ -211,6 +276,7 @@ void graph_destroy(inference_graph_t* g) {
         (void)gpu_stream_synchronize(g->hip_graph);
         gpu_stream_destroy(g->hip_graph);
     }
+    decode_lens_free(g);
     for (int i = 0; i < g->num_nodes; i++) {
         free(g->nodes[i].input_tensors);
         free(g->nodes[i].output_tensors);
@@ -325,8 +391,8 @@ static int op_produced(const inference_graph_t* g, int tid) {
 
 /* Runs one node: resolves its operator, moves its tensors to where the operator runs,
  * calls it (graph.c:820-1030). */
-static int run_node(inference_graph_t* g, const graph_node_t* n, bool use_cuda, unsigned char* fresh,
-                    int* ran_on_gpu) {
+static int run_node(inference_graph_t* g, int nid, const graph_node_t* n, bool use_cuda, unsigned char* fresh,
+                    int* ran_on_gpu, int recording) {
     int ret = 0;
     char name[64];
     const operator_registry_t* op = resolve_node(g, n, use_cuda, name, sizeof(name));
@@ -348,6 +414,33 @@ static int run_node(inference_graph_t* g, const graph_node_t* n, bool use_cuda, 
         case OP_BATCHNORM: reserve = 6; break;
         default: break;
     }
+    /* Decode on the GPU: a uniform length runs from device-held lengths (slot 11); the
+     * reference's bound on cache_len (mha_decode.c:14-16) is checked here, where it is
+     * still a host value.  Per-sequence lengths (the node's 9th weight) are checked on
+     * their host copy. */
+    const mha_decode_params_t* dp = n->type == OP_MHA_DECODE && n->params &&
+                                    n->params_size >= sizeof(mha_decode_params_t)
+                                        ? (const mha_decode_params_t*)n->params : NULL;
+    const int dev_len = on_gpu && dp && dp->cache_len >= 0 && nid >= 0;
+    mha_decode_params_t dev_params;
+    decode_lens_t* dl = NULL;
+    if (dp && dp->cache_len >= dp->max_seq) return -1;
+    if (dp && dp->cache_len < 0 && n->num_weights >= 9) {
+        const tensor_t* lt = n->weights[8];
+        if (!lt || !lt->data || lt->dtype != DATA_TYPE_I32 || lt->numel < dp->batch_size) return -1;
+        for (int64_t b = 0; b < dp->batch_size; b++) {
+            const int32_t v = ((const int32_t*)lt->data)[b];
+            if (v < 0 || v >= dp->max_seq) return -1;
+        }
+    }
+    if (dev_len) {
+        if (!recording && (ret = decode_lens_sync(g, nid)) != 0) return ret;
+        dl = decode_lens_at(g, nid);
+        if (!dl || !dl->lens || dl->held != dp->cache_len) return -1;
+        dev_params = *dp;
+        dev_params.cache_len = MHA_DECODE_CACHE_LEN_DEVICE_UNIFORM;
+        if (reserve < MHA_DECODE_SLOT_SEQLENS + 1) reserve = MHA_DECODE_SLOT_SEQLENS + 1;
+    }
     if (in_slots < reserve) in_slots = reserve;
     const int total = in_slots + n->num_outputs;
     const void* local[32];
@@ -355,6 +448,7 @@ static int run_node(inference_graph_t* g, const graph_node_t* n, bool use_cuda, 
     if (!slots) return -1;
     void** outs = (void**)&slots[in_slots];
     for (int i = n->num_inputs + n->num_weights; i < in_slots; i++) slots[i] = NULL;
+    if (dev_len) slots[MHA_DECODE_SLOT_SEQLENS] = dl->lens;
 
     for (int i = 0; i < n->num_inputs && ret == 0; i++) {
         const int tid = n->input_tensors[i];
@@ -409,7 +503,11 @@ static int run_node(inference_graph_t* g, const graph_node_t* n, bool use_cuda, 
     if (ret == 0 && copied) ret = gpu_stream_synchronize(NULL);
     if (ret == 0) {
         stream_t stream = {g->hip_graph};
-        ret = op->func(slots, outs, (const operator_params_t*)n->params, use_cuda ? &stream : NULL);
+        const void* params = dev_len ? (const void*)&dev_params : n->params;
+        ret = op->func(slots, outs, (const operator_params_t*)params, use_cuda ? &stream : NULL);
+        /* The step is done: its lengths move to the next position. */
+        if (ret == 0 && dev_len && (ret = cf_launch_i32_update(dl->lens, (int32_t)dl->B, 1, 1, g->hip_graph)) == 0)
+            dl->held = dp->cache_len + 1;
     }
     if (ret == 0 && use_cuda && !on_gpu) {
         /* A CPU op wrote host data: device copies are stale.  KV caches stay
@@ -452,13 +550,31 @@ static int preload_inputs(inference_graph_t* g, unsigned char* fresh) {
         for (int w = 0; w < n->num_weights; w++)
             if (n->weights[w] && tensor_copy_to_device(n->weights[w]) != 0) return -1;
     }
+    /* Device lengths of the decode nodes, set on the graph's stream before the recorded
+     * (or replayed) work. */
+    for (int i = 0; i < g->num_nodes; i++) {
+        if (!uniform_decode(&g->nodes[i])) continue;
+        const mha_decode_params_t* p = (const mha_decode_params_t*)g->nodes[i].params;
+        if (p->cache_len >= p->max_seq) return -1;
+        const int rc = decode_lens_sync(g, i);
+        if (rc != 0) return rc;
+    }
     /* The copies ran on the legacy stream; the graph's stream does not wait for it. */
     return gpu_stream_synchronize(NULL);
 }
 
+/* After a replay: the recording advanced every decode node's lengths by one. */
+static void decode_lens_replayed(inference_graph_t* g) {
+    for (int i = 0; i < g->num_nodes && i < g->decode_lens_cap; i++) {
+        decode_lens_t* dl = &((decode_lens_t*)g->decode_lens)[i];
+        if (dl->lens && uniform_decode(&g->nodes[i]))
+            dl->held = ((const mha_decode_params_t*)g->nodes[i].params)->cache_len + 1;
+    }
+}
+
 /* Runs every node once, in topological order, with MHA subgraph fusion on GPU
  * executions.  *all_gpu tells whether every node ran on the GPU. */
-static int run_nodes(inference_graph_t* g, bool use_cuda, unsigned char* fresh, int* all_gpu) {
+static int run_nodes(inference_graph_t* g, bool use_cuda, unsigned char* fresh, int* all_gpu, int recording) {
     /* MHA subgraph fusion (graph.c:766-815, GPU executions only): each match runs as one
      * OP_MHA_FUSED node in place of its last node; its other nodes are skipped. */
     graph_mha_match_t* fz = NULL;
@@ -499,9 +615,9 @@ static int run_nodes(inference_graph_t* g, bool use_cuda, unsigned char* fresh, 
             fn.weights = m->weights;
             fn.params = &m->params;
             fn.params_size = sizeof(m->params);
-            ret = run_node(g, &fn, use_cuda, fresh, &gpu);
+            ret = run_node(g, -1, &fn, use_cuda, fresh, &gpu, recording);
         } else {
-            ret = run_node(g, n, use_cuda, fresh, &gpu);
+            ret = run_node(g, nid, n, use_cuda, fresh, &gpu, recording);
         }
         if (!gpu) *all_gpu = 0;
     }
@@ -538,20 +654,26 @@ int graph_execute(inference_graph_t* g, tensor_t* inputs[], tensor_t* outputs[],
 
     int ret = 0;
     const int replay = use_cuda && !g->replay_off;
+    /* A buffer the recording points at was freed or handed to another stream since it was
+     * made: record again. */
+    if (replay && g->hip_graph_state == 2 && g->replay_generation != gpu_buffer_generation()) replay_reset(g);
     if (replay && g->hip_graph_state == 2 && g->hip_graph_exec) {
         ret = preload_inputs(g, fresh);
         if (ret == 0) ret = gpu_graph_launch(g->hip_graph_exec, g->hip_graph);
+        if (ret == 0) decode_lens_replayed(g);
     } else if (replay && g->hip_graph_state == 1) {
         /* Record this execution's launches, then run the recording. */
         int all_gpu = 0, recorded = 0;
         void* exec = NULL;
         ret = preload_inputs(g, fresh);
+        const uint64_t gen = gpu_buffer_generation();
         if (ret == 0 && gpu_capture_begin(g->hip_graph) == 0) {
-            const int rrc = run_nodes(g, use_cuda, fresh, &all_gpu);
+            const int rrc = run_nodes(g, use_cuda, fresh, &all_gpu, 1);
             const int crc = gpu_capture_end(g->hip_graph, &exec);
-            if (rrc == 0 && crc == 0 && all_gpu) {
+            if (rrc == 0 && crc == 0 && all_gpu && gen == gpu_buffer_generation()) {
                 g->hip_graph_exec = exec;
                 g->hip_graph_state = 2;
+                g->replay_generation = gen;
                 recorded = 1;
                 ret = gpu_graph_launch(exec, g->hip_graph);
             }
@@ -563,11 +685,13 @@ int graph_execute(inference_graph_t* g, tensor_t* inputs[], tensor_t* outputs[],
             (void)gpu_get_last_error();
             g->hip_graph_state = -1;
             memset(fresh, 0, (size_t)(g->num_tensors > 0 ? g->num_tensors : 1));
-            ret = run_nodes(g, use_cuda, fresh, &all_gpu);
+            /* The failed recording's lengths bookkeeping ran ahead of the device. */
+            for (int i = 0; i < g->decode_lens_cap; i++) ((decode_lens_t*)g->decode_lens)[i].held = -1;
+            ret = run_nodes(g, use_cuda, fresh, &all_gpu, 0);
         }
     } else {
         int all_gpu = 0;
-        ret = run_nodes(g, use_cuda, fresh, &all_gpu);
+        ret = run_nodes(g, use_cuda, fresh, &all_gpu, 0);
         if (ret == 0 && replay && all_gpu && g->hip_graph_state == 0) g->hip_graph_state = 1;
     }
     free(fresh);

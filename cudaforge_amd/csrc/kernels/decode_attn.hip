@@ -772,10 +772,12 @@ int wide_lds_bytes(int d, int G) {
     const int qh = (G * d * 2 + 1023) / 1024 * 512;
     return kWideMaxHeads * (kWideStages * 2 * 16 * d + qh) * 2;
 }
-// Uniform lengths only: with ragged lengths the grouped kernel's whole-row workgroups
-// leave a partial last round (config 4: 67 us against 64.6 us one wave per KV head).
+// Uniform lengths only (given on the host, or held on the device and equal): with
+// ragged lengths the grouped kernel's whole-row workgroups leave a partial last round
+// (config 4: 67 us against 64.6 us one wave per KV head).
 bool use_wide(const cf_decode_attn_args_t* a) {
-    return g_wide && a->elem == CF_ELEM_F16 && !a->seq_lens && a->H_kv <= kWideMaxHeads && use_fast(a);
+    return g_wide && a->elem == CF_ELEM_F16 && (!a->seq_lens || a->lens_uniform) && a->H_kv <= kWideMaxHeads &&
+           use_fast(a);
 }
 
 template <int D, int G>

@@ -33,6 +33,7 @@ typedef struct {
     const void*    v;
     void*          o;
     const int32_t* seq_lens;   /* device, NULL = uniform cache_len */
+    int32_t        lens_uniform; /* seq_lens all hold one value (a device-held uniform length) */
     float*         partials;   /* workspace */
     int32_t        B, H_q, H_kv, d;
     int32_t        max_seq, cache_len;
@@ -182,6 +183,9 @@ void cf_flash_set_mode(int32_t mode);
 
 /* CausalMask (S, S) float on the device. */
 int cf_launch_causal_mask(float* mask, int64_t S, void* stream);
+
+/* v[0..n) = value (add = 0) or += value (add = 1), as a kernel (graph decode lengths). */
+int cf_launch_i32_update(int32_t* v, int32_t n, int32_t value, int32_t add, void* stream);
 
 /* ---------------------------------------------------------------------------------
  * Layer-neighbour kernels (layer_ops.hip) for the FP16 path around attention.

@@ -18,7 +18,21 @@ __global__ void causal_mask_kernel(float* __restrict__ mask, int64_t S) {
     }
 }
 
+// v[i] = value (set) or v[i] += value: the device-held decode lengths a graph advances
+// once per step (a kernel, not a memset, so recordings replay it reliably).
+__global__ void i32_update_kernel(int32_t* __restrict__ v, int32_t n, int32_t value, int32_t add) {
+    const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (i < n) v[i] = add ? v[i] + value : value;
+}
+
 }  // namespace
+
+extern "C" int cf_launch_i32_update(int32_t* v, int32_t n, int32_t value, int32_t add, void* stream) {
+    if (!v || n <= 0) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(i32_update_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, v, n,
+                       value, add);
+    return (int)hipGetLastError();
+}
 
 extern "C" int cf_launch_causal_mask(float* mask, int64_t S, void* stream) {
     if (!mask || S <= 0) return (int)hipErrorInvalidValue;

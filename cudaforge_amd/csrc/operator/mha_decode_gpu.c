@@ -29,7 +29,8 @@ void mha_decode_set_split_chunk(int64_t chunk) { g_chunk_override = chunk > 0 ? 
 
 typedef struct {
     int64_t B, D, H, H_kv, d, max_seq, cache_len;
-    int ragged;
+    int ragged;        /* lengths come from the device array in slot 11 */
+    int lens_uniform;  /* ... and the caller guarantees they are all equal (cache_len -2) */
 } decode_shape_t;
 
 /* Validation shared by the op and the core entry (mha_decode.c:14-24, plus the GPU
@@ -44,6 +45,7 @@ static int decode_shape(const mha_decode_params_t* p, decode_shape_t* s) {
     s->max_seq = p->max_seq;
     s->cache_len = p->cache_len;
     s->ragged = p->cache_len < 0;
+    s->lens_uniform = p->cache_len == MHA_DECODE_CACHE_LEN_DEVICE_UNIFORM;
     if (s->B <= 0 || s->H <= 0 || s->d <= 0 || s->H_kv <= 0 || s->max_seq <= 0) return -1;
     if (s->H % s->H_kv != 0) return -1;
     if (!s->ragged && s->cache_len >= s->max_seq) return -1;
@@ -66,7 +68,8 @@ static void plan_split(int elem, const decode_shape_t* s, int64_t t_max, int64_t
          * kernel is one workgroup per (split, b) covering every KV head, the other fp16
          * kernel one wave per (split, b, KV head), each as many per CU as its LDS rings
          * allow; the others are 2-4 waves with registers as their only buffer. */
-        const int32_t wide_cu = s->ragged ? 0 : cf_decode_attn_wide_wgs_per_cu(elem, (int)s->d, G, (int)s->H_kv);
+        const int spread = s->ragged && !s->lens_uniform;   /* lengths may differ */
+        const int32_t wide_cu = spread ? 0 : cf_decode_attn_wide_wgs_per_cu(elem, (int)s->d, G, (int)s->H_kv);
         const int64_t units = wide_cu > 0 ? s->B : s->B * (fast ? s->H_kv : s->H);
         const int32_t ring_cu = wide_cu > 0 ? wide_cu : cf_decode_attn_wgs_per_cu(elem, (int)s->d, G);
         const int64_t per_cu = ring_cu > 0 ? ring_cu : 4;
@@ -75,7 +78,7 @@ static void plan_split(int elem, const decode_shape_t* s, int64_t t_max, int64_t
          * reaches, so plan four times as many (shorter) splits; the busy ones then fill
          * the CUs and rebalance as short sequences finish.  Measured on config 4 shapes:
          * 1-17 % faster than one split per CU slot. */
-        if (s->ragged) target *= 4;
+        if (spread) target *= 4;
         int64_t n = cf_ceil_div(target, units);
         const int64_t nmax = cf_ceil_div(t_max, q);
         if (n > nmax) n = nmax;
@@ -106,6 +109,7 @@ static size_t attn_args(int elem, const decode_shape_t* s, const int32_t* lens,
     int64_t chunk, n_split;
     plan_split(elem, s, t_max, &chunk, &n_split);
     a->seq_lens = lens;
+    a->lens_uniform = s->lens_uniform;
     a->B = (int32_t)s->B;
     a->H_q = (int32_t)s->H;
     a->H_kv = (int32_t)s->H_kv;

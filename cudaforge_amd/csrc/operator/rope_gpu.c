@@ -30,6 +30,7 @@ static void rope_tables_release(void) {
         if (g_tables[i].table) gpu_device_free(g_tables[i].table);
         memset(&g_tables[i], 0, sizeof(g_tables[i]));
     }
+    gpu_buffer_generation_bump();
 }
 
 /* (cos, sin) of angle = pos / powf(base, 2i/d), rope.c:38-45. */
@@ -76,9 +77,11 @@ const float* rope_table_device(float base, int64_t d, int64_t n_pos) {
     free(host);
     rope_table_t* t = hit ? hit : slot;
     if (t->table) {
-        /* Work already enqueued may still read the old table. */
+        /* Work already enqueued may still read the old table, and a recording may
+         * point at it. */
         gpu_device_synchronize();
         gpu_device_free(t->table);
+        gpu_buffer_generation_bump();
     }
     t->dev = dev;
     t->base = base;

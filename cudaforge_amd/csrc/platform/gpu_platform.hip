@@ -31,6 +31,10 @@ Workspace g_ws[kMaxDevices][kWsSlots];
 unsigned long g_ws_clock = 0;
 int g_inject_failures = 0;
 int g_initialized_device = -1;
+// Bumped whenever a buffer that recorded work may point at is freed or handed to
+// another stream (workspace slots, operator tables): recordings made before the bump
+// must not be replayed.
+uint64_t g_buffer_generation = 1;
 
 int current_device() {
     int dev = 0;
@@ -252,6 +256,7 @@ void* gpu_workspace_get_stream(gpu_stream_t stream, size_t bytes) {
         for (int i = 1; i < kWsSlots; i++)
             if (g_ws[dev][i].last < slot->last) slot = &g_ws[dev][i];
         (void)hipDeviceSynchronize();   // its previous stream may still be using it
+        g_buffer_generation++;          // ... and a recording on that stream may point at it
     }
     slot->used = true;
     slot->stream = st;
@@ -264,6 +269,7 @@ void* gpu_workspace_get_stream(gpu_stream_t stream, size_t bytes) {
         (void)hipFree(slot->base);
         slot->base = nullptr;
         slot->bytes = 0;
+        g_buffer_generation++;
     }
     size_t grow = need < (size_t)64 << 20 ? (size_t)64 << 20 : need + need / 4;
     void* p = gpu_device_alloc(grow);
@@ -295,9 +301,13 @@ void gpu_workspace_release(void) {
             if (g_ws[d][i].base) (void)hipFree(g_ws[d][i].base);
             g_ws[d][i] = Workspace{};
         }
+        g_buffer_generation++;
         (void)hipSetDevice(prev);
     }
 }
+
+extern "C" uint64_t gpu_buffer_generation(void) { return g_buffer_generation; }
+extern "C" void gpu_buffer_generation_bump(void) { g_buffer_generation++; }
 
 static void (*g_at_finalize[8])(void);
 

@@ -122,6 +122,14 @@ void*  gpu_workspace_get(size_t bytes);
 size_t gpu_workspace_size(void);     /* bytes held on the current device, all streams */
 void   gpu_workspace_release(void);
 
+/* Buffer generation: a counter bumped whenever a device buffer that recorded work
+ * (a HIP graph) may hold a pointer to is freed or handed to another stream: workspace
+ * growth, takeover and release, and operator tables rebuilt larger.  A recording made
+ * at one generation must not be replayed at another (graph_execute re-records).
+ * gpu_buffer_generation_bump is for operators that keep such buffers themselves. */
+uint64_t gpu_buffer_generation(void);
+void     gpu_buffer_generation_bump(void);
+
 /* Registers fn to run at gpu_platform_finalize, before the workspaces are freed: for
  * device tables an operator keeps across calls (the RoPE angle tables).  Up to 8
  * callbacks; registering the same one again is a no-op.  0, or -1 when full. */

@@ -105,6 +105,9 @@ typedef struct {
     int64_t         graph_cache_B;
     int64_t         graph_cache_S;
     int             replay_off;      /* graph_set_replay(g, 0) */
+    uint64_t        replay_generation; /* gpu_buffer_generation() when hip_graph_exec was recorded */
+    void*           decode_lens;     /* per node: device-held lengths of uniform decode nodes */
+    int             decode_lens_cap; /* entries in decode_lens */
 } inference_graph_t;
 
 inference_graph_t* graph_create(void);
@@ -132,11 +135,14 @@ int   graph_execute(inference_graph_t* g, tensor_t* inputs[],
  * non-blocking stream the graph owns.  After one execution in which every node ran on
  * the GPU, the next execution uploads the graph inputs, records the node launches into a
  * HIP graph and launches it; later executions only upload the inputs, replay the
- * recording and download the outputs.  Adding nodes or tensors, graph_build,
- * graph_set_kv_cache and a changed graph_update_cache_len discard the recording (a
- * decode loop that moves cache_len every step therefore runs eagerly).  An execution
- * with a CPU operator, or whose recording fails, stays eager.  graph_set_replay(g, 0)
- * turns it off; graph_replay_state(g) returns hip_graph_state. */
+ * recording and download the outputs.  A decode node's uniform cache_len is held on
+ * the device and advanced by the recording, so a decode loop that moves cache_len by
+ * one per step keeps replaying.  Adding nodes or tensors, graph_build,
+ * graph_set_kv_cache, switching a decode node between uniform and per-sequence lengths,
+ * and a change of gpu_buffer_generation() (a buffer the recording points at was freed)
+ * discard the recording.  An execution with a CPU operator, or whose recording fails,
+ * stays eager.  graph_set_replay(g, 0) turns it off; graph_replay_state(g) returns
+ * hip_graph_state. */
 void  graph_set_replay(inference_graph_t* g, int enable);
 int   graph_replay_state(const inference_graph_t* g);
 

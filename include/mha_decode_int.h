@@ -7,7 +7,12 @@
  * Extension (absent in the reference, opt-in only): cache_len < 0 selects ragged mode.
  * The op then reads per-sequence cache lengths from one extra input slot (index 11),
  * an int32 device array of B entries; sequence b attends positions 0..len[b] after
- * appending its new token at position len[b].
+ * appending its new token at position len[b].  cache_len == -2 is the same with the
+ * caller's guarantee that all B lengths are equal (a uniform length kept on the device,
+ * as graph_execute does so that a recorded step replays at every length): the op then
+ * plans and runs as for a uniform length, over max_seq positions.  Device-held lengths
+ * cannot be checked on the host: a length >= max_seq appends nothing and attends
+ * max_seq positions, a negative one attends position 0 only.
  */
 #ifndef CF_MHA_DECODE_INT_H_
 #define CF_MHA_DECODE_INT_H_
@@ -28,5 +33,6 @@ typedef struct {
 #define MHA_DECODE_NUM_INPUTS   11
 #define MHA_DECODE_NUM_OUTPUTS  3
 #define MHA_DECODE_SLOT_SEQLENS 11
+#define MHA_DECODE_CACHE_LEN_DEVICE_UNIFORM (-2)
 
 #endif /* CF_MHA_DECODE_INT_H_ */

@@ -344,3 +344,64 @@ def build_attention_subgraph(g: Graph, c: FusedCase, x_id, r_id=None, *, bias=Tr
         cur = out
     ids["out"] = cur
     return ids
+
+
+def build_fused_graph(lib, c: FusedCase, f16_out=False):
+    """One OP_MHA_FUSED node with INPUT/OUTPUT wrappers (tests/test_bert_mha.c:167-306);
+    F32 tensors, or an F16 output tensor.  Returns (graph, node id, X tensor, Y tensor)."""
+    g = Graph(lib)
+    tX, iX = g.tensor(c.X)
+    tR, iR = g.tensor(c.R if c.R is not None else np.zeros_like(c.X))
+    tY, iY = (g.tensor(np.zeros(c.X.shape, np.float16), DT_F16) if f16_out
+              else g.tensor(np.zeros_like(c.X), DT_F32))
+    ws = [g.tensor(w)[0] for w in (c.WQ, c.bQ, c.WK, c.bK, c.WV, c.bV, c.WO, c.bO)]
+    p = O.fused_params(c.B, c.S, c.D, c.H, c.H_kv, c.d, c.residual, c.causal)
+    nid = g.node(OP_MHA_FUSED, [iX, iR], [iY], ws, p)
+    g.lib.graph_set_input(g.g, g.node(OP_INPUT, [], [iX]))
+    g.lib.graph_set_output(g.g, g.node(OP_OUTPUT, [iY], []))
+    assert lib.graph_build(g.g) == 0
+    return g, nid, tX, tY
+
+
+def fused_ref64(c: FusedCase):
+    """MHA_Fused in float64 (numpy) on the case's exact inputs: projections, scaled
+    scores with the causal rule j <= i, softmax, P.V, W_O, bias, residual
+    (mha_fused.c:67-172 in exact arithmetic).  Returns (B, S, D) float64."""
+    f = lambda a: np.asarray(a, np.float64)
+    B, S, D, H, H_kv, d = c.B, c.S, c.D, c.H, c.H_kv, c.d
+    G = H // H_kv
+    X = f(c.X).reshape(B * S, D)
+    q = (X @ f(c.WQ) + f(c.bQ)).reshape(B, S, H, d).transpose(0, 2, 1, 3)
+    k = (X @ f(c.WK) + f(c.bK)).reshape(B, S, H_kv, d).transpose(0, 2, 1, 3)
+    v = (X @ f(c.WV) + f(c.bV)).reshape(B, S, H_kv, d).transpose(0, 2, 1, 3)
+    k = np.repeat(k, G, axis=1)
+    v = np.repeat(v, G, axis=1)
+    s = np.matmul(q, k.transpose(0, 1, 3, 2)) * float(np.float32(1.0 / np.sqrt(d)))
+    if c.causal:
+        s = np.where(np.tril(np.ones((S, S), bool)), s, -np.inf)
+    s = s - s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=-1, keepdims=True)
+    o = np.matmul(p, v).transpose(0, 2, 1, 3).reshape(B * S, D)
+    y = o @ f(c.WO) + f(c.bO)
+    if c.residual and c.R is not None:
+        y = y + f(c.R).reshape(B * S, D)
+    return y.reshape(B, S, D)
+
+
+def attn_ref64_all(Q, K, V, attend, H_kv, scale):
+    """Decode attention core in float64 for every (b, head), vectorised over heads."""
+    B, H, d = Q.shape
+    G = H // H_kv
+    out = np.zeros((B, H, d))
+    for b in range(B):
+        T = int(attend[b])
+        k = K[b, :T].astype(np.float64)                      # (T, H_kv, d)
+        v = V[b, :T].astype(np.float64)
+        q = Q[b].astype(np.float64).reshape(H_kv, G, d)
+        s = np.einsum("tkd,kgd->kgt", k, q) * scale
+        s -= s.max(axis=-1, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(axis=-1, keepdims=True)
+        out[b] = np.einsum("kgt,tkd->kgd", p, v).reshape(H, d)
+    return out

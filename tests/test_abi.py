@@ -22,7 +22,7 @@ import pytest
 
 import oracle as O
 from helpers import (DT_F16, DT_F32, OP_CAUSAL_MASK, OP_INPUT, OP_MHA_DECODE, OP_MHA_FUSED, OP_OUTPUT,
-                     OP_RELU, DecodeCase, FusedCase, Graph)
+                     OP_RELU, DecodeCase, FusedCase, Graph, build_fused_graph)
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 INCLUDE = os.path.join(ROOT, "include")
@@ -196,21 +196,6 @@ def test_graph_topological_order_and_cycle(native):
     g.destroy()
 
 
-def build_fused_graph(lib, c: FusedCase, f16_out=False):
-    g = Graph(lib)
-    tX, iX = g.tensor(c.X)
-    tR, iR = g.tensor(c.R if c.R is not None else np.zeros_like(c.X))
-    tY, iY = (g.tensor(np.zeros(c.X.shape, np.float16), DT_F16) if f16_out
-              else g.tensor(np.zeros_like(c.X), DT_F32))
-    ws = [g.tensor(w)[0] for w in (c.WQ, c.bQ, c.WK, c.bK, c.WV, c.bV, c.WO, c.bO)]
-    p = O.fused_params(c.B, c.S, c.D, c.H, c.H_kv, c.d, c.residual, c.causal)
-    nid = g.node(OP_MHA_FUSED, [iX, iR], [iY], ws, p)
-    g.lib.graph_set_input(g.g, g.node(OP_INPUT, [], [iX]))
-    g.lib.graph_set_output(g.g, g.node(OP_OUTPUT, [iY], []))
-    assert lib.graph_build(g.g) == 0
-    return g, nid, tX, tY
-
-
 def test_graph_name_resolution(cpu_ops):
     lib = cpu_ops
     c = FusedCase(1, 4, 2, 2, 8, fill="lcg", residual=True)
@@ -344,3 +329,50 @@ def test_decode_split_plan_invariants(native, B, H, H_kv, d, cl, max_seq, f16):
     assert n * chunk >= t_max and (n - 1) * chunk < t_max
     if fast_f16:
         assert chunk % 32 == 0
+
+
+@pytest.mark.parametrize("B,H,H_kv,d,max_seq", [(16, 32, 8, 128, 4096), (4, 32, 8, 128, 32768), (3, 6, 2, 32, 255)])
+def test_device_uniform_length_plans_as_uniform_over_capacity(native, B, H, H_kv, d, max_seq):
+    """cache_len -2 (lengths in slot 11, all equal: the graph's device-held length) plans
+    like a uniform length over the whole capacity, so a recorded step fits every length;
+    cache_len -1 (ragged) plans four times as many splits."""
+    import cudaforge_amd as cf
+
+    def plan(cl):
+        p = cf.MhaDecodeParams(B, H * d, H, H_kv, d, 0.1, cl, max_seq)
+        chunk, n = ctypes.c_int64(0), ctypes.c_int64(0)
+        assert native.mha_decode_plan(ctypes.addressof(p), 1, ctypes.byref(chunk), ctypes.byref(n)) == 0
+        return chunk.value, n.value
+
+    assert plan(-2) == plan(max_seq - 1)
+    assert plan(-1)[1] >= plan(-2)[1]
+
+
+def test_buffer_generation_counter(native):
+    """gpu_buffer_generation_bump moves the counter that invalidates recordings."""
+    g0 = native.gpu_buffer_generation()
+    native.gpu_buffer_generation_bump()
+    assert native.gpu_buffer_generation() == g0 + 1
+
+
+def test_graph_decode_length_past_capacity_cpu(cpu_ops):
+    """The executor rejects cache_len >= max_seq with -1 before running the node, as the
+    reference op does (mha_decode.c:14-16)."""
+    lib = cpu_ops
+    c = DecodeCase(1, 4, 2, 8, 8, cache_len=7, seed=4, wstd=0.3)
+    g = Graph(lib)
+    tX, iX = g.tensor(c.X)
+    tK, iK = g.tensor(c.Kc)
+    tV, iV = g.tensor(c.Vc)
+    tY, iY = g.tensor(np.zeros_like(c.X))
+    ws = [g.tensor(w)[0] for w in (c.WQ, c.bQ, c.WK, c.bK, c.WV, c.bV, c.WO, c.bO)]
+    g.node(OP_MHA_DECODE, [iX, iK, iV], [iY, iK, iV], ws, O.decode_params(1, c.D, c.H, c.H_kv, c.d, 7, 8))
+    lib.graph_set_input(g.g, g.node(OP_INPUT, [], [iX]))
+    lib.graph_set_output(g.g, g.node(OP_OUTPUT, [iY], []))
+    lib.graph_set_kv_cache(g.g, iK, iV)
+    assert lib.graph_build(g.g) == 0
+    ins, outs = (c_void_p * 1)(tX), (c_void_p * 1)(tY)
+    assert lib.graph_execute(g.g, ins, outs, False) == 0
+    lib.graph_update_cache_len(g.g, 8)
+    assert lib.graph_execute(g.g, ins, outs, False) == -1
+    g.destroy()

@@ -163,19 +163,21 @@ def test_split_count_invariance(gpu, native):
 
 
 def test_config2_full_size_core(gpu):
-    """BASELINE config 2 at full size (B=16, 32/8 heads, d=128, KV 4096, fp16): every row is
-    checked against a float64 reference for two batch rows, and the mean output over the
-    batch against its float64 value (a checksum of the remaining rows)."""
+    """BASELINE config 2 at full size (B=16, 32/8 heads, d=128, KV 4096, fp16): every
+    output row of every batch row against a float64 reference, and batch rows 0 and 15
+    also against the scalar float64 loop."""
+    from helpers import attn_ref64_all
     B, H, H_kv, d, T = 16, 32, 8, 128, 4096
     Q = O.round_f16(O.normal((B, H, d), 1))
     K = O.round_f16(O.normal((B, T, H_kv, d), 2))
     V = O.round_f16(O.normal((B, T, H_kv, d), 3))
     got = run_decode_attn_gpu(Q, K, V, T - 1, H_kv, True)
     scale = float(1 / np.sqrt(d))
+    ref = attn_ref64_all(Q, K, V, [T] * B, H_kv, scale)
+    per_row = np.abs(ref - got).reshape(B, -1).max(axis=1)
+    assert (per_row <= TOL16).all(), per_row
     rows = [0, B - 1]
-    ref = attn_ref64(Q[rows], K[rows], V[rows], [T, T], H_kv, scale)
-    assert max_abs(ref, got[rows]) <= TOL16
-    assert np.isfinite(got).all()
+    assert max_abs(attn_ref64(Q[rows], K[rows], V[rows], [T, T], H_kv, scale), got[rows]) <= TOL16
 
 
 def test_cache_len_zero_is_value_row(gpu):
@@ -335,9 +337,9 @@ def test_grouped_and_one_wave_split_kernels_agree(gpu, native, d, G, H_kv, T):
 @pytest.mark.parametrize("f16", [False, True])
 def test_graph_decode_replay(gpu, native, f16):
     """A decode graph executed repeatedly at one cache_len (each execution rewrites row
-    cache_len) is recorded on its second execution and replayed after; a length change
-    drops the recording.  Every execution equals, bit for bit, the same graph with replay
-    off, and the oracle."""
+    cache_len) is recorded on its second execution and replayed after; the length lives
+    on the device, so a length change keeps the recording.  Every execution equals, bit
+    for bit, the same graph with replay off, and the oracle."""
     from helpers import build_decode_graph
     dt = np.float16 if f16 else np.float32
     tol = TOL16 if f16 else TOL32
@@ -370,10 +372,83 @@ def test_graph_decode_replay(gpu, native, f16):
                 prev.X = last_x5
                 _, want_case.Kc, want_case.Vc = prev.oracle()
             assert max_abs(want_case.oracle()[0], outs[0]) <= tol
-        assert states == [1, 2, 2, 2, 1, 2, 2]
+        assert states == [1, 2, 2, 2, 2, 2, 2]
     finally:
         for g, _ in graphs:
             g.destroy()
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_graph_decode_replay_advancing_length(gpu, native, f16):
+    """A token-by-token decode loop (execute, then graph_update_cache_len(L + 1)) over
+    seven tokens: from the third execution on, every step replays the one recording
+    (state 2), each output equals the replay-off graph bit for bit and the oracle run
+    step by step on its own caches.  Then a buffer-generation bump (a workspace or table
+    that a recording may point at was freed) makes the next execution re-record."""
+    from helpers import build_decode_graph
+    dt = np.float16 if f16 else np.float32
+    tol = TOL16 if f16 else TOL32
+    L0, n_tok = 5, 7
+    c = DecodeCase(2, 8, 2, 64, 16, cache_len=L0, seed=81, f16=f16, wstd=0.1)
+    graphs = [build_decode_graph(native, c) for _ in range(2)]
+    native.graph_set_replay(graphs[1][0].g, 0)
+    Kc, Vc = c.Kc, c.Vc
+    try:
+        states = []
+        for step in range(n_tok):
+            L = L0 + step
+            X = O.normal(c.X.shape, 900 + step)
+            if f16:
+                X = O.round_f16(X)
+            outs = []
+            for g, t in graphs:
+                g.write(t["X"], O.to_f16(X) if f16 else X)
+                ins, os_ = (ctypes.c_void_p * 1)(t["X"]), (ctypes.c_void_p * 1)(t["Y"])
+                assert native.graph_execute(g.g, ins, os_, True) == 0
+                outs.append(g.read(t["Y"], c.X.shape, dt).astype(np.float32))
+                native.graph_update_cache_len(g.g, L + 1)
+            states.append(native.graph_replay_state(graphs[0][0].g))
+            assert np.array_equal(outs[0], outs[1]), f"step {step}"
+            ref = DecodeCase(2, 8, 2, 64, 16, cache_len=L, seed=81, f16=f16, wstd=0.1)
+            ref.X, ref.Kc, ref.Vc = X, Kc, Vc
+            want = ref.oracle()
+            assert max_abs(want[0], outs[0]) <= tol, f"step {step}"
+            Kc, Vc = want[1], want[2]
+        assert states == [1, 2, 2, 2, 2, 2, 2]
+        # Caches on the device hold every appended token.
+        g0, t0 = graphs[0]
+        assert native.tensor_copy_to_host(t0["K"]) == 0
+        K_dev = g0.read(t0["K"], c.Kc.shape, dt).astype(np.float32)
+        assert max_abs(Kc[:, :L0 + n_tok], K_dev[:, :L0 + n_tok]) <= tol
+        # Re-record after a generation bump.
+        native.gpu_buffer_generation_bump()
+        for g, t in graphs:
+            ins, os_ = (ctypes.c_void_p * 1)(t["X"]), (ctypes.c_void_p * 1)(t["Y"])
+            assert native.graph_execute(g.g, ins, os_, True) == 0
+        assert native.graph_replay_state(graphs[0][0].g) == 1
+        ins, os_ = (ctypes.c_void_p * 1)(t0["X"]), (ctypes.c_void_p * 1)(t0["Y"])
+        assert native.graph_execute(g0.g, ins, os_, True) == 0
+        assert native.graph_replay_state(g0.g) == 2
+    finally:
+        for g, _ in graphs:
+            g.destroy()
+
+
+def test_graph_decode_rejects_length_past_capacity(gpu, native):
+    """cache_len >= max_seq returns -1 from graph_execute (the reference op's check,
+    mha_decode.c:14-16), eager or recorded."""
+    from helpers import build_decode_graph
+    c = DecodeCase(1, 4, 2, 64, 8, cache_len=6, seed=83, f16=True, wstd=0.1)
+    g, t = build_decode_graph(native, c)
+    ins, os_ = (ctypes.c_void_p * 1)(t["X"]), (ctypes.c_void_p * 1)(t["Y"])
+    try:
+        for L in (6, 7):
+            native.graph_update_cache_len(g.g, L)
+            assert native.graph_execute(g.g, ins, os_, True) == 0
+        native.graph_update_cache_len(g.g, 8)
+        assert native.graph_execute(g.g, ins, os_, True) == -1
+    finally:
+        g.destroy()
 
 
 @pytest.mark.parametrize("bn", [64, 128, 256])

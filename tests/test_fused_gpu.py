@@ -62,10 +62,14 @@ def test_fused_vs_oracle(gpu, f16, B, S, H, H_kv, d, causal):
 
 
 def test_config3_bert_base_full_size(gpu):
-    """B=8, S=512, D=768, 12x64, fp16, no mask.  Batch rows 0 and 7 of
-    the full-size run vs the oracle on those rows alone."""
+    """B=8, S=512, D=768, 12x64, fp16, no mask.  Every row of the
+    full-size run against a float64 evaluation of the same math, and batch rows 0 and 7
+    against the oracle on those rows alone."""
+    from helpers import fused_ref64
     c = FusedCase(8, 512, 12, 12, 64, seed=3, f16=True)
     got = run_fused_gpu(c)
+    per_row = np.abs(fused_ref64(c) - got).max(axis=2)
+    assert (per_row <= TOL16).all(), per_row.max()
     for b in (0, 7):
         sub = FusedCase(1, 512, 12, 12, 64, seed=3, f16=True)
         for n in ("X", "WQ", "bQ", "WK", "bK", "WV", "bV", "WO", "bO"):
@@ -76,9 +80,13 @@ def test_config3_bert_base_full_size(gpu):
 
 
 def test_config5_causal_full_size_row(gpu):
-    """BASELINE config 5 shape (B=4, S=1024, D=1024, 16x64, causal, fp16): batch row 2."""
+    """BASELINE config 5 shape (B=4, S=1024, D=1024, 16x64, causal, fp16): every row
+    against a float64 evaluation of the same math, and batch row 2 against the oracle."""
+    from helpers import fused_ref64
     c = FusedCase(4, 1024, 16, 16, 64, seed=5, f16=True, causal=True)
     got = run_fused_gpu(c)
+    per_row = np.abs(fused_ref64(c) - got).max(axis=2)
+    assert (per_row <= TOL16).all(), per_row.max()
     sub = FusedCase(1, 1024, 16, 16, 64, seed=5, f16=True, causal=True)
     for n in ("WQ", "bQ", "WK", "bK", "WV", "bV", "WO", "bO"):
         setattr(sub, n, getattr(c, n))
