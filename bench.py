@@ -33,6 +33,7 @@ sys.path.insert(0, ROOT)
 METRIC = "split-KV decode µs/step + HBM GB/s; fused MHA prefill TFLOP/s (fp16)"
 HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
 
 
 def log(msg: str) -> None:
@@ -223,19 +224,40 @@ def bench_layer_neighbours(cf, stream, steps, warmup, rows=4096, D=768, F=3072, 
     return ms_ln, 2 * rows * D * 2 + 2 * D * 2, ms_mm, 2 * rows * D * F
 
 
-def bench_fused(cf, stream, steps, warmup, B, S, H, d, causal, seed):
+def fused_kernel_times(cf, ins, outs, params, stream, f16, iters, warmup):
+    """Mean time per launch of the fused op's three kernels (QKV GEMM, attention, WO
+    GEMM), each launched back to back between HIP events on the op's stream."""
+    import ctypes
+    from ctypes import POINTER, c_float, c_void_p
+    from cudaforge_amd.api import _ptr
+    lib = cf.load_library()
+    ia = (c_void_p * len(ins))(*[_ptr(x) for x in ins])
+    oa = (c_void_p * len(outs))(*[_ptr(x) for x in outs])
+    ms = (c_float * 3)()
+    rc = lib.mha_fused_kernel_times(ctypes.cast(ia, POINTER(c_void_p)), ctypes.cast(oa, POINTER(c_void_p)),
+                                    ctypes.addressof(params), stream.stream_t(), 1 if f16 else 0, warmup, iters, ms)
+    if rc != 0:
+        raise RuntimeError(f"mha_fused_kernel_times returned {rc}")
+    return [ms[0], ms[1], ms[2]]
+
+
+def bench_fused(cf, stream, steps, warmup, B, S, H, d, causal, seed, f16=True):
+    """The fused op at one shape: ms per call, the algorithmic FLOPs, and per kernel
+    (QKV GEMM, attention, WO GEMM) its time and algorithmic FLOPs."""
     D = H * d
-    mk = (lambda shape, s, std=1.0: cf.DeviceBuffer.from_numpy(f16_normal(shape, seed + s, std)))
-    zero = (lambda n: cf.DeviceBuffer.from_numpy(np.zeros(n, np.float16)))
+    dt = np.float16 if f16 else np.float32
+    mk = (lambda shape, s, std=1.0: cf.DeviceBuffer.from_numpy(normal(shape, seed + s, std).astype(dt)))
+    zero = (lambda n: cf.DeviceBuffer.from_numpy(np.zeros(n, dt)))
     ins = [mk((B, S, D), 1), None, mk((D, D), 2, 0.02), zero(D), mk((D, D), 3, 0.02), zero(D),
            mk((D, D), 4, 0.02), zero(D), mk((D, D), 5, 0.02), zero(D)]
-    Y = cf.DeviceBuffer.empty((B, S, D), np.float16)
+    Y = cf.DeviceBuffer.empty((B, S, D), dt)
     p = cf.MhaFusedParams(B, S, D, H, H, d, float(1 / np.sqrt(d)), False, causal)
-    ms = time_op(cf, "mha_fused_f16_cuda", ins, [Y], p, stream, steps, warmup)
-    proj = 2 * B * S * D * D * 4
+    name = "mha_fused_f16_cuda" if f16 else "mha_fused_f32_cuda"
+    ms = time_op(cf, name, ins, [Y], p, stream, steps, warmup)
+    kms = fused_kernel_times(cf, ins, [Y], p, stream, f16, steps, warmup)
     pairs = B * H * (S * (S + 1) // 2 if causal else S * S)
-    flops = proj + 4 * pairs * d
-    return ms, flops
+    kfl = [2 * B * S * D * 3 * D, 4 * pairs * d, 2 * B * S * D * D]
+    return ms, sum(kfl), kms, kfl
 
 
 def cpu_baseline_decode(budget_s: float):
@@ -269,6 +291,70 @@ def cpu_baseline_decode(budget_s: float):
                   f"scaled x16 to one step; oracle/oracle.c decode_attn, -O3, 1 thread "
                   f"(host has {os.cpu_count()} logical CPUs)",
     }
+
+
+def _cpu_time(fn, budget_s, min_runs=1):
+    """Seconds per call of fn, repeated until budget_s has passed (at least min_runs)."""
+    import oracle as O
+    t0 = O.now()
+    n = 0
+    while n < min_runs or O.now() - t0 < budget_s:
+        fn()
+        n += 1
+    return (O.now() - t0) / n, n
+
+
+def cpu_baseline_configs(budget_s: float) -> dict:
+    """The CPU oracle (C port of the reference fallbacks, -O3, one thread) on configs 1,
+    3, 4 and 5, each on a bounded sample scaled to one step, beside the GPU figures."""
+    import oracle as O
+    out = {}
+    cores = os.cpu_count()
+    # Config 1: the full MHA_Decode FP32 op (mha_decode.c:11-125 restated), whole step.
+    B, H, d, T = 1, 12, 64, 1024
+    D = H * d
+    args = [O.normal((B, 1, D), 11), O.normal((B, T, H, d), 12), O.normal((B, T, H, d), 13),
+            O.normal((D, D), 14, 0, 0.02), np.zeros(D, np.float32), O.normal((D, D), 15, 0, 0.02),
+            np.zeros(D, np.float32), O.normal((D, D), 16, 0, 0.02), np.zeros(D, np.float32),
+            O.normal((D, D), 17, 0, 0.02), np.zeros(D, np.float32)]
+    p = O.decode_params(B, D, H, H, d, T - 1, T)
+    sec, n = _cpu_time(lambda: O.mha_decode(*args, p), budget_s / 4, 3)
+    alg = (2 * B * T * H * d + 4 * D * D + 4 * D + 2 * B * D + 2 * B * H * d) * 4
+    out["config1_decode_full_op_f32"] = {"us_per_step": round(sec * 1e6, 1), "GB_s": round(alg / sec / 1e9, 3),
+                                         "cores": 1, "kind": "port",
+                                         "sample": f"{n} whole steps (includes the reference's per-call cache copy)"}
+    # Config 4: ragged core, one batch row (length 10639 of the seed-404 draw), scaled by
+    # the total attended length.
+    lens = np.random.default_rng(404).integers(1024, 32768 + 1, size=4).astype(np.int64)
+    L = int(lens[1])
+    Q = O.round_f16(O.normal((1, 32, 128), 401))
+    K = O.round_f16(O.normal((1, L, 8, 128), 402))
+    V = O.round_f16(O.normal((1, L, 8, 128), 403))
+    sec, n = _cpu_time(lambda: O.decode_attn(Q, K, V, np.array([L], np.int32), float(1 / np.sqrt(128)), 8),
+                       budget_s / 4, 1)
+    step = sec * float(lens.sum()) / L
+    alg = 4096 * int(lens.sum()) + 2 * 4 * 32 * 128 * 2
+    out["config4_decode_core_ragged"] = {"us_per_step": round(step * 1e6, 1), "GB_s": round(alg / step / 1e9, 3),
+                                         "cores": 1, "kind": "port",
+                                         "sample": f"{n} x batch row 1 (L={L}) of 4, scaled by sum(L)/L = "
+                                                   f"{float(lens.sum()) / L:.3f}"}
+    # Configs 3 and 5: the fused op on one batch row, scaled by B.
+    for key, (Bc, S, H, d, causal) in {"config3_prefill_bert_base": (8, 512, 12, 64, False),
+                                       "config5_prefill_causal_gpt2_medium": (4, 1024, 16, 64, True)}.items():
+        D = H * d
+        X = O.round_f16(O.normal((1, S, D), 31))
+        Ws = [O.round_f16(O.normal((D, D), 32 + i, 0, 0.02)) for i in range(4)]
+        z = np.zeros(D, np.float32)
+        pf = O.fused_params(1, S, D, H, H, d, False, causal)
+        sec, n = _cpu_time(lambda: O.mha_fused(X, None, Ws[0], z, Ws[1], z, Ws[2], z, Ws[3], z, pf), 0.0, 1)
+        step = sec * Bc
+        pairs = Bc * H * (S * (S + 1) // 2 if causal else S * S)
+        fl = 2 * Bc * S * D * D * 4 + 4 * pairs * d
+        out[key] = {"us_per_step": round(step * 1e6, 1), "GFLOP_s": round(fl / step / 1e9, 3), "cores": 1,
+                    "kind": "port", "sample": f"{n} x 1 of {Bc} batch rows, scaled x{Bc}; fp16 values as fp32"}
+    for v in out.values():
+        v["host_logical_cpus"] = cores
+    return out
 
 
 def read_traffic(kernel_prefix: str):
@@ -324,18 +410,34 @@ def vendor_comparison(reps: int = 50) -> dict:
     return out
 
 
-def bench_prefill(cf, stream, steps, warmup) -> dict:
-    """Configs 3 and 5 through mha_fused_f16_cuda: TFLOP/s over the algorithmic FLOPs."""
+def bench_prefill(cf, stream, steps, warmup, fp32=True) -> dict:
+    """Configs 3 and 5 through mha_fused_f16_cuda, and config 3's shape through the FP32
+    entry (mha_fused_f32_cuda, fp32 MFMA): TFLOP/s over the algorithmic FLOPs, with a
+    roofline block per config (the whole op and each of its three kernels, timed in this
+    run) against the dense MFMA peak of the arithmetic type."""
     out = {}
-    for key, (B, S, H, d, causal, seed) in {
-            "prefill_config3_bert_base_f16": (8, 512, 12, 64, False, 300),
-            "prefill_config5_causal_gpt2_medium_f16": (4, 1024, 16, 64, True, 500)}.items():
+    legs = {"prefill_config3_bert_base_f16": (8, 512, 12, 64, False, 300, True),
+            "prefill_config5_causal_gpt2_medium_f16": (4, 1024, 16, 64, True, 500, True)}
+    if fp32:
+        legs["prefill_config3_bert_base_f32"] = (8, 512, 12, 64, False, 300, False)
+    for key, (B, S, H, d, causal, seed, f16) in legs.items():
         log(key)
-        ms_p, fl = bench_fused(cf, stream, max(steps // 4, 10), max(warmup // 2, 3), B, S, H, d, causal, seed)
+        n = max(steps // 4, 10) if f16 else max(steps // 20, 5)
+        ms_p, fl, kms, kfl = bench_fused(cf, stream, n, max(warmup // 2, 3), B, S, H, d, causal, seed, f16)
+        peak = FP16_PEAK_TFLOPS if f16 else FP32_PEAK_TFLOPS
         tf = fl / (ms_p * 1e-3) / 1e12
+        kernels = {}
+        for kname, kt, kf in zip(("qkv_gemm", "attention", "wo_gemm"), kms, kfl):
+            ktf = kf / (kt * 1e-3) / 1e12
+            kernels[kname] = {"us": round(kt * 1e3, 2), "alg_flop": kf, "TFLOP_s": round(ktf, 1),
+                              "frac": round(ktf / peak, 4)}
         out[key] = {"us_per_step": round(ms_p * 1e3, 2), "TFLOP_s": round(tf, 1), "alg_flop": fl,
-                    "mfma_frac": round(tf / FP16_PEAK_TFLOPS, 4)}
-        log(f"  {ms_p * 1e3:.1f} us/step {tf:.1f} TFLOP/s")
+                    "mfma_frac": round(tf / peak, 4),
+                    "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": peak, "unit": "TFLOP/s",
+                                 "frac": round(tf / peak, 4), "dtype": "f16" if f16 else "f32",
+                                 "kernel_sum_us": round(sum(kms) * 1e3, 2), "kernels": kernels}}
+        log(f"  {ms_p * 1e3:.1f} us/step {tf:.1f} TFLOP/s; kernels " +
+            ", ".join(f"{k} {v['us']} us ({v['frac']:.3f})" for k, v in kernels.items()))
     return out
 
 
@@ -435,6 +537,9 @@ def main() -> int:
     if not args.no_cpu:
         log("cpu baseline")
         cpu = cpu_baseline_decode(args.cpu_budget)
+        if not args.only_core:
+            log("cpu baseline, configs 1, 3, 4, 5")
+            extra["cpu_baseline_configs"] = cpu_baseline_configs(args.cpu_budget)
 
     out = {
         "metric": METRIC,

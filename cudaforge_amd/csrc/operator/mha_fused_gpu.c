@@ -16,11 +16,19 @@
 #include "gpu_ops.h"
 #include "op_common.h"
 #include "../kernels/kernels.h"
+#include "op_timing.h"
 
 #include <string.h>
 
-static int fused_op(int elem, const void* inputs[], void* outputs[],
-                    const operator_params_t* params, stream_t* stream) {
+/* The three launches of one call, planned: QKV GEMM, attention, output GEMM. */
+typedef struct {
+    cf_gemm_args_t  qkv;
+    cf_flash_args_t attn;
+    cf_gemm_args_t  wo;
+} fused_plan_t;
+
+static int fused_plan(int elem, const void* inputs[], void* outputs[], const operator_params_t* params,
+                      void* st, fused_plan_t* pl) {
     if (!inputs || !inputs[0] || !outputs || !outputs[0] || !params) return -1;
     if (!inputs[2] || !inputs[4] || !inputs[6] || !inputs[8]) return -1;
     const mha_fused_params_t* p = (const mha_fused_params_t*)params;
@@ -31,7 +39,6 @@ static int fused_op(int elem, const void* inputs[], void* outputs[],
     if (B > 65535 || H > 65535 || B * S > (1LL << 31) - 1 || D > (1 << 20)) return -1;
     const size_t esz = elem == CF_ELEM_F16 ? 2 : 4;
     const int64_t kvd = H_kv * d;
-    void* st = cf_stream_of(stream);
 
     size_t cur = 0;
     const size_t off_q = cf_ws_take(&cur, (size_t)(B * S * D) * esz);
@@ -41,48 +48,88 @@ static int fused_op(int elem, const void* inputs[], void* outputs[],
     char* data = (char*)gpu_workspace_get_stream(st, cur);
     if (!data) return -1;
 
-    cf_gemm_args_t g;
-    memset(&g, 0, sizeof(g));
-    g.a = inputs[0];
-    g.M = (int32_t)(B * S);
-    g.K = (int32_t)D;
-    g.nseg = 3;
-    g.w[0] = inputs[2]; g.bias[0] = inputs[3]; g.n[0] = (int32_t)D;
-    g.w[1] = inputs[4]; g.bias[1] = inputs[5]; g.n[1] = (int32_t)kvd;
-    g.w[2] = inputs[6]; g.bias[2] = inputs[7]; g.n[2] = (int32_t)kvd;
-    g.out_kind = CF_GEMM_OUT_QKV;
-    g.out[0] = data + off_q;
-    g.out[1] = data + off_k;
-    g.out[2] = data + off_v;
-    g.B = (int32_t)B; g.S = (int32_t)S; g.H_q = (int32_t)H; g.H_kv = (int32_t)H_kv; g.d = (int32_t)d;
-    g.elem = elem;
-    int rc = cf_launch_gemm(&g, st);
-    if (rc != 0) return rc;
+    memset(pl, 0, sizeof(*pl));
+    cf_gemm_args_t* g = &pl->qkv;
+    g->a = inputs[0];
+    g->M = (int32_t)(B * S);
+    g->K = (int32_t)D;
+    g->nseg = 3;
+    g->w[0] = inputs[2]; g->bias[0] = inputs[3]; g->n[0] = (int32_t)D;
+    g->w[1] = inputs[4]; g->bias[1] = inputs[5]; g->n[1] = (int32_t)kvd;
+    g->w[2] = inputs[6]; g->bias[2] = inputs[7]; g->n[2] = (int32_t)kvd;
+    g->out_kind = CF_GEMM_OUT_QKV;
+    g->out[0] = data + off_q;
+    g->out[1] = data + off_k;
+    g->out[2] = data + off_v;
+    g->B = (int32_t)B; g->S = (int32_t)S; g->H_q = (int32_t)H; g->H_kv = (int32_t)H_kv; g->d = (int32_t)d;
+    g->elem = elem;
 
-    cf_flash_args_t f;
-    memset(&f, 0, sizeof(f));
-    f.q = data + off_q;
-    f.k = data + off_k;
-    f.vt = data + off_v;
-    f.o = data + off_o;
-    f.B = (int32_t)B; f.S = (int32_t)S; f.H_q = (int32_t)H; f.H_kv = (int32_t)H_kv; f.d = (int32_t)d;
-    f.scale = p->scale;
-    f.causal = p->causal ? 1 : 0;
-    f.elem = elem;
-    if ((rc = cf_launch_flash_attn(&f, st)) != 0) return rc;
+    cf_flash_args_t* f = &pl->attn;
+    f->q = data + off_q;
+    f->k = data + off_k;
+    f->vt = data + off_v;
+    f->o = data + off_o;
+    f->B = (int32_t)B; f->S = (int32_t)S; f->H_q = (int32_t)H; f->H_kv = (int32_t)H_kv; f->d = (int32_t)d;
+    f->scale = p->scale;
+    f->causal = p->causal ? 1 : 0;
+    f->elem = elem;
 
-    cf_gemm_args_t o;
-    memset(&o, 0, sizeof(o));
-    o.a = data + off_o;
-    o.M = (int32_t)(B * S);
-    o.K = (int32_t)D;
-    o.nseg = 1;
-    o.w[0] = inputs[8]; o.bias[0] = inputs[9]; o.n[0] = (int32_t)D;
-    o.out_kind = CF_GEMM_OUT_ROWMAJOR;
-    o.out[0] = outputs[0];
-    o.residual = (p->has_residual && inputs[1]) ? inputs[1] : NULL;
-    o.elem = elem;
-    return cf_launch_gemm(&o, st);
+    cf_gemm_args_t* o = &pl->wo;
+    o->a = data + off_o;
+    o->M = (int32_t)(B * S);
+    o->K = (int32_t)D;
+    o->nseg = 1;
+    o->w[0] = inputs[8]; o->bias[0] = inputs[9]; o->n[0] = (int32_t)D;
+    o->out_kind = CF_GEMM_OUT_ROWMAJOR;
+    o->out[0] = outputs[0];
+    o->residual = (p->has_residual && inputs[1]) ? inputs[1] : NULL;
+    o->elem = elem;
+    return 0;
+}
+
+static int fused_launch(const fused_plan_t* pl, int which, void* st) {
+    switch (which) {
+        case 0: return cf_launch_gemm(&pl->qkv, st);
+        case 1: return cf_launch_flash_attn(&pl->attn, st);
+        default: return cf_launch_gemm(&pl->wo, st);
+    }
+}
+
+static int fused_op(int elem, const void* inputs[], void* outputs[],
+                    const operator_params_t* params, stream_t* stream) {
+    void* st = cf_stream_of(stream);
+    fused_plan_t pl;
+    int rc = fused_plan(elem, inputs, outputs, params, st, &pl);
+    for (int k = 0; k < 3 && rc == 0; k++) rc = fused_launch(&pl, k, st);
+    return rc;
+}
+
+int mha_fused_kernel_times(const void* inputs[], void* outputs[], const operator_params_t* params,
+                           stream_t* stream, int elem_f16, int warmup, int iters, float ms[3]) {
+    if (!ms || iters <= 0 || iters > 4096 || warmup < 0) return -1;
+    void* st = cf_stream_of(stream);
+    fused_plan_t pl;
+    int rc = fused_plan(elem_f16 ? CF_ELEM_F16 : CF_ELEM_F32, inputs, outputs, params, st, &pl);
+    for (int i = 0; i < warmup && rc == 0; i++)
+        for (int k = 0; k < 3 && rc == 0; k++) rc = fused_launch(&pl, k, st);
+    gpu_event_t ev[4] = {NULL, NULL, NULL, NULL};
+    for (int i = 0; i < 4 && rc == 0; i++) rc = gpu_event_create(&ev[i]);
+    if (rc == 0) rc = gpu_stream_synchronize(st);
+    /* Each kernel `iters` times back to back between two events (its inputs are those
+     * the previous kernel left, as in a call). */
+    if (rc == 0) rc = gpu_event_record(ev[0], st);
+    for (int k = 0; k < 3 && rc == 0; k++) {
+        for (int i = 0; i < iters && rc == 0; i++) rc = fused_launch(&pl, k, st);
+        if (rc == 0) rc = gpu_event_record(ev[k + 1], st);
+    }
+    if (rc == 0) rc = gpu_event_synchronize(ev[3]);
+    for (int k = 0; k < 3 && rc == 0; k++) {
+        float t = 0.0f;
+        rc = gpu_event_elapsed_ms(&t, ev[k], ev[k + 1]);
+        ms[k] = t / (float)iters;
+    }
+    for (int i = 0; i < 4; i++) if (ev[i]) gpu_event_destroy(ev[i]);
+    return rc;
 }
 
 int mha_fused_f32_cuda(const void* inputs[], void* outputs[],

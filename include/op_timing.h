@@ -44,6 +44,13 @@ int mha_decode_attn_kernel_times(const void* const* input_sets, int n_inputs, in
                                  stream_t* stream, int elem_f16, int warmup, int iters,
                                  float* ms_split, float* ms_merge);
 
+/* MHA_Fused (mha_fused_{f16,f32}_cuda, inputs and params as for that entry): after
+ * `warmup` full calls, each of its three kernels (QKV projection, attention, output
+ * projection) is launched `iters` times (<= 4096) back to back between two HIP events;
+ * ms[0..2] receive the mean time per launch of each. */
+int mha_fused_kernel_times(const void* inputs[], void* outputs[], const operator_params_t* params,
+                           stream_t* stream, int elem_f16, int warmup, int iters, float ms[3]);
+
 #ifdef __cplusplus
 }
 #endif
