@@ -22,8 +22,9 @@
 // of this kernel are issued heaviest-first; the DMA kernel below pairs each causal query
 // block with its mirror so every workgroup has the same work.
 //
-// Generic path (fp32, or other head sizes): one thread per query, online softmax in
-// fp32 with Q and the accumulator in LDS.
+// fp32 path (d = 64 or 128): the same structure on v_mfma_f32_16x16x4_f32, see flash_f32.
+// Generic path (other head sizes): one thread per query, online softmax in fp32 with Q
+// and the accumulator in LDS.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -518,6 +519,202 @@ void flash_f16_dma64(cf_flash_args_t a) {
     }
 }
 
+// ---- fp32 (the FP32 operator's attention), d = 64 or 128: true fp32 on the matrix
+// cores, v_mfma_f32_16x16x4_f32 (the reference FP32 path's bound is 1e-4, which fp16 or
+// reduced-precision operands would not meet).  A workgroup owns 4 waves x 16*NJ queries;
+// 64-key blocks of K ([key][dim]) and V^T ([dim][key]) go through a two-stage LDS ring,
+// the next block loaded into registers while the current one is used.
+// S^T = K.Q^T per 16-key tile: in MFMA step s, k-slot j (lane group l/16) stands for
+// dim (D/4)*j + s, so a lane's K operand for all D/4 steps is one contiguous run of its
+// key row (ds_read_b128), and Q^T stays in registers in the same order.  The result
+// gives lane l scores of keys 4*(l/16) + e (e = 0..3) of query l%16; in P.V step kk the
+// lane's own score e = kk is its B operand, which makes k-slot j stand for key
+// 4j + kk, so the V^T operand of all four steps is one ds_read_b128 of its dim row.
+// Online softmax in fp32 (exp2 of the scaled score minus the running max).
+constexpr int kQB32 = 64;         // queries per workgroup per 16-query column block
+template <int D, int NJ>
+__global__ __launch_bounds__(kThreads, 2)
+void flash_f32(cf_flash_args_t a) {
+    constexpr int LDK = D + 4;        // floats per K row in LDS
+    constexpr int LDV = kKB + 4;      // floats per V^T row in LDS
+    constexpr int NS = D / 4;         // MFMA steps of S^T per 16-key tile
+    constexpr int UT = D / 16;        // 16-dim tiles of O^T
+    constexpr int K_ST = kKB * LDK, V_ST = D * LDV;
+    constexpr int KCH = kKB * D / 4 / kThreads;   // float4 K chunks per thread per block
+    constexpr int VCH = D * kKB / 4 / kThreads;   // float4 V^T chunks per thread per block
+    constexpr int QB = kQB32 * NJ;                // queries per workgroup
+    __shared__ __attribute__((aligned(16))) float smem[2 * (K_ST + V_ST)];
+
+    const int nqb = (a.S + QB - 1) / QB;
+    const int qi = blockIdx.x;
+    const int qb = a.causal ? (nqb - 1 - qi) : qi;     // causal: heaviest blocks first
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int S = a.S;
+    const int kvh = h / (a.H_q / a.H_kv);
+    const int q0 = qb * QB;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 15, lq = lane >> 4;
+    const int qw = q0 + 16 * NJ * wave;            // first query of this wave
+
+    const float* __restrict__ qp = (const float*)a.q + (((size_t)b * a.H_q + h) * S) * D;
+    const float* __restrict__ kp = (const float*)a.k + (((size_t)b * a.H_kv + kvh) * S) * D;
+    const float* __restrict__ vp = (const float*)a.vt + (((size_t)b * a.H_kv + kvh) * D) * (size_t)S;
+
+    int query[NJ];
+    float qf[NJ][NS];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        query[j] = qw + 16 * j + lr;
+#pragma unroll
+        for (int v = 0; v < NS / 4; v++) {
+            const f4_t x = query[j] < S ? *(const f4_t*)(qp + (size_t)query[j] * D + NS * lq + 4 * v) : f4_t{};
+#pragma unroll
+            for (int e = 0; e < 4; e++) qf[j][4 * v + e] = x[e];
+        }
+    }
+
+    const float c = a.scale * kLog2e;
+    float m_run[NJ], l_run[NJ];
+    f4_t acc[NJ][UT];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        m_run[j] = -INFINITY;
+        l_run[j] = 0.0f;
+#pragma unroll
+        for (int u = 0; u < UT; u++) acc[j][u] = f4_t{0.f, 0.f, 0.f, 0.f};
+    }
+
+    const int k_end = a.causal ? min(S, q0 + QB) : S;
+    const bool v_vec = (S % 4) == 0;
+    f4_t rk[KCH], rv[VCH];
+    auto load_block = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < KCH; i++) {
+            const int ch = tid + i * kThreads;
+            const int r = ch / (D / 4), cc = (ch % (D / 4)) * 4;
+            rk[i] = k0 + r < S ? *(const f4_t*)(kp + (size_t)(k0 + r) * D + cc) : f4_t{};
+        }
+#pragma unroll
+        for (int i = 0; i < VCH; i++) {
+            const int ch = tid + i * kThreads;
+            const int dm = ch / (kKB / 4), kc = (ch % (kKB / 4)) * 4;
+            const float* src = vp + (size_t)dm * S + k0 + kc;
+            f4_t v{};
+            if (v_vec && k0 + kc + 4 <= S) v = *(const f4_t*)src;
+            else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) if (k0 + kc + e < S) v[e] = src[e];
+            }
+            rv[i] = v;
+        }
+    };
+    auto store_block = [&](int stage) {
+        float* Ks = smem + stage * (K_ST + V_ST);
+        float* Vs = Ks + K_ST;
+#pragma unroll
+        for (int i = 0; i < KCH; i++) {
+            const int ch = tid + i * kThreads;
+            *(f4_t*)&Ks[(ch / (D / 4)) * LDK + (ch % (D / 4)) * 4] = rk[i];
+        }
+#pragma unroll
+        for (int i = 0; i < VCH; i++) {
+            const int ch = tid + i * kThreads;
+            *(f4_t*)&Vs[(ch / (kKB / 4)) * LDV + (ch % (kKB / 4)) * 4] = rv[i];
+        }
+    };
+
+    const int nblk = (k_end + kKB - 1) / kKB;
+    load_block(0);
+    store_block(0);
+    __syncthreads();
+    for (int bi = 0; bi < nblk; bi++) {
+        const int k0 = bi * kKB;
+        if (bi + 1 < nblk) load_block(k0 + kKB);
+        const float* Ks = smem + (bi & 1) * (K_ST + V_ST);
+        const float* Vs = Ks + K_ST;
+
+        // st[j][t][e] = score(key k0 + 16t + 4*lq + e, query[j]).
+        f4_t st[NJ][4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+#pragma unroll
+            for (int j = 0; j < NJ; j++) st[j][t] = f4_t{0.f, 0.f, 0.f, 0.f};
+            const float* kr = &Ks[(16 * t + lr) * LDK + NS * lq];
+#pragma unroll
+            for (int v = 0; v < NS / 4; v++) {
+                const f4_t kf = *(const f4_t*)(kr + 4 * v);
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+#pragma unroll
+                    for (int j = 0; j < NJ; j++)
+                        st[j][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[e], qf[j][4 * v + e], st[j][t], 0, 0, 0);
+            }
+        }
+        const bool edge = (k0 + kKB > S) || (a.causal && k0 + kKB - 1 > qw);
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            if (edge) {
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const int key = k0 + 16 * t + 4 * lq + e;
+                        if (key >= S || (a.causal && key > query[j])) st[j][t][e] = -INFINITY;
+                    }
+            }
+            float mloc = st[j][0][0];
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) mloc = fmaxf(mloc, st[j][t][e]);
+            mloc = max_xor16(mloc);
+            mloc = max_xor32(mloc);
+            // Raw dot products; the scale folds into the exponent: p = 2^(s*c - m).
+            const float m_new = fmaxf(m_run[j], mloc * c);
+            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+            const float alpha = exp2f(m_run[j] - m_use);
+            m_run[j] = m_new;
+            float psum = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float pv = exp2f(__builtin_fmaf(st[j][t][e], c, -m_use));
+                    st[j][t][e] = pv;
+                    psum += pv;
+                }
+            l_run[j] = l_run[j] * alpha + psum;
+#pragma unroll
+            for (int u = 0; u < UT; u++) acc[j][u] *= alpha;
+        }
+        // O^T[16u + 4*lq + e][query] += V^T . P^T; step kk of key tile t: k-slot lq is
+        // key k0 + 16t + 4*lq + kk.
+#pragma unroll
+        for (int u = 0; u < UT; u++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const f4_t vf = *(const f4_t*)&Vs[(16 * u + lr) * LDV + 16 * t + 4 * lq];
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+                    for (int j = 0; j < NJ; j++)
+                        acc[j][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[kk], st[j][t][kk], acc[j][u], 0, 0, 0);
+            }
+        if (bi + 1 < nblk) store_block((bi + 1) & 1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const float l_tot = add_xor32(add_xor16(l_run[j]));
+        if (query[j] < S) {
+            const float inv = 1.0f / l_tot;
+            float* op = (float*)a.o + (((size_t)b * S + query[j]) * a.H_q + h) * D;
+#pragma unroll
+            for (int u = 0; u < UT; u++) *(f4_t*)(op + 16 * u + 4 * lq) = acc[j][u] * inv;
+        }
+    }
+}
+
 __device__ __forceinline__ float to_f(float x) { return x; }
 __device__ __forceinline__ float to_f(_Float16 x) { return (float)x; }
 template <typename T> __device__ __forceinline__ T from_f(float x) { return (T)x; }
@@ -605,6 +802,20 @@ extern "C" int cf_launch_flash_attn(const cf_flash_args_t* a, void* stream) {
             else hipLaunchKernelGGL(flash_f16_dma64<2>, grid2, dim3(kThreads), 0, s, *a);
         } else if (a->d == 64) hipLaunchKernelGGL(flash_f16<64>, grid, dim3(kThreads), 0, s, *a);
         else hipLaunchKernelGGL(flash_f16<128>, grid, dim3(kThreads), 0, s, *a);
+        return (int)hipGetLastError();
+    }
+    if (a->elem == CF_ELEM_F32 && aligned && (a->d == 64 || a->d == 128) && a->scale > 0.0f) {
+        // 32 queries per wave where that still gives two workgroups per CU, else 16.
+        const long long bh = (long long)a->B * a->H_q;
+        const int nj = bh * ((a->S + 2 * kQB32 - 1) / (2 * kQB32)) >= 2LL * cu_count() ? 2 : 1;
+        dim3 grid((unsigned)((a->S + nj * kQB32 - 1) / (nj * kQB32)), (unsigned)a->H_q, (unsigned)a->B);
+        if (a->d == 64) {
+            if (nj == 2) hipLaunchKernelGGL((flash_f32<64, 2>), grid, dim3(kThreads), 0, s, *a);
+            else hipLaunchKernelGGL((flash_f32<64, 1>), grid, dim3(kThreads), 0, s, *a);
+        } else {
+            if (nj == 2) hipLaunchKernelGGL((flash_f32<128, 2>), grid, dim3(kThreads), 0, s, *a);
+            else hipLaunchKernelGGL((flash_f32<128, 1>), grid, dim3(kThreads), 0, s, *a);
+        }
         return (int)hipGetLastError();
     }
     if (a->d > 240) return (int)hipErrorInvalidValue;

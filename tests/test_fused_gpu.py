@@ -94,6 +94,18 @@ def test_config5_causal_full_size_row(gpu):
     assert max_abs(sub.oracle(), got[2:3]) <= TOL16
 
 
+@pytest.mark.parametrize("B,S,H,d,causal", [(8, 512, 12, 64, False), (4, 1024, 16, 64, True)])
+def test_fp32_full_size_configs(gpu, B, S, H, d, causal):
+    """Configs 3 and 5's shapes through the FP32 entry (fp32 MFMA GEMMs and attention;
+    the second shape takes the attention kernel's 32-query waves): every row against a
+    float64 evaluation of the same math, within the FP32 bound."""
+    from helpers import fused_ref64
+    c = FusedCase(B, S, H, H, d, seed=70 + S, f16=False, causal=causal, residual=True, bias_std=0.02)
+    got = run_fused_gpu(c)
+    per_row = np.abs(fused_ref64(c) - got).max(axis=2)
+    assert (per_row <= TOL32).all(), per_row.max()
+
+
 def test_residual_flag_with_null_residual(gpu):
     """has_residual with a NULL residual slot adds nothing (the reference's `R != NULL`
     guard, mha_fused.c:165-170)."""
