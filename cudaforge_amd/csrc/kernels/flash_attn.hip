@@ -533,7 +533,7 @@ void flash_f16_dma64(cf_flash_args_t a) {
 // Online softmax in fp32 (exp2 of the scaled score minus the running max).
 constexpr int kQB32 = 64;         // queries per workgroup per 16-query column block
 template <int D, int NJ>
-__global__ __launch_bounds__(kThreads, 2)
+__global__ __launch_bounds__(kThreads, D == 64 ? 2 : 1)   // d = 128: 134 KB of LDS, one per CU
 void flash_f32(cf_flash_args_t a) {
     constexpr int LDK = D + 4;        // floats per K row in LDS
     constexpr int LDV = kKB + 4;      // floats per V^T row in LDS

@@ -184,6 +184,10 @@ void cf_flash_set_mode(int32_t mode);
 /* CausalMask (S, S) float on the device. */
 int cf_launch_causal_mask(float* mask, int64_t S, void* stream);
 
+/* Copies `bytes` bytes with a kernel (either end may be pinned host memory, which the
+ * device reads and writes directly): small stream-ordered transfers between kernels. */
+int cf_launch_copy_bytes(void* dst, const void* src, size_t bytes, void* stream);
+
 /* v[0..n) = value (add = 0) or += value (add = 1), as a kernel (graph decode lengths). */
 int cf_launch_i32_update(int32_t* v, int32_t n, int32_t value, int32_t add, void* stream);
 

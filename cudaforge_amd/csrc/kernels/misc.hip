@@ -25,7 +25,35 @@ __global__ void i32_update_kernel(int32_t* __restrict__ v, int32_t n, int32_t va
     if (i < n) v[i] = add ? v[i] + value : value;
 }
 
+// Byte copy by the compute units, 16 bytes per lane where both ends allow: for small
+// transfers between pinned host memory (mapped, device-accessible) and device memory
+// that sit between kernels on one stream, where a DMA-engine copy would add the
+// engines' hand-over latency on both sides.
+__global__ void copy_bytes_kernel(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, size_t n, int vec) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (vec) {
+        const size_t n16 = n / 16;
+        for (size_t k = i; k < n16; k += stride) ((uint4*)dst)[k] = ((const uint4*)src)[k];
+        for (size_t k = n16 * 16 + i; k < n; k += stride) dst[k] = src[k];
+    } else {
+        for (size_t k = i; k < n; k += stride) dst[k] = src[k];
+    }
+}
+
 }  // namespace
+
+extern "C" int cf_launch_copy_bytes(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return 0;
+    if (!dst || !src) return (int)hipErrorInvalidValue;
+    const int vec = (((uintptr_t)dst | (uintptr_t)src) % 16) == 0;
+    size_t blocks = (bytes / (vec ? 16 : 1) + 255) / 256;
+    if (blocks > 1024) blocks = 1024;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(copy_bytes_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, (uint8_t*)dst,
+                       (const uint8_t*)src, bytes, vec);
+    return (int)hipGetLastError();
+}
 
 extern "C" int cf_launch_i32_update(int32_t* v, int32_t n, int32_t value, int32_t add, void* stream) {
     if (!v || n <= 0) return (int)hipErrorInvalidValue;

@@ -108,6 +108,8 @@ typedef struct {
     uint64_t        replay_generation; /* gpu_buffer_generation() when hip_graph_exec was recorded */
     void*           decode_lens;     /* per node: device-held lengths of uniform decode nodes */
     int             decode_lens_cap; /* entries in decode_lens */
+    void*           pinned;          /* per tensor: pinned host staging of graph inputs/outputs */
+    int             pinned_cap;      /* entries in pinned */
 } inference_graph_t;
 
 inference_graph_t* graph_create(void);
