@@ -66,6 +66,40 @@ __device__ __forceinline__ float* partial_at(const cf_decode_attn_args_t& a, int
     return a.partials + ((size_t)unit * a.n_split + split) * (size_t)part_stride(Gx, D);
 }
 
+// Balanced ragged split (a.balanced, grouped fp16 kernel): the attended positions of all
+// sequences laid end to end (W in all) are cut into n_split equal ranges of R positions
+// (a multiple of 16), one per workgroup.  Sequence b (starting at P_b) spans ranges
+// P_b / R .. (P_b + T_b - 1) / R, one split each; its partial records are numbered
+// after those of sequences 0 .. b-1, record (piece, kv head) at piece * H_kv + kv head.
+struct BalancedGeom { int W, R; };
+__device__ __forceinline__ BalancedGeom balanced_geom(const cf_decode_attn_args_t& a) {
+    int W = 0;
+    for (int b = 0; b < a.B; b++) W += attended(a, b);
+    int R = (W + a.n_split - 1) / a.n_split;
+    R = (R + 15) / 16 * 16;
+    return {W, R};
+}
+
+// The splits of (b, unit): their count and where split s's record is (first + s * step
+// records of `stride` floats).
+struct SplitRecords { int n; const float* first; size_t step; };
+__device__ __forceinline__ SplitRecords split_records(const cf_decode_attn_args_t& a, int b, int unit,
+                                                      int units_per_b, int stride) {
+    if (!a.balanced) {
+        const int T_b = attended(a, b);
+        return {(T_b + a.chunk - 1) / a.chunk, a.partials + (size_t)unit * a.n_split * stride, (size_t)stride};
+    }
+    const BalancedGeom geo = balanced_geom(a);
+    int P = 0, pieces = 0, ns = 1;
+    for (int bb = 0; bb <= b; bb++) {
+        const int T = attended(a, bb);
+        ns = (P + T - 1) / geo.R - P / geo.R + 1;
+        if (bb < b) pieces += ns;
+        P += T;
+    }
+    return {ns, a.partials + ((size_t)pieces * a.H_kv + unit % units_per_b) * stride, (size_t)a.H_kv * stride};
+}
+
 // ------------------------------------------------------------------ fp16 split ---
 // One wave streams `chunk` positions of one (b, kv head) for its whole GQA group, in
 // blocks of 32 positions.  K and V rows go straight from HBM into an NS-stage LDS ring
@@ -94,9 +128,11 @@ __device__ __forceinline__ int vswz(int row) { return 2 * ((row / (128 / D)) % (
 // config-2 layout reads 6.1 TB/s this way against 5.5-5.9 TB/s with one workgroup per
 // (split, KV head).  With 16 positions per block, P.V runs on v_mfma_f32_16x16x16_f16,
 // whose B operand is exactly the four probabilities a score lane holds.
-template <int D, int G, int NS, bool WIDE = false>
-__global__ __launch_bounds__(WIDE ? 512 : 64)
-void split_f16(cf_decode_attn_args_t a) {
+// Positions [t0, t1) of (b, kv head kvh) through one wave's ring: the partial goes to
+// `part`, or, when part is null (the range is the whole sequence), O itself.
+template <int D, int G, int NS, bool WIDE>
+__device__ __forceinline__ void split_range(const cf_decode_attn_args_t& a, _Float16* ring, int b, int kvh,
+                                            int t0, int t1, float* part) {
     constexpr int KT = D / 32;          // 32-dim MFMA steps per 16 positions
     constexpr int BP = WIDE ? 16 : 32;  // positions per block
     constexpr int NH = BP / 16;         // 16-position row blocks per block
@@ -109,20 +145,9 @@ void split_f16(cf_decode_attn_args_t a) {
     constexpr int HDR = part_hdr(G);
     static_assert((NS - 1) * NL < 64, "vmcnt range");
     constexpr int QH = (G * D * 2 + 1023) / 1024 * 512;   // halves of the Q area (whole DMA KBs)
-    constexpr int WAVE_LDS = NS * 2 * TILE + QH;          // halves of one wave's ring + Q area
-    __shared__ __attribute__((aligned(16))) _Float16 ring_all[(WIDE ? 8 : 1) * WAVE_LDS];
-
-    const int split = blockIdx.x;
-    const int kvh = WIDE ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : (int)blockIdx.y;   // wave-uniform
-    const int b = WIDE ? (int)blockIdx.y : (int)blockIdx.z;
-    _Float16* ring = ring_all + (WIDE ? kvh * WAVE_LDS : 0);
-    const int T_b = attended(a, b);
-    const int t0 = split * a.chunk;
-    if (t0 >= T_b) return;
-    const int t1 = min(t0 + a.chunk, T_b);
     const int nblk = (t1 - t0 + BP - 1) / BP;
-    const int nsplit_b = (T_b + a.chunk - 1) / a.chunk;
     const int lane = threadIdx.x & 63, lr = lane & 15, lq = lane >> 4;
+    wait_lds_reads();                                     // a previous range's reads of the ring
 
     const size_t row_stride = (size_t)a.H_kv * D;
     const size_t unit_off = ((size_t)b * a.max_seq * a.H_kv + kvh) * D;
@@ -299,7 +324,7 @@ void split_f16(cf_decode_attn_args_t a) {
     l_run = add_xor32(add_xor16(l_run));
     if (lr >= G) return;
     // Lane (lr, lq) holds O^T rows d = 16n + 4lq + i of head h0 + lr.
-    if (nsplit_b == 1) {
+    if (!part) {
         const float inv = 1.0f / l_run;
         _Float16* out = (_Float16*)a.o + ((size_t)b * a.H_q + h0 + lr) * D + 4 * lq;
 #pragma unroll
@@ -311,13 +336,54 @@ void split_f16(cf_decode_attn_args_t a) {
         }
         return;
     }
-    float* part = partial_at(a, b * a.H_kv + kvh, split, G, D);
 #pragma unroll
     for (int n = 0; n < NT; n++) *(f4_t*)(part + HDR + lr * D + 16 * n + 4 * lq) = acc[n];
     if (lq == 0) {
         part[lr] = m_run;
         part[G + lr] = l_run;
     }
+}
+
+template <int D, int G, int NS, bool WIDE = false>
+__global__ __launch_bounds__(WIDE ? 512 : 64)
+void split_f16(cf_decode_attn_args_t a) {
+    constexpr int BP = WIDE ? 16 : 32;
+    constexpr int TILE = BP * D;
+    constexpr int QH = (G * D * 2 + 1023) / 1024 * 512;
+    constexpr int WAVE_LDS = NS * 2 * TILE + QH;          // halves of one wave's ring + Q area
+    __shared__ __attribute__((aligned(16))) _Float16 ring_all[(WIDE ? 8 : 1) * WAVE_LDS];
+    const int kvh = WIDE ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : (int)blockIdx.y;   // wave-uniform
+    _Float16* ring = ring_all + (WIDE ? kvh * WAVE_LDS : 0);
+    if constexpr (WIDE) {
+        if (a.balanced) {
+            // Ragged lengths: workgroup g takes positions [gR, gR + R) of the batch's
+            // attended positions laid end to end, one piece per sequence it overlaps.
+            const BalancedGeom geo = balanced_geom(a);
+            const int lo = (int)blockIdx.x * geo.R, hi = min(lo + geo.R, geo.W);
+            int P = 0, pieces = 0;
+            for (int b = 0; b < a.B && P < hi; b++) {
+                const int T = attended(a, b);
+                const int first = P / geo.R, ns = (P + T - 1) / geo.R - first + 1;
+                if (P + T > lo) {
+                    float* part = ns == 1 ? nullptr
+                                          : a.partials + ((size_t)(pieces + (int)blockIdx.x - first) * a.H_kv + kvh) *
+                                                             part_stride(G, D);
+                    split_range<D, G, NS, WIDE>(a, ring, b, kvh, max(lo - P, 0), min(hi - P, T), part);
+                }
+                P += T;
+                pieces += ns;
+            }
+            return;
+        }
+    }
+    const int split = blockIdx.x;
+    const int b = WIDE ? (int)blockIdx.y : (int)blockIdx.z;
+    const int T_b = attended(a, b);
+    const int t0 = split * a.chunk;
+    if (t0 >= T_b) return;
+    const int nsplit_b = (T_b + a.chunk - 1) / a.chunk;
+    split_range<D, G, NS, WIDE>(a, ring, b, kvh, t0, min(t0 + a.chunk, T_b),
+                                nsplit_b == 1 ? nullptr : partial_at(a, b * a.H_kv + kvh, split, G, D));
 }
 
 // ------------------------------------------------------------------ fp32 split ---
@@ -572,19 +638,18 @@ void merge_kernel(cf_decode_attn_args_t a, int Gx, int units_per_b) {
     const int g = (int)(ug % Gx);
     const int unit = (int)(ug / Gx);
     const int b = unit / units_per_b;
-    const int T_b = attended(a, b);
-    const int nsplit = (T_b + a.chunk - 1) / a.chunk;
-    if (nsplit <= 1) return;                       // finished by the split kernel
     const int stride = part_stride(Gx, D), hdr = part_hdr(Gx);
-    const float* part = a.partials + (size_t)unit * a.n_split * stride;
+    const SplitRecords sr = split_records(a, b, unit, units_per_b, stride);
+    const int nsplit = sr.n;
+    if (nsplit <= 1) return;                       // finished by the split kernel
     constexpr int NB = 16;
     float M = -INFINITY, num = 0.0f, den = 0.0f;
     for (int s0 = 0; s0 < nsplit; s0 += NB) {
         float mv[NB], lv[NB], av[NB];
 #pragma unroll
         for (int j = 0; j < NB; j++) {
-            const float* ps = part + (size_t)(s0 + j) * stride;
             const bool ok = s0 + j < nsplit;
+            const float* ps = sr.first + (size_t)(ok ? s0 + j : 0) * sr.step;
             mv[j] = ok ? ps[g] : -INFINITY;
             lv[j] = ok ? ps[Gx + g] : 0.0f;
             av[j] = ok ? ps[hdr + g * D + i] : 0.0f;
@@ -617,8 +682,9 @@ void merge_rows(cf_decode_attn_args_t a, int Gx, int units_per_b) {
     const int D = a.d, DV = D >> 2, SG = kMergeThreads / DV;
     const int row = blockIdx.x;
     const int g = row % Gx, unit = row / Gx, b = unit / units_per_b;
-    const int T_b = attended(a, b);
-    const int nsplit = (T_b + a.chunk - 1) / a.chunk;
+    const int stride = part_stride(Gx, D), hdr = part_hdr(Gx);
+    const SplitRecords sr = split_records(a, b, unit, units_per_b, stride);
+    const int nsplit = sr.n;
     if (nsplit <= 1) return;                       // finished by the split kernel
     const int tid = threadIdx.x, col = tid % DV, sg = tid / DV;
     __shared__ float sm[kMergeThreads], sd[kMergeThreads];
@@ -626,8 +692,6 @@ void merge_rows(cf_decode_attn_args_t a, int Gx, int units_per_b) {
     float M = -INFINITY, den = 0.0f;
     f4_t num = {0.f, 0.f, 0.f, 0.f};
     if (sg < SG) {
-        const int stride = part_stride(Gx, D), hdr = part_hdr(Gx);
-        const float* part = a.partials + (size_t)unit * a.n_split * stride;
         constexpr int NB = 8;
         for (int s0 = sg; s0 < nsplit; s0 += SG * NB) {
             float mv[NB], lv[NB];
@@ -636,7 +700,7 @@ void merge_rows(cf_decode_attn_args_t a, int Gx, int units_per_b) {
             for (int j = 0; j < NB; j++) {
                 const int sp = s0 + j * SG;
                 const bool ok = sp < nsplit;
-                const float* ps = part + (size_t)(ok ? sp : 0) * stride;
+                const float* ps = sr.first + (size_t)(ok ? sp : 0) * sr.step;
                 mv[j] = ok ? ps[g] : -INFINITY;
                 lv[j] = ok ? ps[Gx + g] : 0.0f;
                 av[j] = ok ? *(const f4_t*)(ps + hdr + g * D + 4 * col) : f4_t{0.f, 0.f, 0.f, 0.f};
@@ -693,22 +757,22 @@ void merge_wave(cf_decode_attn_args_t a, int Gx, int units_per_b, int rows) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
     const int g = row % Gx, unit = row / Gx, b = unit / units_per_b;
-    const int nsplit = (attended(a, b) + a.chunk - 1) / a.chunk;
-    if (nsplit <= 1) return;                       // finished by the split kernel
     const int stride = part_stride(Gx, D), hdr = part_hdr(Gx);
-    const float* part = a.partials + (size_t)unit * a.n_split * stride;
+    const SplitRecords sr = split_records(a, b, unit, units_per_b, stride);
+    const int nsplit = sr.n;
+    if (nsplit <= 1) return;                       // finished by the split kernel
     // Every load first (one round trip): lane s < nsplit holds split s's (m, l), and each
     // lane the DPL accumulator values of every split for its dims.
     float mv = -INFINITY, lv = 0.0f;
     if (lane < nsplit) {
-        mv = part[(size_t)lane * stride + g];
-        lv = part[(size_t)lane * stride + Gx + g];
+        mv = sr.first[(size_t)lane * sr.step + g];
+        lv = sr.first[(size_t)lane * sr.step + Gx + g];
     }
     float av[MAXS][DPL];
 #pragma unroll
     for (int j = 0; j < MAXS; j++) {
         const bool ok = j < nsplit;
-        const float* ps = part + (size_t)(ok ? j : 0) * stride + hdr + g * D + DPL * lane;
+        const float* ps = sr.first + (size_t)(ok ? j : 0) * sr.step + hdr + g * D + DPL * lane;
 #pragma unroll
         for (int e = 0; e < DPL; e++) av[j][e] = ok ? ps[e] : 0.0f;
     }
@@ -776,16 +840,16 @@ int wide_lds_bytes(int d, int G) {
 // ragged lengths the grouped kernel's whole-row workgroups leave a partial last round
 // (config 4: 67 us against 64.6 us one wave per KV head).
 bool use_wide(const cf_decode_attn_args_t* a) {
-    return g_wide && a->elem == CF_ELEM_F16 && (!a->seq_lens || a->lens_uniform) && a->H_kv <= kWideMaxHeads &&
-           use_fast(a);
+    return g_wide && a->elem == CF_ELEM_F16 && (!a->seq_lens || a->lens_uniform || a->balanced) &&
+           a->H_kv <= kWideMaxHeads && use_fast(a);
 }
 
 template <int D, int G>
 hipError_t launch_split_fast(const cf_decode_attn_args_t& a, hipStream_t s) {
     dim3 grid((unsigned)a.n_split, (unsigned)a.H_kv, (unsigned)a.B);
     if (use_wide(&a)) {
-        hipLaunchKernelGGL((split_f16<D, G, kWideStages, true>), dim3((unsigned)a.n_split, (unsigned)a.B),
-                           dim3(64 * (unsigned)a.H_kv), 0, s, a);
+        const dim3 wgrid = a.balanced ? dim3((unsigned)a.n_split) : dim3((unsigned)a.n_split, (unsigned)a.B);
+        hipLaunchKernelGGL((split_f16<D, G, kWideStages, true>), wgrid, dim3(64 * (unsigned)a.H_kv), 0, s, a);
     } else if (a.elem == CF_ELEM_F16) {
         switch (f16_stages()) {
             case 2: hipLaunchKernelGGL((split_f16<D, G, 2>), grid, dim3(64), 0, s, a); break;
@@ -827,6 +891,11 @@ extern "C" int32_t cf_decode_attn_wide_wgs_per_cu(int32_t elem, int32_t d, int32
     if (!g_wide || elem != CF_ELEM_F16 || h_kv > kWideMaxHeads || !fast_supported(elem, d, group)) return 0;
     const int n = kLdsPerCu / wide_lds_bytes(d, group);
     return n < 1 ? 1 : n;
+}
+
+extern "C" int32_t cf_decode_attn_balanced_ok(int32_t elem, int32_t d, int32_t group, int32_t h_kv, int32_t B) {
+    // Every workgroup and the merge walk the B lengths to find their ranges.
+    return cf_decode_attn_wide_wgs_per_cu(elem, d, group, h_kv) > 0 && B <= 64 ? 1 : 0;
 }
 
 extern "C" int32_t cf_decode_attn_wgs_per_cu(int32_t elem, int32_t d, int32_t group) {

@@ -34,6 +34,9 @@ typedef struct {
     void*          o;
     const int32_t* seq_lens;   /* device, NULL = uniform cache_len */
     int32_t        lens_uniform; /* seq_lens all hold one value (a device-held uniform length) */
+    int32_t        balanced;   /* ragged seq_lens on the grouped fp16 kernel: n_split workgroups
+                                  share the batch's attended positions equally (chunk unused);
+                                  partial records: (n_split + B) x H_kv */
     float*         partials;   /* workspace */
     int32_t        B, H_q, H_kv, d;
     int32_t        max_seq, cache_len;
@@ -62,6 +65,9 @@ void    cf_decode_attn_set_merge_rows(int32_t on);
 /* Workspace floats needed for the partials of a launch. */
 size_t  cf_decode_attn_partials_floats(int32_t B, int32_t H_q, int32_t H_kv, int32_t d,
                                        int32_t n_split, int32_t elem);
+/* 1 when ragged lengths of this shape take the balanced grouped kernel (then n_split
+ * workgroups, as many as fit the CUs at once, share the attended positions equally). */
+int32_t cf_decode_attn_balanced_ok(int32_t elem, int32_t d, int32_t group, int32_t h_kv, int32_t B);
 /* Fixed device scratch for the split partials of the allocation-free decode entry: a
  * file-scope device array of cf_decode_attn_scratch_bytes() bytes, one per GPU.
  * cf_decode_attn_scratch_init looks up the current device's address of it once

@@ -17,6 +17,7 @@
 #include "op_common.h"
 #include "../kernels/kernels.h"
 
+#include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -101,13 +102,24 @@ int mha_decode_plan(const mha_decode_params_t* p, int elem_f16, int64_t* chunk, 
     return 0;
 }
 
-/* Fill the attention-core launch arguments; returns the workspace bytes it needs. */
-static size_t attn_args(int elem, const decode_shape_t* s, const int32_t* lens,
+/* Fill the attention-core launch arguments; returns the workspace bytes it needs.
+ * `fast_ok`: the q/k/v/o pointers are 16-byte aligned and scale > 0, which the grouped
+ * fp16 kernel needs.  Ragged lengths on that kernel split the batch's attended positions
+ * evenly over one round of workgroups (balanced mode) instead of planning chunks over
+ * max_seq, where short sequences leave most of their splits empty. */
+static size_t attn_args(int elem, const decode_shape_t* s, const int32_t* lens, int fast_ok,
                         cf_decode_attn_args_t* a) {
     memset(a, 0, sizeof(*a));
     const int64_t t_max = s->ragged ? s->max_seq : s->cache_len + 1;
     int64_t chunk, n_split;
     plan_split(elem, s, t_max, &chunk, &n_split);
+    const int G = (int)(s->H / s->H_kv);
+    if (s->ragged && !s->lens_uniform && fast_ok &&
+        cf_decode_attn_balanced_ok(elem, (int)s->d, G, (int)s->H_kv, (int)s->B)) {
+        a->balanced = 1;
+        n_split = (int64_t)cf_cu_count() * cf_decode_attn_wide_wgs_per_cu(elem, (int)s->d, G, (int)s->H_kv);
+        chunk = cf_decode_attn_chunk_quantum(elem, (int)s->d, G);   /* unused by the balanced kernel */
+    }
     a->seq_lens = lens;
     a->lens_uniform = s->lens_uniform;
     a->B = (int32_t)s->B;
@@ -119,8 +131,12 @@ static size_t attn_args(int elem, const decode_shape_t* s, const int32_t* lens,
     a->chunk = (int32_t)chunk;
     a->n_split = (int32_t)n_split;
     a->elem = elem;
+    if (a->balanced)   /* records per (piece, kv head); at most n_split + B pieces */
+        return (size_t)(a->n_split + a->B) * (size_t)a->H_q * (size_t)(a->d + 4) * sizeof(float);
     return cf_decode_attn_partials_floats(a->B, a->H_q, a->H_kv, a->d, a->n_split, elem) * sizeof(float);
 }
+
+static int aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 /* Fill the core's launch arguments.  Partials come from the stream's workspace, or,
  * when `fixed` is non-NULL, from that buffer of `fixed_bytes` bytes (no allocation);
@@ -139,7 +155,9 @@ static int attn_prepare(int elem, const void* inputs[], void* outputs[],
         lens = (const int32_t*)inputs[3];
         if (!lens) return -1;
     }
-    const size_t part_bytes = attn_args(elem, &s, lens, a);
+    const int fast_ok = aligned16(inputs[0]) && aligned16(inputs[1]) && aligned16(inputs[2]) &&
+                        aligned16(outputs[0]) && p->scale > 0.0f;
+    const size_t part_bytes = attn_args(elem, &s, lens, fast_ok, a);
     if (fixed) {
         if (part_bytes > fixed_bytes) {
             fprintf(stderr,
@@ -297,7 +315,9 @@ static int decode_op(int elem, const void* inputs[], void* outputs[],
     g1.k_split = gemv_k_split(elem, s.D, ct1, m_tiles);
 
     cf_decode_attn_args_t a;
-    const size_t attn_part = attn_args(elem, &s, lens, &a);
+    /* q and o live in the workspace (256-byte aligned). */
+    const int fast_ok = aligned16(outputs[1]) && aligned16(outputs[2]) && p->scale > 0.0f;
+    const size_t attn_part = attn_args(elem, &s, lens, fast_ok, &a);
 
     cf_gemv_args_t g2;
     memset(&g2, 0, sizeof(g2));

@@ -205,6 +205,31 @@ def test_config4_ragged_full_size(gpu):
     assert max_abs(ref, got) <= TOL16
 
 
+@pytest.mark.parametrize("lens", [[1], [1, 1, 1], [4096, 1, 17, 2999], [33] * 64, [1] * 63 + [5000],
+                                  [16, 4080, 16, 4080], [257, 4095, 1000, 3]])
+def test_balanced_ragged_partition(gpu, native, lens):
+    """Ragged fp16 lengths on the grouped kernel split the batch's attended positions
+    evenly over one round of workgroups: ranges that cut sequences anywhere (inside a
+    16-position block too), many short sequences in one range, length-1 sequences and
+    totals smaller than one position per workgroup.  Every row against float64, and
+    against the one-wave kernel (chunked splits over the capacity)."""
+    from helpers import attn_ref64_all
+    B, H_kv, G, d, cap = len(lens), 2, 4, 128, 4096
+    H = H_kv * G
+    L = np.asarray(lens, np.int32)
+    Q, K, V = (O.round_f16(O.normal(s, 510 + i)) for i, s in enumerate([(B, H, d), (B, cap, H_kv, d), (B, cap, H_kv, d)]))
+    got = run_decode_attn_gpu(Q, K, V, None, H_kv, True, seq_lens=L - 1)
+    ref = attn_ref64_all(Q, K, V, L, H_kv, float(1 / np.sqrt(d)))
+    per_row = np.abs(ref - got).reshape(B, -1).max(axis=1)
+    assert (per_row <= TOL16).all(), per_row
+    try:
+        native.cf_decode_attn_set_wide(0)
+        one_wave = run_decode_attn_gpu(Q, K, V, None, H_kv, True, seq_lens=L - 1)
+    finally:
+        native.cf_decode_attn_set_wide(1)
+    assert max_abs(one_wave, got) <= TOL16
+
+
 @pytest.mark.parametrize("f16", [True, False])
 @pytest.mark.parametrize("chunk", [0, 256])
 def test_ragged_edge_lengths(gpu, native, f16, chunk):
