@@ -153,8 +153,9 @@ def bench_decode_ragged(cf, stream, steps, warmup):
     p = cf.MhaDecodeParams(B, H * d, H, H_kv, d, float(1 / np.sqrt(d)), -1, cap)
     from cudaforge_amd.api import time_op_sets
     ms = time_op_sets("mha_decode_attn_f16_cuda", sets, [[O_]] * KV_SETS, p, stream, warmup, steps)
+    ms_split, ms_merge = kernel_times(cf, sets, [O_], p, stream, min(steps, 1000), warmup)
     alg = int(4096 * int((lens + 1).sum()) + 2 * B * H * d * 2)
-    return ms, alg, [int(x) + 1 for x in lens]
+    return ms, alg, [int(x) + 1 for x in lens], ms_split, ms_merge
 
 
 def bench_decode_graph(cf, steps, warmup, B=16, H=32, H_kv=8, d=128, T=4096, seed=700):
@@ -519,11 +520,14 @@ def main() -> int:
                                                "GB_s": round(alg_1 / (ms_1 * 1e-3) / 1e9, 1),
                                                "alg_bytes": alg_1}
         log("decode ragged, config 4")
-        ms_r, alg_r, lens = bench_decode_ragged(cf, stream, steps, warmup)
+        ms_r, alg_r, lens, ms_rs, ms_rm = bench_decode_ragged(cf, stream, steps, warmup)
         extra["decode_core_config4_ragged"] = {"us_per_step": round(ms_r * 1e3, 2),
                                                "GB_s": round(alg_r / (ms_r * 1e-3) / 1e9, 1),
                                                "alg_bytes": alg_r, "lengths": lens,
-                                               "hbm_frac": round(alg_r / (ms_r * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+                                               "hbm_frac": round(alg_r / (ms_r * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                               "split_kernel_us": round(ms_rs * 1e3, 2),
+                                               "merge_kernel_us": round(ms_rm * 1e3, 2)}
+        log(f"  config 4: {ms_r * 1e3:.2f} us/step; split {ms_rs * 1e3:.2f} us, merge {ms_rm * 1e3:.2f} us")
         extra.update(bench_prefill(cf, stream, steps, warmup))
         log("layer neighbours: LayerNorm F16 (4096 x 768), FFN MatMul F16 (4096 x 768 -> 3072)")
         ms_ln, by_ln, ms_mm, fl_mm = bench_layer_neighbours(cf, stream, max(steps // 4, 10), max(warmup // 2, 3))

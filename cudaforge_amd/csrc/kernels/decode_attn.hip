@@ -71,13 +71,32 @@ __device__ __forceinline__ float* partial_at(const cf_decode_attn_args_t& a, int
 // (a multiple of 16), one per workgroup.  Sequence b (starting at P_b) spans ranges
 // P_b / R .. (P_b + T_b - 1) / R, one split each; its partial records are numbered
 // after those of sequences 0 .. b-1, record (piece, kv head) at piece * H_kv + kv head.
-struct BalancedGeom { int W, R; };
+// Every lane of the calling wave gets the geometry (B <= 64: lane b holds sequence b's
+// figures), from one load per lane and two wave prefix sums.
+struct BalancedGeom {
+    int W, R;          // total attended positions, positions per workgroup
+    int T, P, pieces;  // lane b: T_b, its first position P_b, records before its own
+    int ns;            // lane b: splits (pieces) of sequence b
+};
+__device__ __forceinline__ int wave_excl_sum(int v, int lane) {
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    return x - v;
+}
 __device__ __forceinline__ BalancedGeom balanced_geom(const cf_decode_attn_args_t& a) {
-    int W = 0;
-    for (int b = 0; b < a.B; b++) W += attended(a, b);
-    int R = (W + a.n_split - 1) / a.n_split;
-    R = (R + 15) / 16 * 16;
-    return {W, R};
+    const int lane = threadIdx.x & 63;
+    BalancedGeom g;
+    g.T = lane < a.B ? attended(a, lane) : 0;
+    g.P = wave_excl_sum(g.T, lane);
+    g.W = __builtin_amdgcn_readlane(g.P + g.T, 63);
+    g.R = ((g.W + a.n_split - 1) / a.n_split + 15) / 16 * 16;
+    g.ns = lane < a.B ? (g.P + g.T - 1) / g.R - g.P / g.R + 1 : 0;
+    g.pieces = wave_excl_sum(g.ns, lane);
+    return g;
 }
 
 // The splits of (b, unit): their count and where split s's record is (first + s * step
@@ -90,13 +109,7 @@ __device__ __forceinline__ SplitRecords split_records(const cf_decode_attn_args_
         return {(T_b + a.chunk - 1) / a.chunk, a.partials + (size_t)unit * a.n_split * stride, (size_t)stride};
     }
     const BalancedGeom geo = balanced_geom(a);
-    int P = 0, pieces = 0, ns = 1;
-    for (int bb = 0; bb <= b; bb++) {
-        const int T = attended(a, bb);
-        ns = (P + T - 1) / geo.R - P / geo.R + 1;
-        if (bb < b) pieces += ns;
-        P += T;
-    }
+    const int ns = __builtin_amdgcn_readlane(geo.ns, b), pieces = __builtin_amdgcn_readlane(geo.pieces, b);
     return {ns, a.partials + ((size_t)pieces * a.H_kv + unit % units_per_b) * stride, (size_t)a.H_kv * stride};
 }
 
@@ -360,18 +373,16 @@ void split_f16(cf_decode_attn_args_t a) {
             // attended positions laid end to end, one piece per sequence it overlaps.
             const BalancedGeom geo = balanced_geom(a);
             const int lo = (int)blockIdx.x * geo.R, hi = min(lo + geo.R, geo.W);
-            int P = 0, pieces = 0;
-            for (int b = 0; b < a.B && P < hi; b++) {
-                const int T = attended(a, b);
-                const int first = P / geo.R, ns = (P + T - 1) / geo.R - first + 1;
-                if (P + T > lo) {
-                    float* part = ns == 1 ? nullptr
-                                          : a.partials + ((size_t)(pieces + (int)blockIdx.x - first) * a.H_kv + kvh) *
-                                                             part_stride(G, D);
-                    split_range<D, G, NS, WIDE>(a, ring, b, kvh, max(lo - P, 0), min(hi - P, T), part);
-                }
-                P += T;
-                pieces += ns;
+            for (int b = 0; b < a.B; b++) {
+                const int P = __builtin_amdgcn_readlane(geo.P, b), T = __builtin_amdgcn_readlane(geo.T, b);
+                if (P >= hi) break;
+                if (P + T <= lo) continue;
+                const int first = P / geo.R, ns = __builtin_amdgcn_readlane(geo.ns, b);
+                float* part = ns == 1 ? nullptr
+                                      : a.partials + ((size_t)(__builtin_amdgcn_readlane(geo.pieces, b) +
+                                                               (int)blockIdx.x - first) * a.H_kv + kvh) *
+                                                         part_stride(G, D);
+                split_range<D, G, NS, WIDE>(a, ring, b, kvh, max(lo - P, 0), min(hi - P, T), part);
             }
             return;
         }
@@ -676,10 +687,12 @@ void merge_kernel(cf_decode_attn_args_t a, int Gx, int units_per_b) {
 // own 4 dims each; the SG = 256/DV thread groups take splits sg, sg+SG, ... with NB
 // records in flight per thread, so a sequence with hundreds of splits costs a few load
 // rounds instead of one per 16 splits; the SG running results are combined through LDS.
-template <typename T>
-__global__ __launch_bounds__(kMergeThreads)
+// The thread groups' results combine in a log-depth tree (a serial pass over them cost
+// ~1.5 us with hundreds of splits; 256 threads measured faster than 1024 per row).
+template <typename T, int NT = kMergeThreads>
+__global__ __launch_bounds__(NT)
 void merge_rows(cf_decode_attn_args_t a, int Gx, int units_per_b) {
-    const int D = a.d, DV = D >> 2, SG = kMergeThreads / DV;
+    const int D = a.d, DV = D >> 2, SG = NT / DV;
     const int row = blockIdx.x;
     const int g = row % Gx, unit = row / Gx, b = unit / units_per_b;
     const int stride = part_stride(Gx, D), hdr = part_hdr(Gx);
@@ -687,8 +700,8 @@ void merge_rows(cf_decode_attn_args_t a, int Gx, int units_per_b) {
     const int nsplit = sr.n;
     if (nsplit <= 1) return;                       // finished by the split kernel
     const int tid = threadIdx.x, col = tid % DV, sg = tid / DV;
-    __shared__ float sm[kMergeThreads], sd[kMergeThreads];
-    __shared__ f4_t sn[kMergeThreads];
+    __shared__ float sm[NT], sd[NT];
+    __shared__ f4_t sn[NT];
     float M = -INFINITY, den = 0.0f;
     f4_t num = {0.f, 0.f, 0.f, 0.f};
     if (sg < SG) {
@@ -721,23 +734,28 @@ void merge_rows(cf_decode_attn_args_t a, int Gx, int units_per_b) {
             M = m_new;
         }
     }
+    // The SG groups' (M, den, num) of each column combine in a tree through LDS.
     sm[tid] = M;
     sd[tid] = den;
     sn[tid] = num;
     __syncthreads();
-    if (sg == 0) {
-        float Mx = -INFINITY;
-        for (int k = 0; k < SG; k++) Mx = fmaxf(Mx, sm[k * DV + col]);
-        float dd = 0.0f;
-        f4_t nn = {0.f, 0.f, 0.f, 0.f};
-        for (int k = 0; k < SG; k++) {
-            const float mk = sm[k * DV + col];
-            const float w = mk == -INFINITY ? 0.0f : exp2f(mk - Mx);
-            dd = __builtin_fmaf(w, sd[k * DV + col], dd);
-            nn += w * sn[k * DV + col];
+    for (int half = SG / 2; half >= 1; half >>= 1) {
+        if (sg < half) {
+            const int o = tid + half * DV;
+            const float m1 = sm[tid], m2 = sm[o];
+            const float mx = fmaxf(m1, m2);
+            const float w1 = m1 == -INFINITY ? 0.0f : exp2f(m1 - mx);
+            const float w2 = m2 == -INFINITY ? 0.0f : exp2f(m2 - mx);
+            sm[tid] = mx;
+            sd[tid] = w1 * sd[tid] + w2 * sd[o];
+            sn[tid] = w1 * sn[tid] + w2 * sn[o];
         }
+        __syncthreads();
+    }
+    if (sg == 0) {
         T* out = (T*)a.o + (size_t)row * D + 4 * col;
-        const float inv = 1.0f / dd;
+        const float inv = 1.0f / sd[tid];
+        const f4_t nn = sn[tid];
 #pragma unroll
         for (int e = 0; e < 4; e++) out[e] = from_f<T>(nn[e] * inv);
     }
@@ -959,9 +977,9 @@ extern "C" int cf_launch_decode_attn_merge(const cf_decode_attn_args_t* a, void*
     if (a->d % 4 == 0 && a->d / 4 <= kMergeThreads) {
         dim3 grid((unsigned)((size_t)a->B * units_per_b * Gx));
         if (a->elem == CF_ELEM_F16)
-            hipLaunchKernelGGL(merge_rows<_Float16>, grid, dim3(kMergeThreads), 0, s, *a, Gx, units_per_b);
+            hipLaunchKernelGGL((merge_rows<_Float16>), grid, dim3(kMergeThreads), 0, s, *a, Gx, units_per_b);
         else
-            hipLaunchKernelGGL(merge_rows<float>, grid, dim3(kMergeThreads), 0, s, *a, Gx, units_per_b);
+            hipLaunchKernelGGL((merge_rows<float>), grid, dim3(kMergeThreads), 0, s, *a, Gx, units_per_b);
         return (int)hipGetLastError();
     }
     const size_t total = (size_t)a->B * units_per_b * Gx * a->d;
