@@ -6,7 +6,9 @@ import ctypes
 import os
 from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcudaforge_amd.so")
+# CUDAFORGE_AMD_LIB selects another build of the library (the host-sanitizer build).
+LIB_PATH = os.environ.get("CUDAFORGE_AMD_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                                "libcudaforge_amd.so")
 
 
 class NativeLibraryMissing(RuntimeError):

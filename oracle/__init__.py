@@ -39,7 +39,8 @@ from ctypes import POINTER, c_double, c_float, c_int, c_int32, c_int64, c_size_t
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-ORACLE_SO = os.path.join(HERE, "_build", "liboracle.so")
+# ORACLE_SO may name the sanitizer build (tests/sanitize.sh).
+ORACLE_SO = os.environ.get("CUDAFORGE_ORACLE_SO") or os.path.join(HERE, "_build", "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libcfref.so")
 
 _lib = None
