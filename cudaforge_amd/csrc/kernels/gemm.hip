@@ -102,17 +102,17 @@ __device__ __forceinline__ size_t col_part(const cf_gemm_args_t& a, int seg, int
 }
 
 // Store the accumulators of a wave tile: acc[i][j][e] is C[m0 + 16i + 4*lq + e][n0 + 16j + lr].
-template <typename T>
+template <typename T, int NJ = 4>
 __device__ __forceinline__ void store_tile(const cf_gemm_args_t& a, int seg, int N, int m0, int n0,
-                                           int lr, int lq, const f4_t (&acc)[4][4]) {
+                                           int lr, int lq, const f4_t (&acc)[4][NJ]) {
     const T* __restrict__ bias = (const T*)a.bias[seg];
     const T* __restrict__ res = a.out_kind == CF_GEMM_OUT_ROWMAJOR ? (const T*)a.residual : nullptr;
     T* __restrict__ out = (T*)a.out[seg];
-    size_t cp[4];
-    float bv[4];
-    bool nok[4];
+    size_t cp[NJ];
+    float bv[NJ];
+    bool nok[NJ];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
+    for (int j = 0; j < NJ; j++) {
         const int n = n0 + 16 * j + lr;
         nok[j] = n < N;
         cp[j] = nok[j] ? col_part(a, seg, n) : 0;
@@ -126,7 +126,7 @@ __device__ __forceinline__ void store_tile(const cf_gemm_args_t& a, int seg, int
             if (m >= a.M) continue;
             const size_t rp = row_part(a, seg, m);
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
+            for (int j = 0; j < NJ; j++) {
                 if (!nok[j]) continue;
                 float v = acc[i][j][e] + bv[j];
                 if (res) v += to_f(res[rp + cp[j]]);
@@ -627,37 +627,47 @@ void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
 }
 
 // ------------------------------------------------------------------------- fp32 ---
+// 128 x BNT tiles (BNT = 128, or 96 where 128-column tiles leave CUs idle), k-tiles of
+// 16 double-buffered in LDS: the next k-tile is loaded into registers while the current
+// one is multiplied, then stored to the other buffer, one barrier per k-tile.  Both
+// operands are stored k-major so each MFMA operand is one conflict-free ds_read_b32.
 constexpr int BK32 = 16;
-constexpr int LDM32 = BM + 4;     // floats per k-major LDS row
+constexpr int LDM32 = BM + 4;     // floats per k-major LDS row of A
 
-__global__ __launch_bounds__(kThreads)
+template <int BNT>
+__global__ __launch_bounds__(kThreads, 2)
 void gemm_f32(cf_gemm_args_t a, Tiling t) {
-    __shared__ float As[BK32 * LDM32];   // [k][m]
-    __shared__ float Bs[BK32 * LDM32];   // [k][n]
+    constexpr int NJ = BNT / 32;                  // 16-column MFMA blocks per wave
+    constexpr int LDN = BNT + 4;                  // floats per k-major LDS row of W
+    constexpr int WCH = BK32 * BNT / 4;           // float4 chunks of a W k-tile
+    constexpr int WPT = (WCH + kThreads - 1) / kThreads;
+    __shared__ float As[2][BK32 * LDM32];   // [k][m]
+    __shared__ float Bs[2][BK32 * LDN];     // [k][n]
 
     int tile_m, tile_n;
     tile_of_block(blockIdx.x, t.n_tiles_m, t.seg_start[3], t.group_m, tile_m, tile_n);
     const int seg = find_seg(a, t, tile_n);
     const int N = a.n[seg];
     const int m0 = tile_m * BM;
-    const int n0 = (tile_n - t.seg_start[seg]) * BN;
+    const int n0 = (tile_n - t.seg_start[seg]) * BNT;
     const float* __restrict__ A = (const float*)a.a;
     const float* __restrict__ W = (const float*)a.w[seg];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = (wave & 1) * 64, wn = (wave >> 1) * 64;
+    const int wm = (wave & 1) * 64, wn = (wave >> 1) * (BNT / 2);
     const int lr = lane & 15, lq = lane >> 4;
     const bool a_vec = t.a_vec != 0;
     const bool w_vec = t.w_vec[seg] != 0;
 
-    f4_t acc[4][4];
+    f4_t acc[4][NJ];
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < NJ; j++) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-    for (int k0 = 0; k0 < a.K; k0 += BK32) {
-        // A: 128 rows x 16 k = 512 chunks of 4; 2 per thread; stored transposed [k][m].
+    // A: 128 rows x 16 k = 512 chunks of 4 (2 per thread); W: 16 k x BNT n (WPT per thread).
+    f4_t ra[2], rw[WPT];
+    auto load = [&](int k0) {
 #pragma unroll
         for (int it = 0; it < 2; it++) {
             const int ch = tid + it * kThreads;
@@ -672,17 +682,15 @@ void gemm_f32(cf_gemm_args_t a, Tiling t) {
                     for (int e = 0; e < 4; e++) if (gk + e < a.K) v[e] = src[e];
                 }
             }
-#pragma unroll
-            for (int e = 0; e < 4; e++) As[(kc + e) * LDM32 + r] = v[e];
+            ra[it] = v;
         }
-        // W: 16 k x 128 n = 512 chunks of 4; 2 per thread; stored [k][n].
 #pragma unroll
-        for (int it = 0; it < 2; it++) {
+        for (int it = 0; it < WPT; it++) {
             const int ch = tid + it * kThreads;
-            const int kr = ch >> 5, nc = (ch & 31) * 4;
+            const int kr = ch / (BNT / 4), nc = (ch % (BNT / 4)) * 4;
             const int gk = k0 + kr, gn = n0 + nc;
             f4_t v{};
-            if (gk < a.K) {
+            if (ch < WCH && gk < a.K) {
                 const float* src = W + (size_t)gk * N + gn;
                 if (w_vec && gn + 4 <= N) v = *(const f4_t*)src;
                 else {
@@ -690,25 +698,48 @@ void gemm_f32(cf_gemm_args_t a, Tiling t) {
                     for (int e = 0; e < 4; e++) if (gn + e < N) v[e] = src[e];
                 }
             }
-            *(f4_t*)&Bs[kr * LDM32 + nc] = v;
+            rw[it] = v;
         }
-        __syncthreads();
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int it = 0; it < 2; it++) {
+            const int ch = tid + it * kThreads;
+            const int r = ch >> 2, kc = (ch & 3) * 4;
+#pragma unroll
+            for (int e = 0; e < 4; e++) As[buf][(kc + e) * LDM32 + r] = ra[it][e];
+        }
+#pragma unroll
+        for (int it = 0; it < WPT; it++) {
+            const int ch = tid + it * kThreads;
+            if (ch < WCH) *(f4_t*)&Bs[buf][(ch / (BNT / 4)) * LDN + (ch % (BNT / 4)) * 4] = rw[it];
+        }
+    };
+
+    const int nk = (a.K + BK32 - 1) / BK32;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) load((kt + 1) * BK32);
 #pragma unroll
         for (int kk = 0; kk < BK32; kk += 4) {
-            float af[4], bf[4];
+            float af[4], bf[NJ];
 #pragma unroll
-            for (int i = 0; i < 4; i++) af[i] = As[(kk + lq) * LDM32 + wm + 16 * i + lr];
+            for (int i = 0; i < 4; i++) af[i] = As[buf][(kk + lq) * LDM32 + wm + 16 * i + lr];
 #pragma unroll
-            for (int j = 0; j < 4; j++) bf[j] = Bs[(kk + lq) * LDM32 + wn + 16 * j + lr];
+            for (int j = 0; j < NJ; j++) bf[j] = Bs[buf][(kk + lq) * LDN + wn + 16 * j + lr];
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
-                for (int j = 0; j < 4; j++)
+                for (int j = 0; j < NJ; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
+        if (kt + 1 < nk) store(buf ^ 1);
         __syncthreads();
     }
-    store_tile<float>(a, seg, N, m0 + wm, n0 + wn, lr, lq, acc);
+    store_tile<float, NJ>(a, seg, N, m0 + wm, n0 + wn, lr, lq, acc);
 }
 
 int g_gemm_stages = 0;   // tuning override of the direct-to-LDS kernel's ring depth (3, 4; 0 = automatic)
@@ -806,6 +837,9 @@ extern "C" int cf_launch_gemm(const cf_gemm_args_t* a, void* stream) {
         return tiles_m * tn;
     };
     int bn = BN;
+    // fp32: 96-column tiles where 128 leaves CUs idle and 96 fills more of them.
+    if (a->elem == CF_ELEM_F32 && fits(96) && (!fits(128) || (tiles(128) < cu_count() && tiles(96) > tiles(128))))
+        bn = 96;
     if (full) {
         const bool f128 = fits(128), f96 = fits(96), f192 = fits(192);
         if (!f128 && !f96 && !f192) full = false;
@@ -849,8 +883,10 @@ extern "C" int cf_launch_gemm(const cf_gemm_args_t* a, void* stream) {
         if (e != hipSuccess) return (int)e;
     } else if (a->elem == CF_ELEM_F16) {
         hipLaunchKernelGGL(gemm_f16, grid, dim3(kThreads), 0, st, *a, t);
+    } else if (bn == 96) {
+        hipLaunchKernelGGL(gemm_f32<96>, grid, dim3(kThreads), 0, st, *a, t);
     } else {
-        hipLaunchKernelGGL(gemm_f32, grid, dim3(kThreads), 0, st, *a, t);
+        hipLaunchKernelGGL(gemm_f32<128>, grid, dim3(kThreads), 0, st, *a, t);
     }
     return (int)hipGetLastError();
 }
