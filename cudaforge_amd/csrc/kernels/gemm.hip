@@ -438,16 +438,20 @@ __device__ __forceinline__ int swz_a(int row) { return (row >> 1) & (BK / 8 - 1)
 // W rows are BNT * 2 bytes: 16 chunks (BNT = 128), 12 (96) or 24 (192).  The 96- and
 // 192-column permutations flip chunk bits 1-2 only, so they stay inside the row's
 // chunks.  At 96, rows 8 apart (read by the same half-wave) then sit 32 bytes apart in
-// the banks.  At 192 a row is 384 bytes, so rows of one parity start at the same bank;
-// a transpose read takes 32 bytes from each of 16 rows (8 even, 8 odd: 8r + 4h + 0..3
-// for r < 4), and ((row >> 1) ^ (row >> 3)) & 3 gives each parity's 8 rows every
-// 32-byte bank slot of its half twice, the 2-cycle minimum for 512 bytes.  All three
-// depend on row bits 0..4 only, so the rows of the second 32-k half of a BK = 64 stage
-// (row + 32) are permuted like the first.
+// the banks.  A transpose read takes 32 bytes from each of 16 rows, 8r + 4h + 0..3 for
+// r < 4, and the LDS serves it 32 lanes (8 rows, r = 0, 1 or r = 2, 3) at a time, so
+// each half-wave's 8 rows must cover the 8 32-byte slots of the 256-byte bank window
+// once.  At 192 a row is 384 bytes, so odd rows start half a window after even ones,
+// and the even (and odd) rows x, x+2, x+8, x+10 of a half-wave take the four slots of
+// their half through row bits 1 and 3.  (An earlier ((row >> 1) ^ (row >> 3)) & 3
+// covered each slot twice per full wave but only half the slots per half-wave:
+// SQ_LDS_BANK_CONFLICT counted 37 % of the LDS cycles of config 3's QKV product.)
+// All three depend on row bits 0..4 only, so the rows of the second 32-k half of a
+// BK = 64 stage (row + 32) are permuted like the first.
 template <int BNT>
 __device__ __forceinline__ int swz_w(int row) {
     if constexpr (BNT == 128) return ((row & 3) << 1) ^ (((row >> 3) & 1) << 3);
-    else if constexpr (BNT == 192) return (((row >> 1) ^ (row >> 3)) & 3) << 1;
+    else if constexpr (BNT == 192) return (((row >> 1) & 1) | ((row >> 2) & 2)) << 1;
     else return ((row >> 3) & 1) << 1;
 }
 
