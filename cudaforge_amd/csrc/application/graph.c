@@ -81,6 +81,11 @@ static int decode_lens_sync(inference_graph_t* g, int nid) {
     decode_lens_t* dl = decode_lens_at(g, nid);
     if (!dl) return -1;
     const mha_decode_params_t* p = (const mha_decode_params_t*)n->params;
+    if (dl->lens && dl->B < p->batch_size) {   /* the node's batch grew: a larger array */
+        gpu_device_free(dl->lens);
+        dl->lens = NULL;
+        gpu_buffer_generation_bump();          /* a recording may point at the old one */
+    }
     if (!dl->lens) {
         if (p->batch_size <= 0 || p->batch_size > 65535) return -1;
         dl->lens = (int32_t*)gpu_device_alloc((size_t)p->batch_size * sizeof(int32_t));
@@ -410,7 +415,10 @@ static void* pinned_of(inference_graph_t* g, int tid, size_t bytes) {
     }
     pinned_t* e = &((pinned_t*)g->pinned)[tid];
     if (e->host && e->bytes >= bytes) return e->host;
-    if (e->host) gpu_host_free_pinned(e->host);
+    if (e->host) {
+        gpu_host_free_pinned(e->host);
+        gpu_buffer_generation_bump();   /* a recording may copy through the old buffer */
+    }
     e->host = gpu_host_alloc_pinned(bytes);
     e->bytes = e->host ? bytes : 0;
     return e->host;
