@@ -30,31 +30,3 @@ from .api import (  # noqa: F401
     gpu_available,
     init_gpu,
 )
-
-__all__ = [
-    "LIB_PATH",
-    "NativeLibraryMissing",
-    "lib",
-    "load_library",
-    "DeviceBuffer",
-    "MhaDecodeParams",
-    "MhaFusedParams",
-    "MhaDecodeRopeParams",
-    "RopeParams",
-    "LayerNormParams",
-    "MatmulParams",
-    "CastParams",
-    "CausalMaskParams",
-    "GraphMhaMatch",
-    "OperatorRegistry",
-    "Stream",
-    "Event",
-    "TensorT",
-    "call_entry",
-    "call_op",
-    "device_caps",
-    "graph_detect_mha",
-    "find_op",
-    "gpu_available",
-    "init_gpu",
-]
