@@ -24,7 +24,7 @@
 //   A workgroup (4 waves) owns a 128-column tile and one of `k_split` K chunks; waves
 //   interleave k steps and reduce through LDS.
 // With one K chunk the workgroup adds the bias and scatters the result; otherwise it
-// writes an fp32 partial per K chunk and a second launch (gemv_reduce) sums the
+// writes an fp32 partial per K chunk and a second launch (gemv_reduce4) sums the
 // partials, adds the bias and scatters.  The kernel boundary orders the partials: no
 // fences or atomics (each XCD has its own L2).
 
@@ -158,8 +158,8 @@ __device__ __forceinline__ int seg_of(const cf_gemv_args_t& a, const Tiles& t, i
 }
 
 // Split-K partial kernel.  With one K chunk it applies the epilogue itself; otherwise
-// it writes fp32 partials [k_split][Mp][ncols] (ncols = 128 * column tiles) for
-// gemv_reduce.
+// it writes fp32 partials [k_split][M][ncols] (ncols = 128 * column tiles) for
+// gemv_reduce4.
 template <typename T>
 __global__ __launch_bounds__(kThreads)
 void gemv_kernel(cf_gemv_args_t a, Tiles t) {
@@ -192,7 +192,6 @@ void gemv_kernel(cf_gemv_args_t a, Tiles t) {
         for (int i = 0; i < 4; i++) red[wave * kTileVals + (c * 4 + i) * 64 + l] = acc[c][i];
     __syncthreads();
     const int ncols = t.start[a.nseg] * kColTile;
-    const int Mp = gridDim.z * kMTile;
 #pragma unroll
     for (int j = 0; j < kTileVals / kThreads; j++) {
         const int idx = tid + j * kThreads;
@@ -203,7 +202,7 @@ void gemv_kernel(cf_gemv_args_t a, Tiles t) {
         const int lc = tile_col<T>(ci >> 2, ci & 3, li);
         const int mm = mt * kMTile + (li & 15);
         if (a.k_split > 1) {
-            a.partials[((size_t)ks * Mp + mm) * ncols + (size_t)tile * kColTile + lc] = s;
+            if (mm < a.M) a.partials[((size_t)ks * a.M + mm) * ncols + (size_t)tile * kColTile + lc] = s;
         } else if (nb + lc < N && mm < a.M) {
             store_out<T>(a, sg, mm, nb + lc, s);
         }
@@ -326,45 +325,21 @@ void gemv_f16_dma(cf_gemv_args_t a, Tiles t) {
                 if (m < a.M) store_out<_Float16>(a, sg, m, n0 + 16 * j + lr, acc[j][i]);
             }
     } else {
+        // Partials of real rows only; a full M tile stores without per-lane tests.
         const int ncols = t.start[a.nseg] * BN;
-        const int Mp = gridDim.z * kMTile;
+        float* dst = a.partials + ((size_t)ks * a.M + mt * kMTile + 4 * lq) * ncols + (size_t)tile * BN + lr;
+        if (mt * kMTile + kMTile <= a.M) {
 #pragma unroll
-        for (int j = 0; j < NT; j++)
+            for (int j = 0; j < NT; j++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int m = mt * kMTile + 4 * lq + i;
-                a.partials[((size_t)ks * Mp + m) * ncols + (size_t)tile * BN + 16 * j + lr] = acc[j][i];
-            }
-    }
-}
-
-// Sums the K-chunk partials of every output element and applies the epilogue.
-template <typename T>
-__global__ __launch_bounds__(256)
-void gemv_reduce(cf_gemv_args_t a, Tiles t) {
-    const int ncols = t.start[a.nseg] * t.bn;
-    const int Mp = (a.M + kMTile - 1) / kMTile * kMTile;
-    const size_t total = (size_t)a.M * ncols;
-    const size_t plane = (size_t)Mp * ncols;
-    for (size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (size_t)gridDim.x * 256) {
-        const int m = (int)(idx / ncols), col = (int)(idx - (size_t)m * ncols);
-        const int tile = col / t.bn;
-        const int seg = seg_of(a, t, tile);
-        const int n = (tile - t.start[seg]) * t.bn + (col - tile * t.bn);
-        if (n >= a.seg[seg].n) continue;
-        const float* p = a.partials + (size_t)m * ncols + col;
-        // Eight independent loads in flight per round trip.
-        float s0 = 0.0f, s1 = 0.0f;
-        int kk = 0;
-        for (; kk + 8 <= a.k_split; kk += 8) {
-            float v[8];
+                for (int i = 0; i < 4; i++) dst[(size_t)i * ncols + 16 * j] = acc[j][i];
+        } else {
 #pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = p[(size_t)(kk + j) * plane];
+            for (int j = 0; j < NT; j++)
 #pragma unroll
-            for (int j = 0; j < 8; j += 2) { s0 += v[j]; s1 += v[j + 1]; }
+                for (int i = 0; i < 4; i++)
+                    if (mt * kMTile + 4 * lq + i < a.M) dst[(size_t)i * ncols + 16 * j] = acc[j][i];
         }
-        for (; kk < a.k_split; kk++) s0 += p[(size_t)kk * plane];
-        store_out<T>(a, a.seg[seg], m, n, s0 + s1);
     }
 }
 
@@ -386,32 +361,37 @@ int dma_bn(const cf_gemv_args_t* a) {
     return bn;
 }
 
-// Reduce for the DMA path (tile widths are multiples of 64): a thread owns 4 adjacent
-// columns of one row and issues all of its K-chunk loads (16-byte) before summing, so
-// the whole reduction is one round trip to memory.  One-wave workgroups spread the
-// partials over every CU (16 rows x 6144 columns is 384 of them).
+// Partial reduce (tile widths are multiples of 64, so 4 adjacent columns share a tile):
+// a thread owns 4 adjacent columns of one row and issues all of its K-chunk loads
+// (16-byte) before summing, so the whole reduction is one round trip to memory.
+// One-wave workgroups spread the partials over every CU (16 rows x 6144 columns is
+// 384 of them).
 constexpr int kReduceThreads = 64;
+constexpr int kMaxKSplit = 32;    // K chunks the reduce keeps in flight
+template <typename T>
 __global__ __launch_bounds__(kReduceThreads)
 void gemv_reduce4(cf_gemv_args_t a, Tiles t) {
-    constexpr int MAXKS = 32;
+    constexpr int MAXKS = kMaxKSplit;
     const int ncols = t.start[a.nseg] * t.bn;
-    const int Mp = (a.M + kMTile - 1) / kMTile * kMTile;
-    const size_t plane = (size_t)Mp * ncols;
+    const size_t plane = (size_t)a.M * ncols;
     const size_t total = (size_t)a.M * (ncols / 4);
     const size_t idx = (size_t)blockIdx.x * kReduceThreads + threadIdx.x;
     if (idx >= total) return;
     const int m = (int)(idx / (ncols / 4));
     const int col = (int)(idx - (size_t)m * (ncols / 4)) * 4;
     const float* p = a.partials + (size_t)m * ncols + col;
-    f4_t v[MAXKS];
-#pragma unroll
-    for (int k = 0; k < MAXKS; k++)
-        if (k < a.k_split) v[k] = *(const f4_t*)(p + (size_t)k * plane);
     f4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < a.k_split; kb += MAXKS) {   // one pass: k_split <= MAXKS
+        const int nk = min(MAXKS, a.k_split - kb);
+        f4_t v[MAXKS];
 #pragma unroll
-    for (int k = 0; k < MAXKS; k += 2) {
-        if (k < a.k_split) s0 += v[k];
-        if (k + 1 < a.k_split) s1 += v[k + 1];
+        for (int k = 0; k < MAXKS; k++)
+            if (k < nk) v[k] = *(const f4_t*)(p + (size_t)(kb + k) * plane);
+#pragma unroll
+        for (int k = 0; k < MAXKS; k += 2) {
+            if (k < nk) s0 += v[k];
+            if (k + 1 < nk) s1 += v[k + 1];
+        }
     }
     s0 += s1;
     const int tile = col / t.bn;
@@ -419,7 +399,7 @@ void gemv_reduce4(cf_gemv_args_t a, Tiles t) {
     const int n = (tile - t.start[seg]) * t.bn + (col - tile * t.bn);
 #pragma unroll
     for (int e = 0; e < 4; e++)
-        if (n + e < a.seg[seg].n) store_out<_Float16>(a, a.seg[seg], m, n + e, s0[e]);
+        if (n + e < a.seg[seg].n) store_out<T>(a, a.seg[seg], m, n + e, s0[e]);
 }
 
 Tiles make_tiles(const cf_gemv_args_t* a) {
@@ -443,11 +423,11 @@ Tiles make_tiles(const cf_gemv_args_t* a) {
         ks = (per_cu * cu_count() + units - 1) / units;
         if (ks > a->K / kDK) ks = a->K / kDK;
         if (g_dma_ks > 0) ks = g_dma_ks;
-        if (ks > 32) ks = 32;                 // gemv_reduce4 keeps all chunks in flight
         if (ks < 1) ks = 1;
     } else {
         ks = a->k_split > 0 ? a->k_split : 1;
     }
+    if (ks > kMaxKSplit) ks = kMaxKSplit;
     int chunk = (a->K + ks - 1) / ks;
     chunk = (chunk + kstep - 1) / kstep * kstep;
     t.k_chunk = chunk;
@@ -472,8 +452,7 @@ extern "C" int32_t cf_gemv_k_step(int32_t elem) {
 extern "C" size_t cf_gemv_partials_floats(const cf_gemv_args_t* a) {
     const Tiles t = make_tiles(a);
     if (t.ks <= 1) return 0;
-    const size_t Mp = (size_t)((a->M + kMTile - 1) / kMTile) * kMTile;
-    return (size_t)t.ks * Mp * (size_t)t.start[a->nseg] * t.bn;
+    return (size_t)t.ks * (size_t)a->M * (size_t)t.start[a->nseg] * t.bn;
 }
 
 extern "C" int cf_launch_gemv(const cf_gemv_args_t* a, void* stream) {
@@ -496,18 +475,11 @@ extern "C" int cf_launch_gemv(const cf_gemv_args_t* a, void* stream) {
         hipLaunchKernelGGL(gemv_kernel<float>, grid, dim3(kThreads), 0, s, args, t);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || t.ks == 1) return (int)e;
-    if (t.dma) {
-        const size_t total4 = (size_t)a->M * t.start[a->nseg] * t.bn / 4;
-        hipLaunchKernelGGL(gemv_reduce4, dim3((unsigned)((total4 + kReduceThreads - 1) / kReduceThreads)),
-                           dim3(kReduceThreads), 0, s, args, t);
-        return (int)hipGetLastError();
-    }
-    const size_t total = (size_t)a->M * t.start[a->nseg] * t.bn;
-    size_t blocks = (total + 255) / 256;
-    if (blocks > 4096) blocks = 4096;
+    const size_t total4 = (size_t)a->M * t.start[a->nseg] * t.bn / 4;
+    const dim3 rgrid((unsigned)((total4 + kReduceThreads - 1) / kReduceThreads));
     if (a->elem == CF_ELEM_F16)
-        hipLaunchKernelGGL(gemv_reduce<_Float16>, dim3((unsigned)blocks), dim3(256), 0, s, args, t);
+        hipLaunchKernelGGL(gemv_reduce4<_Float16>, rgrid, dim3(kReduceThreads), 0, s, args, t);
     else
-        hipLaunchKernelGGL(gemv_reduce<float>, dim3((unsigned)blocks), dim3(256), 0, s, args, t);
+        hipLaunchKernelGGL(gemv_reduce4<float>, rgrid, dim3(kReduceThreads), 0, s, args, t);
     return (int)hipGetLastError();
 }

@@ -109,7 +109,8 @@ typedef struct {
     int64_t        pos_uniform;
     int64_t        pos_limit; /* rows whose pos is outside [0, pos_limit) are not stored;
                                  0 = no limit */
-    int32_t        k_split;   /* >= 1; K chunk = ceil(K / k_split) rounded to the k step */
+    int32_t        k_split;   /* 1..32 (larger is taken as 32); K chunk = ceil(K / k_split)
+                                 rounded to the k step */
     float*         partials;  /* workspace */
     int32_t        elem;
 } cf_gemv_args_t;

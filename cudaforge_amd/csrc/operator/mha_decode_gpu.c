@@ -256,6 +256,7 @@ static int gemv_k_split(int elem, int64_t K, int64_t col_tiles, int64_t m_tiles)
     int64_t ks = cf_ceil_div(target, col_tiles * m_tiles);
     int64_t kmax = K / (4 * kstep);  /* keep >= 4 k steps (one per wave) per chunk */
     if (ks > kmax) ks = kmax;
+    if (ks > 32) ks = 32;            /* the reduce sums up to 32 chunks in one round trip */
     if (ks < 1) ks = 1;
     /* every chunk non-empty */
     while (ks > 1) {
