@@ -399,6 +399,8 @@ static int is_kv(const inference_graph_t* g, int tid) {
 typedef struct {
     void*  host;
     size_t bytes;
+    int    rec_in;    /* its upload copy is a node of the recording */
+    int    rec_out;   /* its download copy is a node of the recording */
 } pinned_t;
 
 #define GRAPH_PINNED_MAX ((size_t)16 << 20)
@@ -424,6 +426,14 @@ static void* pinned_of(inference_graph_t* g, int tid, size_t bytes) {
     return e->host;
 }
 
+static pinned_t* pinned_entry(inference_graph_t* g, int tid) {
+    return tid >= 0 && tid < g->pinned_cap ? &((pinned_t*)g->pinned)[tid] : NULL;
+}
+
+static void pinned_clear_recorded(inference_graph_t* g) {
+    for (int i = 0; i < g->pinned_cap; i++) ((pinned_t*)g->pinned)[i].rec_in = ((pinned_t*)g->pinned)[i].rec_out = 0;
+}
+
 static void pinned_free(inference_graph_t* g) {
     pinned_t* v = (pinned_t*)g->pinned;
     for (int i = 0; i < g->pinned_cap; i++)
@@ -433,19 +443,59 @@ static void pinned_free(inference_graph_t* g) {
     g->pinned_cap = 0;
 }
 
+/* How an execution moves a staged graph input to the device. */
+enum {
+    UPLOAD_NOW = 0,     /* copy kernel on the graph's stream now */
+    UPLOAD_RECORD = 1,  /* fill the staging and mark it: the recording's first nodes copy it */
+    UPLOAD_REPLAY = 2,  /* fill the staging of the inputs whose copy is in the recording */
+};
+
 /* Host -> device copy of graph input tid: through its pinned staging on the graph's
  * stream, ordered before the launches that read it (no host synchronisation).  The first
  * upload of a tensor, and tensors without staging, go through tensor_upload (legacy
  * stream); *legacy is then set so the caller waits for it. */
-static int upload_input(inference_graph_t* g, int tid, tensor_t* t, int* legacy) {
+static int upload_input(inference_graph_t* g, int tid, tensor_t* t, int* legacy, int mode) {
     const size_t bytes = tensor_nbytes(t);
     void* stage = t->data_device ? pinned_of(g, tid, bytes) : NULL;
+    if (stage && mode == UPLOAD_REPLAY && !pinned_entry(g, tid)->rec_in) stage = NULL;
     if (!stage) {
         *legacy = 1;
         return tensor_upload(t);
     }
     memcpy(stage, t->data, bytes);
+    if (mode == UPLOAD_RECORD) pinned_entry(g, tid)->rec_in = 1;
+    if (mode != UPLOAD_NOW) return 0;
     return cf_launch_copy_bytes(t->data_device, stage, bytes, g->hip_graph) == 0 ? 0 : -1;
+}
+
+/* Inside a capture: the copies of the staged inputs (first) or of the graph outputs
+ * (last) as nodes of the recording, so a replay runs them back to back with the
+ * operators' launches instead of as separate launches around the graph. */
+static int record_input_copies(inference_graph_t* g) {
+    for (int tid = 0; tid < g->pinned_cap && tid < g->num_tensors; tid++) {
+        const pinned_t* e = pinned_entry(g, tid);
+        if (!e->rec_in) continue;
+        tensor_t* t = g->tensors[tid].tensor;
+        if (cf_launch_copy_bytes(t->data_device, e->host, tensor_nbytes(t), g->hip_graph) != 0) return -1;
+    }
+    return 0;
+}
+
+static int record_output_copies(inference_graph_t* g) {
+    for (int i = 0; i < g->num_outputs; i++) {
+        const graph_node_t* n = &g->nodes[g->output_node_ids[i]];
+        if (n->type != OP_OUTPUT || n->num_inputs <= 0) continue;
+        const int tid = n->input_tensors[0];
+        if (tid < 0 || tid >= g->num_tensors) continue;
+        tensor_t* src = g->tensors[tid].tensor;
+        if (!src->data_device) continue;
+        const size_t bytes = tensor_nbytes(src);
+        void* stage = pinned_of(g, tid, bytes);
+        if (!stage) continue;
+        if (cf_launch_copy_bytes(stage, src->data_device, bytes, g->hip_graph) != 0) return -1;
+        pinned_entry(g, tid)->rec_out = 1;
+    }
+    return 0;
 }
 
 /* Written by an operator during execution (so its device copy is the current one), as
@@ -527,7 +577,7 @@ static int run_node(inference_graph_t* g, int nid, const graph_node_t* n, bool u
                 copied |= !t->data_device;
                 if (tensor_copy_to_device(t) != 0) ret = -1;
             } else if (!fresh[tid]) {
-                if (upload_input(g, tid, t, &copied) != 0) ret = -1;
+                if (upload_input(g, tid, t, &copied, UPLOAD_NOW) != 0) ret = -1;
                 fresh[tid] = 1;
             }
             slots[i] = t->data_device;
@@ -599,7 +649,7 @@ static int run_node(inference_graph_t* g, int nid, const graph_node_t* n, bool u
  * produced by an operator (the graph inputs and constant inputs), marking it fresh, and
  * makes sure the KV caches and weights are on the device: a recorded execution may not
  * copy from the host. */
-static int preload_inputs(inference_graph_t* g, unsigned char* fresh) {
+static int preload_inputs(inference_graph_t* g, unsigned char* fresh, int mode) {
     int legacy = 0;
     for (int i = 0; i < g->num_nodes; i++) {
         const graph_node_t* n = &g->nodes[i];
@@ -611,7 +661,7 @@ static int preload_inputs(inference_graph_t* g, unsigned char* fresh) {
                 if (is_kv(g, tid) && tensor_copy_to_device(t) != 0) return -1;
                 continue;
             }
-            if (upload_input(g, tid, t, &legacy) != 0) return -1;
+            if (upload_input(g, tid, t, &legacy, mode) != 0) return -1;
             fresh[tid] = 1;
         }
         for (int w = 0; w < n->num_weights; w++)
@@ -721,22 +771,46 @@ int graph_execute(inference_graph_t* g, tensor_t* inputs[], tensor_t* outputs[],
     if (!fresh) return -1;
 
     int ret = 0;
+    int in_graph = 0;   /* this execution launched the recording, its I/O copies included */
     const int replay = use_cuda && !g->replay_off;
     /* A buffer the recording points at was freed or handed to another stream since it was
      * made: record again. */
     if (replay && g->hip_graph_state == 2 && g->replay_generation != gpu_buffer_generation()) replay_reset(g);
     if (replay && g->hip_graph_state == 2 && g->hip_graph_exec) {
-        ret = preload_inputs(g, fresh);
-        if (ret == 0) ret = gpu_graph_launch(g->hip_graph_exec, g->hip_graph);
-        if (ret == 0) decode_lens_replayed(g);
+        ret = preload_inputs(g, fresh, UPLOAD_REPLAY);
+        if (ret == 0 && g->replay_generation != gpu_buffer_generation()) {
+            /* The preload itself replaced such a buffer: this execution runs eagerly. */
+            replay_reset(g);
+            pinned_clear_recorded(g);
+            memset(fresh, 0, (size_t)(g->num_tensors > 0 ? g->num_tensors : 1));
+            int all_gpu = 0;
+            ret = run_nodes(g, use_cuda, fresh, &all_gpu, 0);
+            if (ret == 0 && all_gpu) g->hip_graph_state = 1;
+        } else if (ret == 0) {
+            ret = gpu_graph_launch(g->hip_graph_exec, g->hip_graph);
+            if (ret == 0) {
+                decode_lens_replayed(g);
+                in_graph = 1;
+            }
+        }
     } else if (replay && g->hip_graph_state == 1) {
         /* Record this execution's launches, then run the recording. */
         int all_gpu = 0, recorded = 0;
         void* exec = NULL;
-        ret = preload_inputs(g, fresh);
+        pinned_clear_recorded(g);
+        ret = preload_inputs(g, fresh, UPLOAD_RECORD);
+        /* Output staging is allocated before the capture (no allocation inside it). */
+        for (int i = 0; i < g->num_outputs && ret == 0; i++) {
+            const graph_node_t* n = &g->nodes[g->output_node_ids[i]];
+            const int tid = n->type == OP_OUTPUT && n->num_inputs > 0 ? n->input_tensors[0] : -1;
+            if (tid >= 0 && tid < g->num_tensors && g->tensors[tid].tensor->data_device)
+                (void)pinned_of(g, tid, tensor_nbytes(g->tensors[tid].tensor));
+        }
         const uint64_t gen = gpu_buffer_generation();
         if (ret == 0 && gpu_capture_begin(g->hip_graph) == 0) {
-            const int rrc = run_nodes(g, use_cuda, fresh, &all_gpu, 1);
+            int rrc = record_input_copies(g);
+            if (rrc == 0) rrc = run_nodes(g, use_cuda, fresh, &all_gpu, 1);
+            if (rrc == 0 && all_gpu) rrc = record_output_copies(g);
             const int crc = gpu_capture_end(g->hip_graph, &exec);
             if (rrc == 0 && crc == 0 && all_gpu && gen == gpu_buffer_generation()) {
                 g->hip_graph_exec = exec;
@@ -744,6 +818,7 @@ int graph_execute(inference_graph_t* g, tensor_t* inputs[], tensor_t* outputs[],
                 g->replay_generation = gen;
                 recorded = 1;
                 ret = gpu_graph_launch(exec, g->hip_graph);
+                in_graph = ret == 0;
             }
         }
         if (ret == 0 && !recorded) {
@@ -752,6 +827,7 @@ int graph_execute(inference_graph_t* g, tensor_t* inputs[], tensor_t* outputs[],
             gpu_graph_exec_destroy(exec);
             (void)gpu_get_last_error();
             g->hip_graph_state = -1;
+            pinned_clear_recorded(g);
             memset(fresh, 0, (size_t)(g->num_tensors > 0 ? g->num_tensors : 1));
             /* The failed recording's lengths bookkeeping ran ahead of the device. */
             for (int i = 0; i < g->decode_lens_cap; i++) ((decode_lens_t*)g->decode_lens)[i].held = -1;
@@ -776,8 +852,13 @@ int graph_execute(inference_graph_t* g, tensor_t* inputs[], tensor_t* outputs[],
         tensor_t* src = g->tensors[tid].tensor;
         if (use_cuda && src->data_device) {
             const size_t bytes = tensor_nbytes(src);
-            void* stage = pinned_of(g, tid, bytes);
-            if (stage) {
+            const pinned_t* rec = in_graph ? pinned_entry(g, tid) : NULL;
+            void* stage = rec && rec->rec_out ? NULL : pinned_of(g, tid, bytes);
+            if (rec && rec->rec_out) {
+                /* The recording's last nodes copied it into the staging. */
+                if (!synced && gpu_stream_synchronize(g->hip_graph) != 0) return -1;
+                memcpy(src->data, rec->host, bytes);
+            } else if (stage) {
                 if (cf_launch_copy_bytes(stage, src->data_device, bytes, g->hip_graph) != 0 ||
                     gpu_stream_synchronize(g->hip_graph) != 0)
                     return -1;
