@@ -158,7 +158,7 @@ def bench_decode_ragged(cf, stream, steps, warmup):
     return ms, alg, [int(x) + 1 for x in lens], ms_split, ms_merge
 
 
-def bench_decode_graph(cf, steps, warmup, B=16, H=32, H_kv=8, d=128, T=4096, seed=700):
+def bench_decode_graph(cf, steps, warmup, B=16, H=32, H_kv=8, d=128, T=4096, seed=700, replay=True):
     """Config-2 decode through the graph executor, the host-buffer boundary: each step
     copies X_new host->device, runs the MHA_Decode node against device-resident in-place
     KV caches (graph_set_kv_cache), synchronises and copies Y back (graph.c:670-1115 is
@@ -196,6 +196,8 @@ def bench_decode_graph(cf, steps, warmup, B=16, H=32, H_kv=8, d=128, T=4096, see
     lib.graph_set_kv_cache(g, iK, iV)
     if lib.graph_build(g) != 0:
         raise RuntimeError("graph_build failed")
+    if not replay:
+        lib.graph_set_replay(g, 0)
     ins, outs = (c_void_p * 1)(tX), (c_void_p * 1)(tY)
     t_start, cl = None, cl0
     for i in range(warmup + steps):

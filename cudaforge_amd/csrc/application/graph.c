@@ -35,10 +35,11 @@
 #include <string.h>
 
 /* Device-held length of a uniform-length decode node (GPU executions).  The node runs in
- * the operator's device-uniform mode (cache_len MHA_DECODE_CACHE_LEN_DEVICE_UNIFORM,
- * lengths in slot 11), so its launches do not depend on cache_len, and a kernel issued
- * after it adds one: a recorded execution therefore replays at every length of a decode
- * loop.  `held` is the value the device array holds after the work issued so far. */
+ * the operator's advancing device-uniform mode (cache_len
+ * MHA_DECODE_CACHE_LEN_DEVICE_ADVANCE, lengths in slot 11), so its launches do not depend
+ * on cache_len and its last kernel adds one: a recorded execution therefore replays at
+ * every length of a decode loop.  `held` is the value the device array holds after the
+ * work issued so far. */
 typedef struct {
     int32_t* lens;   /* device, B entries; NULL until the node first runs on the GPU */
     int64_t  B;
@@ -555,7 +556,7 @@ static int run_node(inference_graph_t* g, int nid, const graph_node_t* n, bool u
         dl = decode_lens_at(g, nid);
         if (!dl || !dl->lens || dl->held != dp->cache_len) return -1;
         dev_params = *dp;
-        dev_params.cache_len = MHA_DECODE_CACHE_LEN_DEVICE_UNIFORM;
+        dev_params.cache_len = MHA_DECODE_CACHE_LEN_DEVICE_ADVANCE;
         if (reserve < MHA_DECODE_SLOT_SEQLENS + 1) reserve = MHA_DECODE_SLOT_SEQLENS + 1;
     }
     if (in_slots < reserve) in_slots = reserve;
@@ -621,9 +622,8 @@ static int run_node(inference_graph_t* g, int nid, const graph_node_t* n, bool u
         stream_t stream = {g->hip_graph};
         const void* params = dev_len ? (const void*)&dev_params : n->params;
         ret = op->func(slots, outs, (const operator_params_t*)params, use_cuda ? &stream : NULL);
-        /* The step is done: its lengths move to the next position. */
-        if (ret == 0 && dev_len && (ret = cf_launch_i32_update(dl->lens, (int32_t)dl->B, 1, 1, g->hip_graph)) == 0)
-            dl->held = dp->cache_len + 1;
+        /* The op's last kernel moved the lengths to the next position. */
+        if (ret == 0 && dev_len) dl->held = dp->cache_len + 1;
     }
     if (ret == 0 && use_cuda && !on_gpu) {
         /* A CPU op wrote host data: device copies are stale.  KV caches stay

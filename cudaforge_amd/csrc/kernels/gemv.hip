@@ -139,6 +139,12 @@ __device__ __forceinline__ void kstep<float>(const cf_gemv_args_t& a, const floa
     }
 }
 
+// The launch's last kernel advances the caller's device lengths (its first workgroup).
+__device__ __forceinline__ void advance_lengths(const cf_gemv_args_t& a) {
+    if (a.advance && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0)
+        for (int i = threadIdx.x; i < a.advance_n; i += blockDim.x) a.advance[i] += 1;
+}
+
 // Store one finished output element (bias added) of segment `seg`, segment-local column n.
 template <typename T>
 __device__ __forceinline__ void store_out(const cf_gemv_args_t& a, const cf_gemv_seg_t& sg, int m, int n, float v) {
@@ -192,6 +198,7 @@ void gemv_kernel(cf_gemv_args_t a, Tiles t) {
         for (int i = 0; i < 4; i++) red[wave * kTileVals + (c * 4 + i) * 64 + l] = acc[c][i];
     __syncthreads();
     const int ncols = t.start[a.nseg] * kColTile;
+    if (a.k_split == 1) advance_lengths(a);
 #pragma unroll
     for (int j = 0; j < kTileVals / kThreads; j++) {
         const int idx = tid + j * kThreads;
@@ -317,6 +324,7 @@ void gemv_f16_dma(cf_gemv_args_t a, Tiles t) {
 
     // Lane (lr, lq) holds Y[m = 16mt + 4lq + i][n0 + 16j + lr].
     if (t.ks == 1) {
+        advance_lengths(a);
 #pragma unroll
         for (int j = 0; j < NT; j++)
 #pragma unroll
@@ -375,6 +383,7 @@ void gemv_reduce4(cf_gemv_args_t a, Tiles t) {
     const int ncols = t.start[a.nseg] * t.bn;
     const size_t plane = (size_t)a.M * ncols;
     const size_t total = (size_t)a.M * (ncols / 4);
+    advance_lengths(a);
     const size_t idx = (size_t)blockIdx.x * kReduceThreads + threadIdx.x;
     if (idx >= total) return;
     const int m = (int)(idx / (ncols / 4));

@@ -113,6 +113,9 @@ typedef struct {
                                  rounded to the k step */
     float*         partials;  /* workspace */
     int32_t        elem;
+    int32_t*       advance;   /* device, may be NULL: the launch's last kernel adds one to
+                                 advance[0 .. advance_n) (nothing in it reads them) */
+    int32_t        advance_n;
 } cf_gemv_args_t;
 
 int32_t cf_gemv_col_tile(int32_t elem);

@@ -31,7 +31,8 @@ void mha_decode_set_split_chunk(int64_t chunk) { g_chunk_override = chunk > 0 ? 
 typedef struct {
     int64_t B, D, H, H_kv, d, max_seq, cache_len;
     int ragged;        /* lengths come from the device array in slot 11 */
-    int lens_uniform;  /* ... and the caller guarantees they are all equal (cache_len -2) */
+    int lens_uniform;  /* ... and the caller guarantees they are all equal (cache_len -2, -3) */
+    int advance;       /* ... and the op adds one to each after the step (cache_len -3) */
 } decode_shape_t;
 
 /* Validation shared by the op and the core entry (mha_decode.c:14-24, plus the GPU
@@ -46,7 +47,8 @@ static int decode_shape(const mha_decode_params_t* p, decode_shape_t* s) {
     s->max_seq = p->max_seq;
     s->cache_len = p->cache_len;
     s->ragged = p->cache_len < 0;
-    s->lens_uniform = p->cache_len == MHA_DECODE_CACHE_LEN_DEVICE_UNIFORM;
+    s->advance = p->cache_len == MHA_DECODE_CACHE_LEN_DEVICE_ADVANCE;
+    s->lens_uniform = p->cache_len == MHA_DECODE_CACHE_LEN_DEVICE_UNIFORM || s->advance;
     if (s->B <= 0 || s->H <= 0 || s->d <= 0 || s->H_kv <= 0 || s->max_seq <= 0) return -1;
     if (s->H % s->H_kv != 0) return -1;
     if (!s->ragged && s->cache_len >= s->max_seq) return -1;
@@ -147,7 +149,7 @@ static int attn_prepare(int elem, const void* inputs[], void* outputs[],
     if (!params || !inputs || !outputs) return -1;
     const mha_decode_params_t* p = (const mha_decode_params_t*)params;
     decode_shape_t s;
-    if (decode_shape(p, &s) != 0) return -1;
+    if (decode_shape(p, &s) != 0 || s.advance) return -1;
     for (int i = 0; i < 3; i++) if (!inputs[i]) return -1;
     if (!outputs[0]) return -1;
     const int32_t* lens = NULL;
@@ -328,6 +330,10 @@ static int decode_op(int elem, const void* inputs[], void* outputs[],
     g2.seg[0] = (cf_gemv_seg_t){inputs[9], inputs[10], outputs[0], s.D, s.D, 0};
     g2.elem = elem;
     g2.k_split = gemv_k_split(elem, s.H * s.d, cf_ceil_div(s.D, tile), m_tiles);
+    if (s.advance) {   /* nothing after the output projection reads the lengths */
+        g2.advance = (int32_t*)lens;
+        g2.advance_n = (int32_t)s.B;
+    }
 
     size_t cur = 0;
     const size_t off_q = cf_ws_take(&cur, (size_t)s.B * s.H * s.d * esz);

@@ -10,9 +10,11 @@
  * appending its new token at position len[b].  cache_len == -2 is the same with the
  * caller's guarantee that all B lengths are equal (a uniform length kept on the device,
  * as graph_execute does so that a recorded step replays at every length): the op then
- * plans and runs as for a uniform length, over max_seq positions.  Device-held lengths
- * cannot be checked on the host: a length >= max_seq appends nothing and attends
- * max_seq positions, a negative one attends position 0 only.
+ * plans and runs as for a uniform length, over max_seq positions.  cache_len == -3 is
+ * -2 for the full op whose last kernel also adds one to each of the B lengths after the
+ * step (a recorded decode step then advances its own position; the attention-only entry
+ * rejects -3).  Device-held lengths cannot be checked on the host: a length >= max_seq
+ * appends nothing and attends max_seq positions, a negative one attends position 0 only.
  */
 #ifndef CF_MHA_DECODE_INT_H_
 #define CF_MHA_DECODE_INT_H_
@@ -34,5 +36,6 @@ typedef struct {
 #define MHA_DECODE_NUM_OUTPUTS  3
 #define MHA_DECODE_SLOT_SEQLENS 11
 #define MHA_DECODE_CACHE_LEN_DEVICE_UNIFORM (-2)
+#define MHA_DECODE_CACHE_LEN_DEVICE_ADVANCE (-3)
 
 #endif /* CF_MHA_DECODE_INT_H_ */

@@ -145,6 +145,36 @@ def test_ragged_lengths(gpu, f16):
     assert max_abs(ref, core) <= tol
 
 
+@pytest.mark.parametrize("f16", [True, False])
+def test_device_held_uniform_length_modes(gpu, f16):
+    """cache_len -2 and -3 (one length for the whole batch, held in a device array in
+    slot 11) give the host-length result; -3 also adds one to every device length after
+    the step and -2 leaves them; the attention-only entry rejects -3."""
+    import cudaforge_amd as cf
+    from helpers import dev
+    B, H, H_kv, d, max_seq, L = 3, 8, 2, 64, 640, 517
+    c = DecodeCase(B, H, H_kv, d, max_seq, cache_len=L, seed=31, f16=f16)
+    want = c.oracle()
+    tol = TOL16 if f16 else TOL32
+    dt = np.float16 if f16 else np.float32
+    name = "mha_decode_f16_cuda" if f16 else "mha_decode_f32_cuda"
+    for mode, step in ((-2, 0), (-3, 1)):
+        bufs = [dev(a, f16) for a in c.arrays()]
+        lens = dev(np.full(B, L, np.int32))
+        Y = cf.DeviceBuffer.empty((B, 1, c.D), dt)
+        p = cf.MhaDecodeParams(B, c.D, H, H_kv, d, float(1 / np.sqrt(d)), mode, max_seq)
+        assert cf.call_op(name, bufs, [Y, bufs[1], bufs[2]], p, None, extra_inputs=[lens]) == 0
+        got = [Y.download(), bufs[1].download(), bufs[2].download()]
+        for w, g in zip(want, got):
+            assert max_abs(w, g.astype(np.float32)) <= tol
+        assert np.array_equal(lens.download(), np.full(B, L + step, np.int32))
+    Q = dev(O.normal((B, H, d), 5), f16)
+    out = cf.DeviceBuffer.empty((B, H, d), dt)
+    p = cf.MhaDecodeParams(B, c.D, H, H_kv, d, float(1 / np.sqrt(d)), -3, max_seq)
+    core = "mha_decode_attn_f16_cuda" if f16 else "mha_decode_attn_f32_cuda"
+    assert cf.call_op(core, [Q, bufs[1], bufs[2]], [out], p, None, extra_inputs=[lens]) == -1
+
+
 def test_split_count_invariance(gpu, native):
     """The result must not depend on how positions are split across workgroups."""
     B, H, H_kv, d, T = 2, 16, 4, 128, 3000
