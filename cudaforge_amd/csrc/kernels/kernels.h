@@ -62,6 +62,9 @@ void    cf_decode_attn_set_wide(int32_t on);
 /* Tests: 1 selects the workgroup-per-row merge for every head size (0 = the one-wave
  * merge for d = 64 / 128). */
 void    cf_decode_attn_set_merge_rows(int32_t on);
+/* Tuning override: rows (one wave each) per workgroup of the one-wave merge, 1..4
+ * (default 2). */
+void    cf_decode_attn_set_merge_wave_wg(int32_t rows);
 /* Workspace floats needed for the partials of a launch. */
 size_t  cf_decode_attn_partials_floats(int32_t B, int32_t H_q, int32_t H_kv, int32_t d,
                                        int32_t n_split, int32_t elem);

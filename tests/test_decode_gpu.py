@@ -585,7 +585,8 @@ def test_split_chunks_longer_than_4096(gpu, native):
                                      (False, 64, 1), (False, 128, 8)])
 def test_merge_kernels_agree(gpu, native, f16, d, G):
     """The one-wave merge (d = 64 / 128, up to 16 splits) and the workgroup-per-row merge
-    on the same partials: both within the bound of the oracle, and close to each other."""
+    on the same partials: both within the bound of the oracle, and close to each other.
+    The one-wave merge gives the same bits with 1, 2 or 4 rows per workgroup."""
     B, H_kv, T = 3, 2, 3000
     H = H_kv * G
     r = O.round_f16 if f16 else (lambda a: a)
@@ -598,9 +599,17 @@ def test_merge_kernels_agree(gpu, native, f16, d, G):
         for rows in (0, 1):
             native.cf_decode_attn_set_merge_rows(rows)
             outs.append(run_decode_attn_gpu(Q, K, V, None, H_kv, f16, seq_lens=lens))
+        native.cf_decode_attn_set_merge_rows(0)
+        per_wg = []
+        for per in (1, 4):
+            native.cf_decode_attn_set_merge_wave_wg(per)
+            per_wg.append(run_decode_attn_gpu(Q, K, V, None, H_kv, f16, seq_lens=lens))
     finally:
+        native.cf_decode_attn_set_merge_wave_wg(2)
         native.cf_decode_attn_set_merge_rows(0)
         native.mha_decode_set_split_chunk(0)
+    for got in per_wg:
+        assert np.array_equal(got, outs[0])
     tol = TOL16 if f16 else TOL32
     for got in outs:
         assert max_abs(want, got) <= tol
