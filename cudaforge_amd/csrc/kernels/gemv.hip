@@ -145,14 +145,29 @@ __device__ __forceinline__ void advance_lengths(const cf_gemv_args_t& a) {
         for (int i = threadIdx.x; i < a.advance_n; i += blockDim.x) a.advance[i] += 1;
 }
 
-// Store one finished output element (bias added) of segment `seg`, segment-local column n.
+// Store one finished output element of segment `seg`, segment-local column n.
+template <typename T>
+__device__ __forceinline__ void store_val(const cf_gemv_args_t& a, const cf_gemv_seg_t& sg, int m, int n, float v) {
+    const int64_t pos = a.pos_lens ? (int64_t)a.pos_lens[m] : a.pos_uniform;
+    if (a.pos_limit == 0 || (pos >= 0 && pos < a.pos_limit))
+        ((T*)sg.out)[(size_t)m * sg.ld_m + (size_t)pos * sg.ld_pos + n] = from_f<T>(v);
+}
+
+// ... with the segment's bias added first.
 template <typename T>
 __device__ __forceinline__ void store_out(const cf_gemv_args_t& a, const cf_gemv_seg_t& sg, int m, int n, float v) {
     const T* __restrict__ bias = (const T*)sg.bias;
     if (bias) v += to_f(bias[n]);
-    const int64_t pos = a.pos_lens ? (int64_t)a.pos_lens[m] : a.pos_uniform;
-    if (a.pos_limit == 0 || (pos >= 0 && pos < a.pos_limit))
-        ((T*)sg.out)[(size_t)m * sg.ld_m + (size_t)pos * sg.ld_pos + n] = from_f<T>(v);
+    store_val<T>(a, sg, m, n, v);
+}
+
+// One RoPE pair, rotated as the rope operator does it (fp32, no contraction).
+__device__ __forceinline__ void rotate_pair(float& x0, float& x1, float2 cs) {
+#pragma clang fp contract(off)
+    const float a = x0 * cs.x, b = x1 * cs.y;
+    const float c = x0 * cs.y, e = x1 * cs.x;
+    x0 = a - b;
+    x1 = c + e;
 }
 
 __device__ __forceinline__ int seg_of(const cf_gemv_args_t& a, const Tiles& t, int tile) {
@@ -405,10 +420,26 @@ void gemv_reduce4(cf_gemv_args_t a, Tiles t) {
     s0 += s1;
     const int tile = col / t.bn;
     const int seg = seg_of(a, t, tile);
+    const cf_gemv_seg_t& sg = a.seg[seg];
     const int n = (tile - t.start[seg]) * t.bn + (col - tile * t.bn);
+    const T* __restrict__ bias = (const T*)sg.bias;
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = bias && n + e < sg.n ? s0[e] + to_f(bias[n + e]) : s0[e];
+    if (a.rope_table && ((a.rope_segs >> seg) & 1)) {
+        // n is a multiple of 4 and rope_d is even, so (n, n+1) and (n+2, n+3) are pairs.
+        const int64_t pos = a.pos_lens ? (int64_t)a.pos_lens[m] : a.pos_uniform;
+        if (pos >= 0 && pos < a.rope_rows) {
+            const int half = a.rope_d >> 1;
+            const float2* tb = (const float2*)a.rope_table + pos * half;
+#pragma unroll
+            for (int e = 0; e < 4; e += 2)
+                if (n + e + 1 < sg.n) rotate_pair(v[e], v[e + 1], tb[((n + e) % a.rope_d) >> 1]);
+        }
+    }
 #pragma unroll
     for (int e = 0; e < 4; e++)
-        if (n + e < a.seg[seg].n) store_out<T>(a, a.seg[seg], m, n + e, s0[e]);
+        if (n + e < sg.n) store_val<T>(a, sg, m, n + e, v[e]);
 }
 
 Tiles make_tiles(const cf_gemv_args_t* a) {
@@ -467,6 +498,8 @@ extern "C" size_t cf_gemv_partials_floats(const cf_gemv_args_t* a) {
 extern "C" int cf_launch_gemv(const cf_gemv_args_t* a, void* stream) {
     const Tiles t = make_tiles(a);
     if (a->M <= 0 || a->K <= 0 || t.start[a->nseg] <= 0) return (int)hipErrorInvalidValue;
+    // RoPE is applied in the K-chunk sum only.
+    if (a->rope_table && (t.ks == 1 || a->rope_d <= 0 || (a->rope_d & 1))) return (int)hipErrorInvalidValue;
     cf_gemv_args_t args = *a;
     args.k_split = t.ks;
     hipStream_t s = (hipStream_t)stream;

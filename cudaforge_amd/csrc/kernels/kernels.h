@@ -119,6 +119,14 @@ typedef struct {
     int32_t*       advance;   /* device, may be NULL: the launch's last kernel adds one to
                                  advance[0 .. advance_n) (nothing in it reads them) */
     int32_t        advance_n;
+    /* RoPE on the stored values, in the K-chunk sum (a launch with k_split 1 rejects it):
+     * in segment s with bit s of rope_segs set, columns (2i, 2i+1) of each rope_d-wide
+     * head are rotated by table[pos * rope_d/2 + i] (cos, sin) after the bias is added,
+     * where pos is the row's position; a position outside [0, rope_rows) is not rotated. */
+    const float*   rope_table;
+    int32_t        rope_d;
+    int32_t        rope_segs;
+    int64_t        rope_rows;
 } cf_gemv_args_t;
 
 int32_t cf_gemv_col_tile(int32_t elem);

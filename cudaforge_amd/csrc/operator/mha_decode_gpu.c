@@ -6,7 +6,8 @@
  * three launches on the caller's stream:
  *   1. projection GEMV: X_new·[WQ | WK | WV] + b; Q goes to the workspace, K_new/V_new
  *      straight into row cache_len (or seq_lens[b]) of the output caches; the RoPE
- *      variant (mha_decode_rope_*) then rotates Q and that K row in place;
+ *      variant (mha_decode_rope_*) rotates Q and that K row as the projection's
+ *      K-chunk sum stores them (or, with a single K chunk, in place afterwards);
  *   2. split-KV attention over positions 0..cache_len with the LSE merge;
  *   3. output GEMV: O·WO + bO -> Y.
  * Temporaries live in the persistent device workspace (no per-call allocation).
@@ -316,6 +317,15 @@ static int decode_op(int elem, const void* inputs[], void* outputs[],
     const int64_t tile = cf_gemv_col_tile(elem);
     const int64_t ct1 = cf_ceil_div(s.H * s.d, tile) + 2 * cf_ceil_div(kvd, tile);
     g1.k_split = gemv_k_split(elem, s.D, ct1, m_tiles);
+    /* RoPE rides in the projection's K-chunk sum when it has one (Q and K_new are rotated
+     * before they are stored); otherwise a kernel of its own rotates them afterwards. */
+    const int fuse_rope = rope_table && cf_gemv_partials_floats(&g1) > 0;
+    if (fuse_rope) {
+        g1.rope_table = rope_table;
+        g1.rope_d = (int32_t)s.d;
+        g1.rope_segs = 3;              /* Q and K */
+        g1.rope_rows = s.max_seq;
+    }
 
     cf_decode_attn_args_t a;
     /* q and o live in the workspace (256-byte aligned). */
@@ -348,7 +358,7 @@ static int decode_op(int elem, const void* inputs[], void* outputs[],
     g1.partials = (float*)(data + off_p1);
     if ((rc = cf_launch_gemv(&g1, st)) != 0) return rc;
 
-    if (rope_table) {
+    if (rope_table && !fuse_rope) {
         cf_rope_decode_args_t r;
         memset(&r, 0, sizeof(r));
         r.q = data + off_q;
