@@ -229,6 +229,19 @@ def test_mha_decode_rope_long_context_gqa_f16(gpu):
 
 
 @pytest.mark.gpu
+def test_mha_decode_rope_config2_full_size(gpu):
+    """Config 2 (B 16, 32/8 heads, d 128, KV 4096, fp16) with RoPE at base 500000, the
+    Llama-3 step: every output row and the appended (rotated) K row of every sequence
+    against the oracle; the rest of the K cache unchanged."""
+    c = DecodeCase(16, 32, 8, 128, 4096, cache_len=4095, seed=17, f16=True)
+    want = _decode_rope_oracle(c, 500000.0)
+    Y, K = _decode_rope_gpu(c, 500000.0)
+    assert max_abs(want[0], Y) <= TOL16
+    assert max_abs(want[1][:, 4095], K[:, 4095]) <= TOL16
+    assert np.array_equal(K[:, :4095], c.Kc[:, :4095])
+
+
+@pytest.mark.gpu
 def test_mha_decode_rope_at_position_zero_equals_decode(gpu):
     from helpers import run_decode_gpu
     c = DecodeCase(2, 4, 4, 32, 16, cache_len=0, seed=13)
