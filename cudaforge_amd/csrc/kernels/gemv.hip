@@ -25,8 +25,10 @@
 //   interleave k steps and reduce through LDS.
 // With one K chunk the workgroup adds the bias and scatters the result; otherwise it
 // writes an fp32 partial per K chunk and a second launch (gemv_reduce4) sums the
-// partials, adds the bias and scatters.  The kernel boundary orders the partials: no
-// fences or atomics (each XCD has its own L2).
+// partials, adds the bias, optionally rotates RoPE pairs (decode's Q and K_new) and
+// scatters.  The kernel boundary orders the partials: no fences or atomics (each XCD
+// has its own L2).  The launch's last kernel can also advance the caller's device-held
+// decode lengths (cf_gemv_args_t.advance), since nothing after it in the step reads them.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
