@@ -111,6 +111,7 @@ def _proto(lib):
         "cf_decode_attn_set_merge_wave_wg": (None, [c_int32]),
         "cf_decode_attn_set_stages": (None, [c_int32]),
         "cf_decode_attn_set_merge_rows": (None, [c_int32]),
+        "cf_decode_attn_set_merge_rows_split": (None, [c_int32]),
         "cf_decode_attn_set_wide": (None, [c_int32]),
         "cf_gemm_set_stages": (None, [c_int32]),
         "cf_gemm_set_group_m": (None, [c_int32]),

@@ -683,23 +683,25 @@ void merge_kernel(cf_decode_attn_args_t a, int Gx, int units_per_b) {
     ((T*)a.o)[idx] = from_f<T>(num / den);
 }
 
-// Row merge (D % 4 == 0): one workgroup per output row (unit, head g).  DV = D/4 threads
-// own 4 dims each; the SG = 256/DV thread groups take splits sg, sg+SG, ... with NB
-// records in flight per thread, so a sequence with hundreds of splits costs a few load
-// rounds instead of one per 16 splits; the SG running results are combined through LDS.
-// The thread groups' results combine in a log-depth tree (a serial pass over them cost
-// ~1.5 us with hundreds of splits; 256 threads measured faster than 1024 per row).
+// Row merge (D % 4 == 0): DS workgroups per output row (unit, head g), each owning
+// D / DS dims.  DV = D / (4 DS) threads own 4 dims each; the SG = 256/DV thread groups
+// take splits sg, sg+SG, ... with NB records in flight per thread, so a sequence with
+// hundreds of splits costs a few load rounds instead of one per 16 splits, and DS > 1
+// spreads a row's records over more CUs.  The SG running results combine through LDS
+// in a log-depth tree that folds the upper half of the live groups onto the lower half,
+// so SG need not be a power of two (a serial pass over them cost ~1.5 us with hundreds
+// of splits; 256 threads measured faster than 1024 per row).
 template <typename T, int NT = kMergeThreads>
 __global__ __launch_bounds__(NT)
-void merge_rows(cf_decode_attn_args_t a, int Gx, int units_per_b) {
-    const int D = a.d, DV = D >> 2, SG = NT / DV;
-    const int row = blockIdx.x;
+void merge_rows(cf_decode_attn_args_t a, int Gx, int units_per_b, int ds) {
+    const int D = a.d, DV = D / (4 * ds), SG = NT / DV;
+    const int row = blockIdx.x / ds, part = blockIdx.x - row * ds;
     const int g = row % Gx, unit = row / Gx, b = unit / units_per_b;
     const int stride = part_stride(Gx, D), hdr = part_hdr(Gx);
     const SplitRecords sr = split_records(a, b, unit, units_per_b, stride);
     const int nsplit = sr.n;
     if (nsplit <= 1) return;                       // finished by the split kernel
-    const int tid = threadIdx.x, col = tid % DV, sg = tid / DV;
+    const int tid = threadIdx.x, col = part * DV + tid % DV, sg = tid / DV;
     __shared__ float sm[NT], sd[NT];
     __shared__ f4_t sn[NT];
     float M = -INFINITY, den = 0.0f;
@@ -734,14 +736,16 @@ void merge_rows(cf_decode_attn_args_t a, int Gx, int units_per_b) {
             M = m_new;
         }
     }
-    // The SG groups' (M, den, num) of each column combine in a tree through LDS.
+    // The SG groups' (M, den, num) of each column combine in a tree through LDS: with n
+    // groups live, groups [h, n) (h = ceil(n / 2)) fold onto groups [0, n - h).
     sm[tid] = M;
     sd[tid] = den;
     sn[tid] = num;
     __syncthreads();
-    for (int half = SG / 2; half >= 1; half >>= 1) {
-        if (sg < half) {
-            const int o = tid + half * DV;
+    for (int n = SG; n > 1;) {
+        const int h = (n + 1) >> 1;
+        if (sg < n - h) {
+            const int o = tid + h * DV;
             const float m1 = sm[tid], m2 = sm[o];
             const float mx = fmaxf(m1, m2);
             const float w1 = m1 == -INFINITY ? 0.0f : exp2f(m1 - mx);
@@ -751,6 +755,7 @@ void merge_rows(cf_decode_attn_args_t a, int Gx, int units_per_b) {
             sn[tid] = w1 * sn[tid] + w2 * sn[o];
         }
         __syncthreads();
+        n = h;
     }
     if (sg == 0) {
         T* out = (T*)a.o + (size_t)row * D + 4 * col;
@@ -835,6 +840,19 @@ bool use_fast(const cf_decode_attn_args_t* a) {
 
 int g_stages = 0;   // tuning override of the fp16 ring depth (2..4; 0 = kDecodeStages)
 int g_merge_rows = 0;   // 1: use the workgroup-per-row merge for every head size (tests)
+int g_merge_rows_ds = -1;   // tuning override of merge_rows' workgroups per row (-1 = automatic)
+
+// Workgroups per row of merge_rows: the largest of 1, 2, 4 that divides d / 4 and leaves
+// at least 16 threads (64 dims) per thread group.  Ragged config 4 (d = 128, up to ~100
+// records per row) measured a 5.0 us merge at 2 per row against 5.7 us at 1 and 5.5 us
+// at 4.
+int merge_rows_dsplit(int d) {
+    const int dv = d / 4;
+    if (g_merge_rows_ds > 0 && dv % g_merge_rows_ds == 0) return g_merge_rows_ds;
+    for (int ds = 4; ds > 1; ds >>= 1)
+        if (dv % ds == 0 && dv / ds >= 16) return ds;
+    return 1;
+}
 int g_merge_wave_wg = 2; // rows (waves) per merge_wave workgroup (2 and 1 measured 0.15-0.2 us faster than 4)
 
 int g_wide = 1;     // 0: one workgroup per (split, KV head) even where the grouped kernel applies
@@ -903,6 +921,7 @@ extern "C" int32_t cf_decode_attn_chunk_quantum(int32_t elem, int32_t d, int32_t
 extern "C" void cf_decode_attn_set_stages(int32_t stages) { g_stages = stages; }
 
 extern "C" void cf_decode_attn_set_merge_rows(int32_t on) { g_merge_rows = on != 0; }
+extern "C" void cf_decode_attn_set_merge_rows_split(int32_t ds) { g_merge_rows_ds = ds >= 1 && ds <= 4 ? ds : -1; }
 extern "C" void cf_decode_attn_set_merge_wave_wg(int32_t rows) { g_merge_wave_wg = rows >= 1 && rows <= 4 ? rows : 2; }
 
 extern "C" void cf_decode_attn_set_wide(int32_t on) { g_wide = on != 0; }
@@ -978,11 +997,12 @@ extern "C" int cf_launch_decode_attn_merge(const cf_decode_attn_args_t* a, void*
         return (int)hipGetLastError();
     }
     if (a->d % 4 == 0 && a->d / 4 <= kMergeThreads) {
-        dim3 grid((unsigned)((size_t)a->B * units_per_b * Gx));
+        const int ds = merge_rows_dsplit(a->d);
+        dim3 grid((unsigned)((size_t)a->B * units_per_b * Gx * ds));
         if (a->elem == CF_ELEM_F16)
-            hipLaunchKernelGGL((merge_rows<_Float16>), grid, dim3(kMergeThreads), 0, s, *a, Gx, units_per_b);
+            hipLaunchKernelGGL((merge_rows<_Float16>), grid, dim3(kMergeThreads), 0, s, *a, Gx, units_per_b, ds);
         else
-            hipLaunchKernelGGL((merge_rows<float>), grid, dim3(kMergeThreads), 0, s, *a, Gx, units_per_b);
+            hipLaunchKernelGGL((merge_rows<float>), grid, dim3(kMergeThreads), 0, s, *a, Gx, units_per_b, ds);
         return (int)hipGetLastError();
     }
     const size_t total = (size_t)a->B * units_per_b * Gx * a->d;

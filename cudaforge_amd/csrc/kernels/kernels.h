@@ -62,6 +62,9 @@ void    cf_decode_attn_set_wide(int32_t on);
 /* Tests: 1 selects the workgroup-per-row merge for every head size (0 = the one-wave
  * merge for d = 64 / 128). */
 void    cf_decode_attn_set_merge_rows(int32_t on);
+/* Tuning override: workgroups per row of the row merge, 1, 2 or 4 dividing d / 4
+ * (0 = automatic: up to 4, keeping at least 64 dims per workgroup). */
+void    cf_decode_attn_set_merge_rows_split(int32_t ds);
 /* Tuning override: rows (one wave each) per workgroup of the one-wave merge, 1..4
  * (default 2). */
 void    cf_decode_attn_set_merge_wave_wg(int32_t rows);

@@ -76,8 +76,12 @@ def test_config1_gpt2_small_f32(gpu):
 
 @pytest.mark.parametrize("f16", [False, True])
 @pytest.mark.parametrize("H,H_kv,d,T", [(8, 8, 64, 333), (8, 4, 128, 700), (16, 4, 128, 1030),
-                                         (16, 2, 64, 129), (8, 1, 128, 64), (6, 2, 32, 250), (4, 4, 80, 90)])
+                                         (16, 2, 64, 129), (8, 1, 128, 64), (6, 2, 32, 250), (4, 4, 80, 90),
+                                         (4, 4, 80, 1000), (4, 2, 96, 777), (4, 4, 48, 600)])
 def test_attn_core_vs_oracle(gpu, f16, H, H_kv, d, T):
+    """Head sizes off the MFMA path (80, 96, 48) with 10-16 splits take the row merge
+    with 12, 10 and 21 thread groups: its LDS tree must fold a group count that is not a
+    power of two (a tree that halved 12 groups as 6, 3, 1 dropped group 2's splits)."""
     B, max_seq = 3, T + 5
     Q = O.normal((B, H, d), 7 + d)
     K = O.normal((B, max_seq, H_kv, d), 8 + H)
@@ -584,9 +588,10 @@ def test_split_chunks_longer_than_4096(gpu, native):
 @pytest.mark.parametrize("f16,d,G", [(True, 128, 4), (True, 64, 2), (True, 64, 8), (True, 128, 1),
                                      (False, 64, 1), (False, 128, 8)])
 def test_merge_kernels_agree(gpu, native, f16, d, G):
-    """The one-wave merge (d = 64 / 128, up to 16 splits) and the workgroup-per-row merge
-    on the same partials: both within the bound of the oracle, and close to each other.
-    The one-wave merge gives the same bits with 1, 2 or 4 rows per workgroup."""
+    """The one-wave merge (d = 64 / 128, up to 16 splits) and the row merge on the same
+    partials: both within the bound of the oracle, and close to each other.  The one-wave
+    merge gives the same bits with 1, 2 or 4 rows per workgroup; the row merge with 1, 2
+    or 4 workgroups per row (each a different summation tree) stays within the bound."""
     B, H_kv, T = 3, 2, 3000
     H = H_kv * G
     r = O.round_f16 if f16 else (lambda a: a)
@@ -599,6 +604,10 @@ def test_merge_kernels_agree(gpu, native, f16, d, G):
         for rows in (0, 1):
             native.cf_decode_attn_set_merge_rows(rows)
             outs.append(run_decode_attn_gpu(Q, K, V, None, H_kv, f16, seq_lens=lens))
+        for ds in (1, 2, 4):
+            native.cf_decode_attn_set_merge_rows_split(ds)
+            outs.append(run_decode_attn_gpu(Q, K, V, None, H_kv, f16, seq_lens=lens))
+        native.cf_decode_attn_set_merge_rows_split(0)
         native.cf_decode_attn_set_merge_rows(0)
         per_wg = []
         for per in (1, 4):
@@ -606,6 +615,7 @@ def test_merge_kernels_agree(gpu, native, f16, d, G):
             per_wg.append(run_decode_attn_gpu(Q, K, V, None, H_kv, f16, seq_lens=lens))
     finally:
         native.cf_decode_attn_set_merge_wave_wg(2)
+        native.cf_decode_attn_set_merge_rows_split(0)
         native.cf_decode_attn_set_merge_rows(0)
         native.mha_decode_set_split_chunk(0)
     for got in per_wg:
@@ -613,4 +623,5 @@ def test_merge_kernels_agree(gpu, native, f16, d, G):
     tol = TOL16 if f16 else TOL32
     for got in outs:
         assert max_abs(want, got) <= tol
-    assert max_abs(outs[0], outs[1]) <= tol
+    for got in outs[1:]:
+        assert max_abs(outs[0], got) <= tol
