@@ -108,6 +108,7 @@ def _proto(lib):
         "mha_decode_set_split_chunk": (None, [c_int64]),
         "cf_gemv_set_dma_tile": (None, [c_int32]),
         "cf_gemv_set_dma_ksplit": (None, [c_int32]),
+        "cf_gemv_set_small": (None, [c_int32]),
         "cf_decode_attn_set_merge_wave_wg": (None, [c_int32]),
         "cf_decode_attn_set_stages": (None, [c_int32]),
         "cf_decode_attn_set_merge_rows": (None, [c_int32]),

@@ -33,6 +33,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "kernels.h"
 #include "cdna4.h"
 
@@ -58,6 +60,7 @@ struct Tiles {
     int bn;                           // columns per tile
     int ks;                           // K chunks (workgroups along K)
     int dma;                          // fp16 DMA path: its tile width (64/128/256), else 0
+    int small;                        // one-pass kernel for small projections (gemv_small)
 };
 
 __device__ __forceinline__ float to_f(float x) { return x; }
@@ -444,8 +447,170 @@ void gemv_reduce4(cf_gemv_args_t a, Tiles t) {
         if (n + e < sg.n) store_val<T>(a, sg, m, n + e, v[e]);
 }
 
+// ---- small projections (a few batch rows, weights of a few MB, e.g. GPT-2-small
+// decode at batch 1): one pass over all of K, so no partials and no second launch; at
+// that size the fixed cost of the extra launch is most of the time.  A workgroup owns
+// kSmallCols = 16 columns and its 4 waves a quarter of K each.  A lane loads 16 bytes of
+// a W row (VEC columns; LPR lanes per row, RPI = 64 / LPR rows per wave instruction),
+// NB rows in flight, and multiplies them with X staged in LDS (fp32).  The first batch
+// of W loads is issued before X is staged, so both arrive in one round trip.  Lanes of
+// one column group then sum over their rows with shuffles, the waves through LDS, and
+// M * 4 threads add the bias, rotate RoPE pairs and store 4 columns each.
+constexpr int kSmallCols = 16;
+constexpr int kSmallMaxM = 4;
+constexpr int kSmallMaxX = 4096;                  // M * K floats of X staged in LDS
+constexpr long long kSmallMaxBytes = 8ll << 20;   // weight bytes up to which the path is taken
+template <typename T>
+__global__ __launch_bounds__(kThreads)
+void gemv_small(cf_gemv_args_t a, Tiles t) {
+    constexpr int VEC = 16 / (int)sizeof(T);
+    constexpr int LPR = kSmallCols / VEC;         // lanes per W row
+    constexpr int RPI = 64 / LPR;                 // rows per wave instruction
+    constexpr int NB = sizeof(T) == 4 ? 16 : 8;   // row loads in flight per lane
+    using V = std::conditional_t<sizeof(T) == 4, f4_t, h8_t>;
+    __shared__ float xs[kSmallMaxX];
+    __shared__ float wsum[kWaves][kSmallMaxM][kSmallCols];
+    const int tile = blockIdx.x;
+    const int seg = seg_of(a, t, tile);
+    const cf_gemv_seg_t& sg = a.seg[seg];
+    const int N = (int)sg.n;
+    const int nb = (tile - t.start[seg]) * kSmallCols;
+    const T* __restrict__ W = (const T*)sg.w + nb;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane / LPR, c = lane % LPR;
+    const int M = a.M, K = a.K;
+    const int kq = (K + kWaves * RPI - 1) / (kWaves * RPI) * RPI;   // rows per wave
+    const int k_lo = wave * kq, k_hi = min(K, k_lo + kq);
+    V w[NB];
+    auto load_batch = [&](int r0) {
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            const int k = min(r0 + j * RPI + lr, K - 1);
+            w[j] = *(const V*)(W + (size_t)k * N + c * VEC);
+        }
+    };
+    if (k_lo < k_hi) load_batch(k_lo);
+    // The storing threads' bias, position and RoPE angles are loaded now as well, not
+    // after the sums, where they would cost another round trip.
+    const int store_m = tid / (kSmallCols / 4), n = nb + 4 * (tid % (kSmallCols / 4));
+    const bool storer = tid < M * (kSmallCols / 4);
+    const T* __restrict__ bias = (const T*)sg.bias;
+    float bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    int64_t pos = a.pos_uniform;
+    float2 rot[2] = {{1.0f, 0.0f}, {1.0f, 0.0f}};
+    bool rotate = false;
+    if (storer) {
+        if (bias)
+#pragma unroll
+            for (int e = 0; e < 4; e++) bv[e] = to_f(bias[n + e]);
+        if (a.pos_lens) pos = a.pos_lens[store_m];
+        if (a.rope_table && ((a.rope_segs >> seg) & 1) && pos >= 0 && pos < a.rope_rows) {
+            // n is a multiple of 4 and rope_d is even, so (n, n+1) and (n+2, n+3) are pairs.
+            const float2* tb = (const float2*)a.rope_table + pos * (a.rope_d >> 1);
+            rot[0] = tb[(n % a.rope_d) >> 1];
+            rot[1] = tb[((n + 2) % a.rope_d) >> 1];
+            rotate = true;
+        }
+    }
+    {
+        // Every X load is issued before the first LDS store, so they share the W loads'
+        // round trip.
+        constexpr int XPT = kSmallMaxX / kThreads;
+        const T* __restrict__ xg = (const T*)a.x;
+        const int nx = M * K;
+        T xv[XPT];
+#pragma unroll
+        for (int j = 0; j < XPT; j++) xv[j] = xg[min(tid + j * kThreads, nx - 1)];
+#pragma unroll
+        for (int j = 0; j < XPT; j++)
+            if (tid + j * kThreads < nx) xs[tid + j * kThreads] = to_f(xv[j]);
+    }
+    __syncthreads();
+    float acc[kSmallMaxM][VEC];
+#pragma unroll
+    for (int m = 0; m < kSmallMaxM; m++)
+#pragma unroll
+        for (int v = 0; v < VEC; v++) acc[m][v] = 0.0f;
+    for (int r0 = k_lo; r0 < k_hi; r0 += NB * RPI) {
+        if (r0 != k_lo) load_batch(r0);
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            const int k = r0 + j * RPI + lr;
+            if (k < k_hi) {
+#pragma unroll
+                for (int m = 0; m < kSmallMaxM; m++) {
+                    if (m >= M) break;
+                    const float xv = xs[m * K + k];
+#pragma unroll
+                    for (int v = 0; v < VEC; v++) acc[m][v] = __builtin_fmaf(to_f(w[j][v]), xv, acc[m][v]);
+                }
+            }
+        }
+    }
+    // Sum over the rows of the wave (lanes with the same column group c), then store the
+    // wave's 16 column sums per batch row.
+#pragma unroll
+    for (int m = 0; m < kSmallMaxM; m++) {
+        if (m >= M) break;
+#pragma unroll
+        for (int v = 0; v < VEC; v++) {
+#pragma unroll
+            for (int off = LPR; off < 64; off <<= 1) acc[m][v] += __shfl_xor(acc[m][v], off, 64);
+            if (lr == 0) wsum[wave][m][c * VEC + v] = acc[m][v];
+        }
+    }
+    __syncthreads();
+    advance_lengths(a);
+    if (!storer) return;
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        float x = 0.0f;
+#pragma unroll
+        for (int q = 0; q < kWaves; q++) x += wsum[q][store_m][n - nb + e];
+        v[e] = bias ? x + bv[e] : x;
+    }
+    if (rotate) {
+        rotate_pair(v[0], v[1], rot[0]);
+        rotate_pair(v[2], v[3], rot[1]);
+    }
+    if (a.pos_limit == 0 || (pos >= 0 && pos < a.pos_limit)) {
+        T* out = (T*)sg.out + (size_t)store_m * sg.ld_m + (size_t)pos * sg.ld_pos + n;
+#pragma unroll
+        for (int e = 0; e < 4; e++) out[e] = from_f<T>(v[e]);
+    }
+}
+
+int g_small = 1;    // 0: never take gemv_small; 1: for small weights; 2: wherever it applies
+
+int small_ok(const cf_gemv_args_t* a) {
+    if (g_small == 0 || a->M > kSmallMaxM || (long long)a->M * a->K > kSmallMaxX) return 0;
+    if (((uintptr_t)a->x) % 4 != 0) return 0;
+    const long long esz = a->elem == CF_ELEM_F16 ? 2 : 4;
+    long long bytes = 0;
+    for (int s = 0; s < a->nseg; s++) {
+        if (a->seg[s].n % kSmallCols != 0 || ((uintptr_t)a->seg[s].w) % 16 != 0) return 0;
+        bytes += (long long)a->K * a->seg[s].n * esz;
+    }
+    return g_small == 2 || bytes <= kSmallMaxBytes;
+}
+
 Tiles make_tiles(const cf_gemv_args_t* a) {
     Tiles t{};
+    if (small_ok(a)) {
+        t.small = 1;
+        t.bn = kSmallCols;
+        int acc = 0;
+        for (int s = 0; s < a->nseg; s++) {
+            t.start[s] = acc;
+            acc += (int)(a->seg[s].n / kSmallCols);
+        }
+        for (int s = a->nseg; s <= CF_GEMV_MAX_SEGS; s++) t.start[s] = acc;
+        t.ks = 1;
+        t.k_chunk = a->K;
+        t.vec_ok = 1;
+        return t;
+    }
     const int bn = dma_bn(a);
     t.dma = bn;
     t.bn = bn ? bn : kColTile;
@@ -498,6 +663,11 @@ Tiles make_tiles(const cf_gemv_args_t* a) {
 extern "C" int32_t cf_gemv_col_tile(int32_t elem) { (void)elem; return kColTile; }
 extern "C" void cf_gemv_set_dma_tile(int32_t bn) { g_dma_bn = bn; }
 extern "C" void cf_gemv_set_dma_ksplit(int32_t ks) { g_dma_ks = ks; }
+extern "C" void cf_gemv_set_small(int32_t mode) { g_small = mode >= 0 && mode <= 2 ? mode : 1; }
+extern "C" int32_t cf_gemv_fuses_rope(const cf_gemv_args_t* a) {
+    const Tiles t = make_tiles(a);
+    return t.small || t.ks > 1 ? 1 : 0;
+}
 extern "C" int32_t cf_gemv_k_step(int32_t elem) {
     return elem == CF_ELEM_F16 ? Cfg<_Float16>::KSTEP : Cfg<float>::KSTEP;
 }
@@ -511,11 +681,19 @@ extern "C" size_t cf_gemv_partials_floats(const cf_gemv_args_t* a) {
 extern "C" int cf_launch_gemv(const cf_gemv_args_t* a, void* stream) {
     const Tiles t = make_tiles(a);
     if (a->M <= 0 || a->K <= 0 || t.start[a->nseg] <= 0) return (int)hipErrorInvalidValue;
-    // RoPE is applied in the K-chunk sum only.
-    if (a->rope_table && (t.ks == 1 || a->rope_d <= 0 || (a->rope_d & 1))) return (int)hipErrorInvalidValue;
+    // RoPE is applied in the K-chunk sum or the one-pass small kernel only.
+    if (a->rope_table && ((t.ks == 1 && !t.small) || a->rope_d <= 0 || (a->rope_d & 1)))
+        return (int)hipErrorInvalidValue;
     cf_gemv_args_t args = *a;
     args.k_split = t.ks;
     hipStream_t s = (hipStream_t)stream;
+    if (t.small) {
+        if (a->elem == CF_ELEM_F16)
+            hipLaunchKernelGGL(gemv_small<_Float16>, dim3((unsigned)t.start[a->nseg]), dim3(kThreads), 0, s, args, t);
+        else
+            hipLaunchKernelGGL(gemv_small<float>, dim3((unsigned)t.start[a->nseg]), dim3(kThreads), 0, s, args, t);
+        return (int)hipGetLastError();
+    }
     const int m_tiles = (a->M + kMTile - 1) / kMTile;
     dim3 grid((unsigned)t.start[a->nseg], (unsigned)t.ks, (unsigned)m_tiles);
     if (t.dma == 256)

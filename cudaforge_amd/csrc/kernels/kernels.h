@@ -116,13 +116,15 @@ typedef struct {
     int64_t        pos_limit; /* rows whose pos is outside [0, pos_limit) are not stored;
                                  0 = no limit */
     int32_t        k_split;   /* 1..32 (larger is taken as 32); K chunk = ceil(K / k_split)
-                                 rounded to the k step */
+                                 rounded to the k step (the fp16 DMA path and the small
+                                 one-pass kernel plan their own) */
     float*         partials;  /* workspace */
     int32_t        elem;
     int32_t*       advance;   /* device, may be NULL: the launch's last kernel adds one to
                                  advance[0 .. advance_n) (nothing in it reads them) */
     int32_t        advance_n;
-    /* RoPE on the stored values, in the K-chunk sum (a launch with k_split 1 rejects it):
+    /* RoPE on the stored values, in the K-chunk sum or the small one-pass kernel (other
+     * single-chunk launches reject it, see cf_gemv_fuses_rope):
      * in segment s with bit s of rope_segs set, columns (2i, 2i+1) of each rope_d-wide
      * head are rotated by table[pos * rope_d/2 + i] (cos, sin) after the bias is added,
      * where pos is the row's position; a position outside [0, rope_rows) is not rotated. */
@@ -141,6 +143,13 @@ int     cf_launch_gemv(const cf_gemv_args_t* a, void* stream);
 void    cf_gemv_set_dma_tile(int32_t bn);
 /* Tuning override of the fp16 DMA path's K split (1..32; 0 = automatic). */
 void    cf_gemv_set_dma_ksplit(int32_t ks);
+/* The one-pass kernel for small projections (M <= 4, M * K <= 4096, every segment width
+ * a multiple of 16, weights of at most 8 MB): 0 never, 1 automatic (default), 2 wherever
+ * the shape allows it whatever the weight size (tests). */
+void    cf_gemv_set_small(int32_t mode);
+/* 1 when a launch with these arguments can apply RoPE (rope_table): the K-chunk sum or
+ * the one-pass small kernel runs it; a single-chunk split-K launch cannot. */
+int32_t cf_gemv_fuses_rope(const cf_gemv_args_t* a);
 
 /* ---------------------------------------------------------------------------------
  * Prefill GEMM with fused epilogue: C = A·W + bias (+ residual), A (M, K) row-major,

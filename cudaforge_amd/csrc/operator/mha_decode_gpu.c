@@ -319,7 +319,7 @@ static int decode_op(int elem, const void* inputs[], void* outputs[],
     g1.k_split = gemv_k_split(elem, s.D, ct1, m_tiles);
     /* RoPE rides in the projection's K-chunk sum when it has one (Q and K_new are rotated
      * before they are stored); otherwise a kernel of its own rotates them afterwards. */
-    const int fuse_rope = rope_table && cf_gemv_partials_floats(&g1) > 0;
+    const int fuse_rope = rope_table && cf_gemv_fuses_rope(&g1);
     if (fuse_rope) {
         g1.rope_table = rope_table;
         g1.rope_d = (int32_t)s.d;

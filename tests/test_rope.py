@@ -195,11 +195,13 @@ def test_mha_decode_rope_matches_oracle(gpu, f16, ragged):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("f16", [True, False])
-def test_mha_decode_rope_fused_and_separate_rotation(gpu, native, f16):
-    """The rotation done in the projection's K-chunk sum (where the projection splits K)
-    and by the separate rotation kernel after a single-chunk projection: both within the
-    bound of the oracle.  fp16: the projection's K split forced to one chunk, then
-    automatic; fp32: hidden size 16 plans one chunk, 512 several."""
+@pytest.mark.parametrize("small", [0, 2])
+def test_mha_decode_rope_fused_and_separate_rotation(gpu, native, f16, small):
+    """The rotation done in the projection's K-chunk sum (where the projection splits K),
+    by the separate rotation kernel after a single-chunk projection, and in the one-pass
+    small projection kernel: each within the bound of the oracle.  small = 0 keeps the
+    split-K kernels (fp16: K split forced to one chunk, then automatic; fp32: hidden size
+    16 plans one chunk, 512 several); small = 2 runs the same cases on the one-pass kernel."""
     tol = TOL16 if f16 else TOL32
     if f16:
         cases = [(DecodeCase(3, 8, 2, 64, 300, cache_len=257, seed=14, f16=True), ks) for ks in (1, 0)]
@@ -207,6 +209,7 @@ def test_mha_decode_rope_fused_and_separate_rotation(gpu, native, f16):
         cases = [(DecodeCase(2, 1, 1, 16, 100, cache_len=77, seed=15), 0),
                  (DecodeCase(2, 8, 8, 64, 100, cache_len=77, seed=16), 0)]
     try:
+        native.cf_gemv_set_small(small)
         for c, ks in cases:
             native.cf_gemv_set_dma_ksplit(ks)
             Y, K = _decode_rope_gpu(c, 10000.0)
@@ -215,6 +218,7 @@ def test_mha_decode_rope_fused_and_separate_rotation(gpu, native, f16):
             assert max_abs(want[1], K) <= tol
     finally:
         native.cf_gemv_set_dma_ksplit(0)
+        native.cf_gemv_set_small(1)
 
 
 @pytest.mark.gpu
