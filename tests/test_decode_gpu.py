@@ -111,12 +111,13 @@ def test_full_decode_f16(gpu, B, H, H_kv, d, max_seq, cl):
 
 @pytest.mark.parametrize("f16", [False, True])
 @pytest.mark.parametrize("B,H,H_kv,d,max_seq,cl", [(1, 12, 12, 64, 1024, 1023), (4, 8, 2, 64, 200, 150),
-                                                   (3, 2, 1, 16, 40, 0)])
+                                                   (3, 2, 1, 16, 40, 0), (4, 16, 4, 64, 64, 31)])
 def test_full_decode_small_projection_paths(gpu, native, f16, B, H, H_kv, d, max_seq, cl):
     """The one-pass projection kernel for small weights (batch rows <= 4) and the split-K
     kernels with their reduce on the same op: both within the bound of the oracle for
     the output and the appended cache rows, at config 1's shape (batch 1, 12 heads,
-    d 64), a GQA shape with batch 4, and projection widths of 32 and 16 columns."""
+    d 64), a GQA shape with batch 4, projection widths of 32 and 16 columns, and batch
+    4 x hidden 1024, where X fills the kernel's 4096-float LDS stage exactly."""
     c = DecodeCase(B, H, H_kv, d, max_seq, cache_len=cl, seed=B + 7 * H, f16=f16)
     want = c.oracle()
     tol = TOL16 if f16 else TOL32
