@@ -287,6 +287,7 @@ void graph_destroy(inference_graph_t* g) {
     }
     decode_lens_free(g);
     pinned_free(g);
+    free(g->fused_away);
     for (int i = 0; i < g->num_nodes; i++) {
         free(g->nodes[i].input_tensors);
         free(g->nodes[i].output_tensors);
@@ -551,6 +552,11 @@ static int run_node(inference_graph_t* g, int nid, const graph_node_t* n, bool u
             if (v < 0 || v >= dp->max_seq) return -1;
         }
     }
+    /* Per-sequence lengths change between steps: their host copy, checked above, is
+     * uploaded on every GPU execution, which a recording could not repeat, so such a
+     * step is not recorded (the graph then runs eagerly until the mode changes). */
+    const int ragged_lens = on_gpu && dp && dp->cache_len < 0 && n->num_weights >= 9;
+    if (ragged_lens && recording) return -1;
     if (dev_len) {
         if (!recording && (ret = decode_lens_sync(g, nid)) != 0) return ret;
         dl = decode_lens_at(g, nid);
@@ -566,7 +572,6 @@ static int run_node(inference_graph_t* g, int nid, const graph_node_t* n, bool u
     if (!slots) return -1;
     void** outs = (void**)&slots[in_slots];
     for (int i = n->num_inputs + n->num_weights; i < in_slots; i++) slots[i] = NULL;
-    if (dev_len) slots[MHA_DECODE_SLOT_SEQLENS] = dl->lens;
 
     for (int i = 0; i < n->num_inputs && ret == 0; i++) {
         const int tid = n->input_tensors[i];
@@ -593,13 +598,22 @@ static int run_node(inference_graph_t* g, int nid, const graph_node_t* n, bool u
         slots[n->num_inputs + w] = NULL;
         if (!t) continue;
         if (on_gpu) {
-            copied |= !t->data_device;
-            if (tensor_copy_to_device(t) != 0) ret = -1;
+            if (ragged_lens && w == 8) {
+                copied = 1;
+                if (tensor_upload(t) != 0) ret = -1;
+            } else {
+                copied |= !t->data_device;
+                if (tensor_copy_to_device(t) != 0) ret = -1;
+            }
             slots[n->num_inputs + w] = t->data_device;
         } else {
             slots[n->num_inputs + w] = t->data;
         }
     }
+    /* A uniform length runs from the node's device-held lengths, never from a 9th
+     * weight the node may also carry for its ragged steps (that weight is left as the
+     * caller wrote it). */
+    if (dev_len) slots[MHA_DECODE_SLOT_SEQLENS] = dl->lens;
     for (int i = 0; i < n->num_outputs && ret == 0; i++) {
         const int tid = n->output_tensors[i];
         outs[i] = NULL;
@@ -690,6 +704,51 @@ static void decode_lens_replayed(inference_graph_t* g) {
     }
 }
 
+/* Permanent fusion (graph_set_permanent_fusion): node m->out_node becomes the match's
+ * OP_MHA_FUSED node and the match's other nodes are marked absorbed.  The fused node
+ * keeps its id, its output tensor and so its place in the topological order; its new
+ * inputs (X, the residual) are produced before the pattern's last node, which read
+ * them too.  Returns -1 (graph unchanged) if memory runs out. */
+static int make_fusion_permanent(inference_graph_t* g, const graph_mha_match_t* m) {
+    if (g->fused_away_cap < g->num_nodes) {
+        unsigned char* p = (unsigned char*)realloc(g->fused_away, (size_t)g->num_nodes);
+        if (!p) return -1;
+        memset(p + g->fused_away_cap, 0, (size_t)(g->num_nodes - g->fused_away_cap));
+        g->fused_away = p;
+        g->fused_away_cap = g->num_nodes;
+    }
+    int* in = (int*)malloc(2 * sizeof(int));
+    int* out = (int*)malloc(sizeof(int));
+    tensor_t** w = (tensor_t**)malloc(8 * sizeof(tensor_t*));
+    mha_fused_params_t* fp = (mha_fused_params_t*)malloc(sizeof(mha_fused_params_t));
+    if (!in || !out || !w || !fp) {
+        free(in); free(out); free(w); free(fp);
+        return -1;
+    }
+    in[0] = m->input_tid;
+    in[1] = m->residual_tid;
+    out[0] = m->output_tid;
+    memcpy(w, m->weights, 8 * sizeof(tensor_t*));
+    *fp = m->params;
+    graph_node_t* n = &g->nodes[m->out_node];
+    free(n->input_tensors);
+    free(n->output_tensors);
+    free(n->weights);
+    free(n->params);
+    n->type = OP_MHA_FUSED;
+    n->num_inputs = 2;
+    n->input_tensors = in;
+    n->num_outputs = 1;
+    n->output_tensors = out;
+    n->num_weights = 8;
+    n->weights = w;
+    n->params = fp;
+    n->params_size = sizeof(*fp);
+    for (int i = 0; i < m->num_nodes; i++)
+        if (m->nodes[i] != m->out_node) g->fused_away[m->nodes[i]] = 1;
+    return 0;
+}
+
 /* Runs every node once, in topological order, with MHA subgraph fusion on GPU
  * executions.  *all_gpu tells whether every node ran on the GPU. */
 static int run_nodes(inference_graph_t* g, bool use_cuda, unsigned char* fresh, int* all_gpu, int recording) {
@@ -705,6 +764,13 @@ static int run_nodes(inference_graph_t* g, bool use_cuda, unsigned char* fresh, 
         fused_at = (int*)malloc((size_t)g->num_nodes * sizeof(int));
         if (!fz || !fused_at) { free(fz); free(fused_at); return -1; }
         n_fused = graph_detect_mha(g, fz, cap);
+        if (g->permanent_fusion && n_fused > 0) {
+            /* Rewrite once; this and every later execution run the fused nodes as
+             * ordinary nodes. */
+            for (int k = 0; k < n_fused; k++)
+                if (make_fusion_permanent(g, &fz[k]) != 0) { free(fz); free(fused_at); return -1; }
+            n_fused = 0;
+        }
         for (int i = 0; i < g->num_nodes; i++) fused_at[i] = -1;
         for (int k = 0; k < n_fused; k++)
             for (int i = 0; i < fz[k].num_nodes; i++)
@@ -716,6 +782,7 @@ static int run_nodes(inference_graph_t* g, bool use_cuda, unsigned char* fresh, 
         const int nid = g->topo_order[oi];
         graph_node_t* n = &g->nodes[nid];
         if (n->type == OP_INPUT || n->type == OP_OUTPUT) continue;
+        if (nid < g->fused_away_cap && g->fused_away[nid]) continue;
         if (fused_at && fused_at[nid] == -2) continue;
         int gpu = 0;
         if (fused_at && fused_at[nid] >= 0) {

@@ -181,10 +181,10 @@ static int match_at(const inference_graph_t* g, const unsigned char* used, int x
     int cur = out0(g, attn);
     int nx = sole_reader(g, cur, used);
     if (!is(g, nx, OP_MUL) || g->nodes[nx].num_inputs < 1 || g->nodes[nx].input_tensors[0] != cur) return 0;
-    /* The scale: a 1-element weight, or a 1-element second input that no node produces. */
+    /* The scale: a 1-element node weight.  Its host value becomes a kernel argument,
+     * which a recorded replay keeps; a graph tensor the caller may rewrite between
+     * executions would then go stale, so a scale that is not a weight is not fused. */
     const tensor_t* scale_t = weight_of(&g->nodes[nx]);
-    if (!scale_t && g->nodes[nx].num_inputs >= 2 && producer_of(g, g->nodes[nx].input_tensors[1]) < 0)
-        scale_t = tensor_of(g, g->nodes[nx].input_tensors[1]);
     if (!scale_t || scale_t->numel != 1 || !scale_t->data) return 0;
     take(&l, nx);
     cur = out0(g, nx);
@@ -308,6 +308,8 @@ int graph_detect_mha(const inference_graph_t* g, graph_mha_match_t* matches, int
     if (!g || !matches || max_matches <= 0 || g->num_nodes <= 0) return 0;
     unsigned char* used = (unsigned char*)calloc((size_t)g->num_nodes, 1);
     if (!used) return 0;
+    /* Nodes absorbed by a permanent fusion take part in no match. */
+    for (int i = 0; i < g->num_nodes && i < g->fused_away_cap; i++) used[i] = g->fused_away[i];
     int count = 0;
     for (int tid = 0; tid < g->num_tensors && count < max_matches; tid++) {
         /* X: read by exactly three MatMuls (graph.c:363-380). */

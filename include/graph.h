@@ -110,6 +110,8 @@ typedef struct {
     int             decode_lens_cap; /* entries in decode_lens */
     void*           pinned;          /* per tensor: pinned host staging of graph inputs/outputs */
     int             pinned_cap;      /* entries in pinned */
+    unsigned char*  fused_away;      /* per node: absorbed by a permanent MHA fusion (never runs) */
+    int             fused_away_cap;  /* entries in fused_away */
 } inference_graph_t;
 
 inference_graph_t* graph_create(void);
@@ -126,8 +128,14 @@ void  graph_destroy(inference_graph_t* g);
 
 void  graph_set_kv_cache(inference_graph_t* g, int K_tensor_id, int V_tensor_id);
 void  graph_update_cache_len(inference_graph_t* g, int64_t new_cache_len);
-/* Accepted for source compatibility.  Fusion here is decided anew on every execution
- * and never rewrites the graph, so the flag changes nothing. */
+/* graph.c:151-153 and :810-815.  Off (the default): each GPU execution finds the
+ * attention subgraphs again and runs each as one fused node without changing the graph.
+ * On: the next GPU execution that finds them rewrites the graph for good: each match's
+ * last node becomes that OP_MHA_FUSED node (inputs X and the residual, the 8 weights,
+ * its params) and the match's other nodes are marked absorbed, so no later execution
+ * runs them or looks for the pattern again.  Turning the flag off afterwards does not
+ * undo a rewrite (the reference kept no restore record either).  A rewritten graph runs
+ * its fused nodes through mha_fused_*_cuda, so it needs use_cuda. */
 void  graph_set_permanent_fusion(inference_graph_t* g, int enable);
 
 int   graph_execute(inference_graph_t* g, tensor_t* inputs[],
@@ -155,7 +163,8 @@ int   graph_replay_state(const inference_graph_t* g);
  *   -> Transpose -> Reshape -> MatMul(W_O) (-> Add b_O) (-> Add residual)
  * Every intermediate tensor must have exactly one reader.  When use_cuda is set,
  * graph_execute runs each match as one OP_MHA_FUSED node in place of the pattern's last
- * node and skips the others; the graph itself is never modified. */
+ * node and skips the others; the graph itself is modified only under
+ * graph_set_permanent_fusion. */
 #define GRAPH_MHA_MAX_NODES 24
 typedef struct {
     int       out_node;                      /* the pattern's last node */

@@ -213,10 +213,15 @@ class Graph:
         self.lib.graph_destroy(self.g)
 
 
-def build_decode_graph(lib, c: DecodeCase):
+DT_I32 = 3
+
+
+def build_decode_graph(lib, c: DecodeCase, lens=None):
     """One OP_MHA_DECODE node with in-place KV caches registered through graph_set_kv_cache
     (the reference's decode-session wiring, graph.c:133-153).  f16 cases use F16 tensors,
-    so the executor resolves mha_decode_f16_cuda.  Returns (graph, {name: tensor})."""
+    so the executor resolves mha_decode_f16_cuda.  `lens` (int32, B entries) adds the
+    per-sequence lengths as the node's 9th weight, read when cache_len < 0.  Returns
+    (graph, {name: tensor})."""
     dt = DT_F16 if c.f16 else DT_F32
     conv = (lambda a: O.to_f16(a)) if c.f16 else (lambda a: np.asarray(a, np.float32))
     g = Graph(lib)
@@ -225,13 +230,17 @@ def build_decode_graph(lib, c: DecodeCase):
     tV, iV = g.tensor(conv(c.Vc), dt)
     tY, iY = g.tensor(conv(np.zeros_like(c.X)), dt)
     ws = [g.tensor(conv(w), dt)[0] for w in (c.WQ, c.bQ, c.WK, c.bK, c.WV, c.bV, c.WO, c.bO)]
+    tL = None
+    if lens is not None:
+        tL = g.tensor(np.asarray(lens, np.int32), DT_I32)[0]
+        ws.append(tL)
     p = O.decode_params(c.B, c.D, c.H, c.H_kv, c.d, c.cache_len, c.max_seq)
     g.node(OP_MHA_DECODE, [iX, iK, iV], [iY, iK, iV], ws, p)
     lib.graph_set_input(g.g, g.node(OP_INPUT, [], [iX]))
     lib.graph_set_output(g.g, g.node(OP_OUTPUT, [iY], []))
     lib.graph_set_kv_cache(g.g, iK, iV)
     assert lib.graph_build(g.g) == 0
-    return g, {"X": tX, "K": tK, "V": tV, "Y": tY}
+    return g, {"X": tX, "K": tK, "V": tV, "Y": tY, "L": tL}
 
 
 # op_type_t values of the unfused attention pattern (include/graph.h enum order).

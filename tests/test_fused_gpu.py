@@ -350,6 +350,50 @@ def test_graph_fuses_every_layer(gpu, native):
         g.destroy()
 
 
+@pytest.mark.parametrize("replay", [1, 0])
+def test_graph_permanent_fusion_rewrites_once(gpu, native, replay):
+    """graph_set_permanent_fusion (graph.c:151-153, :810-815): the first GPU execution
+    rewrites each attention block of a two-layer stack into one OP_MHA_FUSED node (the
+    block's last node, which then resolves to mha_fused_f32_cuda) and the pattern is no
+    longer found; later executions, with new inputs, run the rewritten graph and match
+    the oracle, recorded and replayed or eager."""
+    import cudaforge_amd as cf
+    from helpers import DT_F32, OP_INPUT, OP_OUTPUT, Graph, build_attention_subgraph
+    import oracle as O
+    c = FusedCase(1, 24, 4, 4, 16, seed=33, residual=True, bias_std=0.02)
+    g = Graph(native)
+    try:
+        tX, iX = g.tensor(np.asarray(c.X, np.float32))
+        ids1 = build_attention_subgraph(g, c, iX, iX)
+        ids2 = build_attention_subgraph(g, c, ids1["out"], ids1["out"])
+        native.graph_set_input(g.g, g.node(OP_INPUT, [], [iX]))
+        native.graph_set_output(g.g, g.node(OP_OUTPUT, [ids2["out"]], []))
+        assert native.graph_build(g.g) == 0
+        native.graph_set_replay(g.g, replay)
+        native.graph_set_permanent_fusion(g.g, 1)
+        last = [m.out_node for m in cf.graph_detect_mha(g.g)]
+        assert len(last) == 2
+        tY = g.tensor(np.zeros_like(c.X, dtype=np.float32), DT_F32)[0]
+        ins, outs = (ctypes.c_void_p * 1)(tX), (ctypes.c_void_p * 1)(tY)
+        p = O.fused_params(c.B, c.S, c.D, c.H, c.H_kv, c.d, True, False)
+        w = [c.WQ, c.bQ, c.WK, c.bK, c.WV, c.bV, c.WO, c.bO]
+        buf = ctypes.create_string_buffer(64)
+        for it in range(4):
+            X = O.normal(c.X.shape, 600 + it)
+            g.write(tX, X)
+            assert native.graph_execute(g.g, ins, outs, True) == 0, f"execution {it}"
+            y1 = O.mha_fused(X, X, *w, p)
+            assert max_abs(O.mha_fused(y1, y1, *w, p), g.read(tY, c.X.shape)) <= 2 * TOL32, f"execution {it}"
+            assert cf.graph_detect_mha(g.g) == []
+            for nid in last:
+                assert native.graph_resolve_op(g.g, nid, True, buf, 64) and buf.value == b"mha_fused_f32_cuda"
+        native.graph_set_permanent_fusion(g.g, 0)       # does not undo the rewrite
+        assert cf.graph_detect_mha(g.g) == []
+        assert native.graph_execute(g.g, ins, outs, True) == 0
+    finally:
+        g.destroy()
+
+
 def test_graph_broken_attention_pattern_is_not_fused(gpu, native):
     """Softmax replaced by ReLU: nothing is fused, so the nodes run as themselves and the
     execution fails at the first one that cannot (its MatMul nodes carry no params here,

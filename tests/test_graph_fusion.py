@@ -133,10 +133,13 @@ def test_shared_mask_node_still_runs(native):
         g.destroy()
 
 
-@pytest.mark.parametrize("style,fused", [("constant", True), ("produced", False), ("swapped", False)])
+@pytest.mark.parametrize("style,fused", [("weight", True), ("constant", False), ("produced", False),
+                                         ("swapped", False)])
 def test_scale_operand_rules(native, style, fused):
-    """The scale is read on the host, so only a weight or a tensor no node writes counts,
-    and the scores must be the Mul's first input."""
+    """The scale is read on the host and becomes a kernel argument that a recorded replay
+    keeps, so only a node weight counts (a graph tensor, even one no node writes, may be
+    rewritten by the caller between executions), and the scores must be the Mul's first
+    input."""
     import cudaforge_amd as cf
     c = FusedCase(1, 8, 2, 2, 8, seed=6, residual=True)
     g, _, _, _ = _graph(native, c, scale=0.3, scale_style=style)
