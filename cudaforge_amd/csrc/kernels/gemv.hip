@@ -150,12 +150,20 @@ __device__ __forceinline__ void advance_lengths(const cf_gemv_args_t& a) {
         for (int i = threadIdx.x; i < a.advance_n; i += blockDim.x) a.advance[i] += 1;
 }
 
+// Rows are stored unless their position is out of [0, pos_limit); the limit applies only
+// to segments indexed by position (ld_pos != 0, the cache rows K_new and V_new), so the Q
+// segment is always written and the attention has a defined query even for a length the
+// cache cannot take.
+__device__ __forceinline__ bool pos_ok(const cf_gemv_args_t& a, const cf_gemv_seg_t& sg, int64_t pos) {
+    return sg.ld_pos == 0 || a.pos_limit == 0 || (pos >= 0 && pos < a.pos_limit);
+}
+
 // Store one finished output element of segment `seg`, segment-local column n.
 template <typename T>
 __device__ __forceinline__ void store_val(const cf_gemv_args_t& a, const cf_gemv_seg_t& sg, int m, int n, float v) {
     const int64_t pos = a.pos_lens ? (int64_t)a.pos_lens[m] : a.pos_uniform;
-    if (a.pos_limit == 0 || (pos >= 0 && pos < a.pos_limit))
-        ((T*)sg.out)[(size_t)m * sg.ld_m + (size_t)pos * sg.ld_pos + n] = from_f<T>(v);
+    if (pos_ok(a, sg, pos))
+        ((T*)sg.out)[(size_t)m * sg.ld_m + (size_t)(sg.ld_pos ? pos : 0) * sg.ld_pos + n] = from_f<T>(v);
 }
 
 // ... with the segment's bias added first.
@@ -574,8 +582,8 @@ void gemv_small(cf_gemv_args_t a, Tiles t) {
         rotate_pair(v[0], v[1], rot[0]);
         rotate_pair(v[2], v[3], rot[1]);
     }
-    if (a.pos_limit == 0 || (pos >= 0 && pos < a.pos_limit)) {
-        T* out = (T*)sg.out + (size_t)store_m * sg.ld_m + (size_t)pos * sg.ld_pos + n;
+    if (pos_ok(a, sg, pos)) {
+        T* out = (T*)sg.out + (size_t)store_m * sg.ld_m + (size_t)(sg.ld_pos ? pos : 0) * sg.ld_pos + n;
 #pragma unroll
         for (int e = 0; e < 4; e++) out[e] = from_f<T>(v[e]);
     }

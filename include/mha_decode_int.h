@@ -14,7 +14,9 @@
  * -2 for the full op whose last kernel also adds one to each of the B lengths after the
  * step (a recorded decode step then advances its own position; the attention-only entry
  * rejects -3).  Device-held lengths cannot be checked on the host: a length >= max_seq
- * appends nothing and attends max_seq positions, a negative one attends position 0 only.
+ * appends nothing and attends max_seq positions, a negative one appends nothing and
+ * attends position 0 only; Q is projected either way (the RoPE variants then leave it
+ * unrotated, having no angle for that position).
  */
 #ifndef CF_MHA_DECODE_INT_H_
 #define CF_MHA_DECODE_INT_H_

@@ -238,6 +238,45 @@ def test_config2_full_size_core(gpu):
     assert max_abs(attn_ref64(Q[rows], K[rows], V[rows], [T, T], H_kv, scale), got[rows]) <= TOL16
 
 
+def test_full_decode_config2_full_size(gpu):
+    """Config 2 (B 16, D 4096, 32/8 heads, d 128, KV 4096, fp16) through the plain full op
+    (mha_decode_f16_cuda: projections, append, attention, output projection), the
+    reference's CUDA-against-CPU op check (tests/test_mha_decode.c:263-414) at the
+    headline shape: every output row and the appended K and V row of every sequence
+    against the oracle, and the rest of both caches unchanged."""
+    c = DecodeCase(16, 32, 8, 128, 4096, cache_len=4095, seed=19, f16=True)
+    want = c.oracle()
+    got = run_decode_gpu(c)
+    assert max_abs(want[0], got[0]) <= TOL16
+    for i, cache in ((1, c.Kc), (2, c.Vc)):
+        assert max_abs(want[i][:, 4095], got[i][:, 4095]) <= TOL16
+        assert np.array_equal(got[i][:, :4095], cache[:, :4095])
+
+
+@pytest.mark.parametrize("L", [40, 41, -1])
+def test_device_length_outside_the_cache(gpu, L):
+    """A device-held uniform length (cache_len -2) the host cannot check: at max_seq or
+    beyond, nothing is appended and all max_seq positions are attended; a negative one
+    appends nothing and attends position 0.  Q is projected either way (its store has no
+    position), so Y is the float64 result of X.WQ+bQ attending the unchanged cache, then
+    the output projection."""
+    import cudaforge_amd as cf
+    from helpers import dev
+    B, H, H_kv, d, max_seq = 2, 4, 2, 64, 40
+    c = DecodeCase(B, H, H_kv, d, max_seq, cache_len=0, seed=37)
+    bufs = [dev(a) for a in c.arrays()]
+    lens = dev(np.full(B, L, np.int32))
+    Y = cf.DeviceBuffer.empty((B, 1, c.D), np.float32)
+    p = cf.MhaDecodeParams(B, c.D, H, H_kv, d, float(1 / np.sqrt(d)), -2, max_seq)
+    assert cf.call_op("mha_decode_f32_cuda", bufs, [Y, bufs[1], bufs[2]], p, None, extra_inputs=[lens]) == 0
+    q = (c.X[:, 0].astype(np.float64) @ c.WQ + c.bQ).reshape(B, H, d)
+    att = np.full(B, max_seq if L >= max_seq else 1)
+    o = attn_ref64(q, c.Kc, c.Vc, att, H_kv, 1 / np.sqrt(d))
+    want = o.reshape(B, c.D) @ c.WO.astype(np.float64) + c.bO
+    assert max_abs(want, Y.download()[:, 0]) <= TOL32
+    assert np.array_equal(bufs[1].download(), c.Kc) and np.array_equal(bufs[2].download(), c.Vc)
+
+
 def test_cache_len_zero_is_value_row(gpu):
     """T = 1: softmax is 1, so the core returns the single V row (closed form)."""
     B, H, H_kv, d = 2, 8, 2, 128
@@ -515,6 +554,52 @@ def test_graph_decode_replay_advancing_length(gpu, native, f16):
     finally:
         for g, _ in graphs:
             g.destroy()
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_graph_decode_uniform_then_ragged_with_lengths_weight(gpu, native, f16):
+    """A decode node that carries per-sequence lengths as its 9th weight runs uniform
+    steps (device-held length, replayed), then ragged steps whose host lengths change
+    between executions, then uniform again; every output against the oracle run step by
+    step on its own caches.  The uniform steps neither read nor advance the lengths
+    weight (its device copy, read back, still holds what the caller wrote), and each
+    ragged step uses the lengths the caller wrote for it."""
+    from helpers import build_decode_graph
+    dt = np.float16 if f16 else np.float32
+    tol = TOL16 if f16 else TOL32
+    B, H, H_kv, d, max_seq = 3, 8, 2, 64, 48
+    lens0 = np.array([30, 12, 41], np.int32)
+    c = DecodeCase(B, H, H_kv, d, max_seq, cache_len=5, seed=91, f16=f16, wstd=0.1)
+    g, t = build_decode_graph(native, c, lens=lens0)
+    Kc, Vc = c.Kc, c.Vc
+    ins, os_ = (ctypes.c_void_p * 1)(t["X"]), (ctypes.c_void_p * 1)(t["Y"])
+    # (cache_len, lengths written to the weight before the step)
+    plan = [(5, None), (6, None), (7, None), (-1, lens0), (-1, lens0 + 1), (-1, np.array([3, 47, 0], np.int32)),
+            (9, None)]
+    try:
+        for step, (cl, lens) in enumerate(plan):
+            X = O.normal(c.X.shape, 700 + step)
+            if f16:
+                X = O.round_f16(X)
+            g.write(t["X"], O.to_f16(X) if f16 else X)
+            if lens is not None:
+                g.write(t["L"], lens)
+            native.graph_update_cache_len(g.g, cl)
+            assert native.graph_execute(g.g, ins, os_, True) == 0, f"step {step}"
+            got = g.read(t["Y"], c.X.shape, dt).astype(np.float32)
+            ref = DecodeCase(B, H, H_kv, d, max_seq, cache_len=None if cl < 0 else cl,
+                             seq_lens=None if cl >= 0 else lens, seed=91, f16=f16, wstd=0.1)
+            ref.X, ref.Kc, ref.Vc = X, Kc, Vc
+            want = ref.oracle()
+            assert max_abs(want[0], got) <= tol, f"step {step}"
+            Kc, Vc = want[1], want[2]
+            if step == 2:
+                assert native.tensor_copy_to_host(t["L"]) == 0
+                assert np.array_equal(g.read(t["L"], (B,), np.int32), lens0)
+        assert native.tensor_copy_to_host(t["K"]) == 0
+        assert max_abs(Kc, g.read(t["K"], c.Kc.shape, dt).astype(np.float32)) <= tol
+    finally:
+        g.destroy()
 
 
 def test_graph_decode_rejects_length_past_capacity(gpu, native):
