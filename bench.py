@@ -47,14 +47,40 @@ def time_op(cf, name, inputs, outputs, params, stream, steps, warmup, extra=()):
     return _t(name, inputs, outputs, params, stream, warmup, steps, extra_inputs=extra)
 
 
-def normal(shape, seed, std=1.0):
-    """Seeded N(0, std) float32 synthetic data (numpy's PCG64; the GPU legs never call
-    the oracle)."""
-    return (np.random.default_rng(seed).standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
+def dnormal(cf, shape, seed, std=1.0, f16=True):
+    """Seeded N(0, std) synthetic data made on the device: splitmix64 + Box-Muller
+    (synthetic_fill_normal), the generator the CPU baseline's oracle inputs come from, so
+    a seed names the same values in both legs.  The GPU legs never call the oracle."""
+    return cf.DeviceBuffer.normal(shape, np.float16 if f16 else np.float32, seed, std)
 
 
-def f16_normal(shape, seed, std=1.0):
-    return normal(shape, seed, std).astype(np.float16)
+def splitmix_uniform_int(n, seed, lo, hi):
+    """n integers lo + (splitmix64 output % (hi - lo + 1)) from one sequence seeded with
+    `seed` (the oracle's oracle_fill_uniform_int, restated so the GPU legs need no oracle)."""
+    mask = (1 << 64) - 1
+    st, out = seed & mask, []
+    for _ in range(n):
+        st = (st + 0x9E3779B97F4A7C15) & mask
+        z = st
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & mask
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & mask
+        z ^= z >> 31
+        out.append(lo + z % (hi - lo + 1))
+    return np.array(out, np.int64)
+
+
+# Seeds of every synthetic tensor, written into the JSON line.
+SEEDS = {
+    "config2_core": "set i (0..2): Q 101+10i, K 102+10i, V 103+10i",
+    "config2_full_op": "set i: base 200+100i; X base+1, K base+2, V base+3, WQ base+4, WK base+6, WV base+8, "
+                       "WO base+10 (weights std 0.02, biases 0)",
+    "config1_full_op_f32": "base 200: as config2_full_op, set 0 only",
+    "config4_ragged": "lengths splitmix64 seed 404 uniform in [1024, 32768]; set i: Q 401+10i, K 402+10i, V 403+10i",
+    "config3_prefill": "base 300: X base+1, WQ/WK/WV/WO base+2..5 (std 0.02), biases 0",
+    "config5_prefill": "base 500: as config3_prefill",
+    "layer_neighbours": "base 900",
+    "generator": "splitmix64 + Box-Muller (both outputs), fp16 by round-to-nearest-even from fp32",
+}
 
 
 # Independent input sets the decode legs rotate over: 3 x 268 MB of KV cache (plus the
@@ -64,21 +90,33 @@ def f16_normal(shape, seed, std=1.0):
 KV_SETS = 3
 
 
+STAT_REPS = 9   # extra timed loops of K steps behind the median / min figures
+
+
+def step_stats(cf, name, sets, out_sets, p, stream, steps):
+    """Median and min of the per-step mean over STAT_REPS further timed loops of `steps`
+    back-to-back steps each (events around each loop, no per-step events, which would
+    add their own gaps between launches)."""
+    from cudaforge_amd.api import time_op_sets
+    v = sorted(time_op_sets(name, sets, out_sets, p, stream, 1, steps) for _ in range(STAT_REPS))
+    return v[len(v) // 2], v[0]
+
+
 def bench_decode_core(cf, stream, steps, warmup):
     B, H, H_kv, d, T = 16, 32, 8, 128, 4096
-    sets = [[cf.DeviceBuffer.from_numpy(f16_normal((B, H, d), 101 + 10 * i)),
-             cf.DeviceBuffer.from_numpy(f16_normal((B, T, H_kv, d), 102 + 10 * i)),
-             cf.DeviceBuffer.from_numpy(f16_normal((B, T, H_kv, d), 103 + 10 * i))] for i in range(KV_SETS)]
+    sets = [[dnormal(cf, (B, H, d), 101 + 10 * i), dnormal(cf, (B, T, H_kv, d), 102 + 10 * i),
+             dnormal(cf, (B, T, H_kv, d), 103 + 10 * i)] for i in range(KV_SETS)]
     O_ = cf.DeviceBuffer.empty((B, H, d), np.float16)
     p = cf.MhaDecodeParams(B, H * d, H, H_kv, d, float(1 / np.sqrt(d)), T - 1, T)
     from cudaforge_amd.api import time_op_sets
     ms = time_op_sets("mha_decode_attn_f16_cuda", sets, [[O_]] * KV_SETS, p, stream, warmup, steps)
+    med, mn = step_stats(cf, "mha_decode_attn_f16_cuda", sets, [[O_]] * KV_SETS, p, stream, steps)
     ms_split, ms_merge = kernel_times(cf, sets, [O_], p, stream, min(steps, 1000), warmup)
     kv_bytes = 2 * B * T * H_kv * d * 2
     alg_bytes = kv_bytes + 2 * B * H * d * 2
     chunk, n_split = plan(cf, p)
-    return ms, ms_split, ms_merge, alg_bytes, dict(B=B, H_q=H, H_kv=H_kv, d=d, kv_len=T, chunk=chunk,
-                                                   n_split=n_split, kv_sets=KV_SETS)
+    return ms, (med, mn), ms_split, ms_merge, alg_bytes, dict(B=B, H_q=H, H_kv=H_kv, d=d, kv_len=T, chunk=chunk,
+                                                              n_split=n_split, kv_sets=KV_SETS)
 
 
 def kernel_times(cf, input_sets, outputs, params, stream, iters, warmup, f16=True):
@@ -115,8 +153,7 @@ def bench_decode_full(cf, stream, steps, warmup, f16=True, B=16, H=32, H_kv=8, d
     dt = np.float16 if f16 else np.float32
 
     def mk(shape, s, std=1.0):
-        a = normal(shape, s, std)
-        return cf.DeviceBuffer.from_numpy(a.astype(np.float16) if f16 else a)
+        return dnormal(cf, shape, s, std, f16)
 
     input_sets, output_sets = [], []
     for i in range(n_sets):
@@ -136,26 +173,32 @@ def bench_decode_full(cf, stream, steps, warmup, f16=True, B=16, H=32, H_kv=8, d
         name = name.replace("mha_decode_", "mha_decode_rope_")
     from cudaforge_amd.api import time_op_sets
     ms = time_op_sets(name, input_sets, output_sets, p, stream, warmup, steps)
+    med, mn = step_stats(cf, name, input_sets, output_sets, p, stream, steps)
     esz = 2 if f16 else 4
     alg = (2 * B * T * kvd + (D * D * 2 + 2 * D * kvd) + 2 * D + 2 * kvd + 2 * B * D + 2 * B * kvd) * esz
-    return ms, alg
+    return ms, alg, (med, mn)
 
 
 def bench_decode_ragged(cf, stream, steps, warmup):
     B, H, H_kv, d, cap = 4, 32, 8, 128, 32768
     # Attended lengths L_b ~ U[1024, 32768] from a seed; cache_len_b = L_b - 1.
-    lens = np.random.default_rng(404).integers(1024, cap + 1, size=B).astype(np.int32) - 1
-    L = cf.DeviceBuffer.from_numpy(lens.astype(np.int32))
-    sets = [[cf.DeviceBuffer.from_numpy(f16_normal((B, H, d), 401 + 10 * i)),
-             cf.DeviceBuffer.from_numpy(f16_normal((B, cap, H_kv, d), 402 + 10 * i)),
-             cf.DeviceBuffer.from_numpy(f16_normal((B, cap, H_kv, d), 403 + 10 * i)), L] for i in range(KV_SETS)]
+    lens = (ragged_lengths(B, cap) - 1).astype(np.int32)
+    L = cf.DeviceBuffer.from_numpy(lens)
+    sets = [[dnormal(cf, (B, H, d), 401 + 10 * i), dnormal(cf, (B, cap, H_kv, d), 402 + 10 * i),
+             dnormal(cf, (B, cap, H_kv, d), 403 + 10 * i), L] for i in range(KV_SETS)]
     O_ = cf.DeviceBuffer.empty((B, H, d), np.float16)
     p = cf.MhaDecodeParams(B, H * d, H, H_kv, d, float(1 / np.sqrt(d)), -1, cap)
     from cudaforge_amd.api import time_op_sets
     ms = time_op_sets("mha_decode_attn_f16_cuda", sets, [[O_]] * KV_SETS, p, stream, warmup, steps)
+    med, mn = step_stats(cf, "mha_decode_attn_f16_cuda", sets, [[O_]] * KV_SETS, p, stream, steps)
     ms_split, ms_merge = kernel_times(cf, sets, [O_], p, stream, min(steps, 1000), warmup)
-    alg = int(4096 * int((lens + 1).sum()) + 2 * B * H * d * 2)
-    return ms, alg, [int(x) + 1 for x in lens], ms_split, ms_merge
+    alg = int(4096 * int((lens.astype(np.int64) + 1).sum()) + 2 * B * H * d * 2)
+    return ms, alg, [int(x) + 1 for x in lens], ms_split, ms_merge, (med, mn)
+
+
+def ragged_lengths(B=4, cap=32768):
+    """Config 4's attended lengths: splitmix64 seed 404, uniform in [1024, cap]."""
+    return splitmix_uniform_int(B, 404, 1024, cap)
 
 
 def bench_decode_graph(cf, steps, warmup, B=16, H=32, H_kv=8, d=128, T=4096, seed=700, replay=True):
@@ -177,7 +220,7 @@ def bench_decode_graph(cf, steps, warmup, B=16, H=32, H_kv=8, d=128, T=4096, see
         ctypes.memmove(tt.data, arr.ctypes.data, arr.nbytes)
         return t, lib.graph_add_tensor(g, t)
 
-    mk = (lambda shape, s, std=1.0: f16_normal(shape, seed + s, std))
+    mk = (lambda shape, s, std=1.0: dnormal(cf, shape, seed + s, std).download())
     tX, iX = tensor(mk((B, 1, D), 1))
     _, iK = tensor(mk((B, T, H_kv, d), 2))
     _, iV = tensor(mk((B, T, H_kv, d), 3))
@@ -214,13 +257,13 @@ def bench_decode_graph(cf, steps, warmup, B=16, H=32, H_kv=8, d=128, T=4096, see
 
 def bench_layer_neighbours(cf, stream, steps, warmup, rows=4096, D=768, F=3072, seed=900):
     """LayerNorm (F16, BERT-base rows) and the FFN MatMul (F16, rows x D -> F with bias)."""
-    x = cf.DeviceBuffer.from_numpy(f16_normal((rows, D), seed))
-    g = cf.DeviceBuffer.from_numpy(f16_normal((D,), seed + 1, 0.1))
-    b = cf.DeviceBuffer.from_numpy(f16_normal((D,), seed + 2, 0.1))
+    x = dnormal(cf, (rows, D), seed)
+    g = dnormal(cf, (D,), seed + 1, 0.1)
+    b = dnormal(cf, (D,), seed + 2, 0.1)
     y = cf.DeviceBuffer.empty((rows, D), np.float16)
     ms_ln = time_op(cf, "layernorm_f16_cuda", [x, g, b], [y], cf.LayerNormParams(rows, D, 1e-12), stream, steps, warmup)
-    W = cf.DeviceBuffer.from_numpy(f16_normal((D, F), seed + 3, 0.02))
-    bias = cf.DeviceBuffer.from_numpy(f16_normal((F,), seed + 4, 0.02))
+    W = dnormal(cf, (D, F), seed + 3, 0.02)
+    bias = dnormal(cf, (F,), seed + 4, 0.02)
     C = cf.DeviceBuffer.empty((rows, F), np.float16)
     p = cf.MatmulParams(rows, F, D, False, False, 1, 0, 0, 0, 0)
     ms_mm = time_op(cf, "matmul_f16_cuda", [x, W, bias], [C], p, stream, steps, warmup)
@@ -249,7 +292,7 @@ def bench_fused(cf, stream, steps, warmup, B, S, H, d, causal, seed, f16=True):
     (QKV GEMM, attention, WO GEMM) its time and algorithmic FLOPs."""
     D = H * d
     dt = np.float16 if f16 else np.float32
-    mk = (lambda shape, s, std=1.0: cf.DeviceBuffer.from_numpy(normal(shape, seed + s, std).astype(dt)))
+    mk = (lambda shape, s, std=1.0: dnormal(cf, shape, seed + s, std, f16))
     zero = (lambda n: cf.DeviceBuffer.from_numpy(np.zeros(n, dt)))
     ins = [mk((B, S, D), 1), None, mk((D, D), 2, 0.02), zero(D), mk((D, D), 3, 0.02), zero(D),
            mk((D, D), 4, 0.02), zero(D), mk((D, D), 5, 0.02), zero(D)]
@@ -316,10 +359,10 @@ def cpu_baseline_configs(budget_s: float) -> dict:
     # Config 1: the full MHA_Decode FP32 op (mha_decode.c:11-125 restated), whole step.
     B, H, d, T = 1, 12, 64, 1024
     D = H * d
-    args = [O.normal((B, 1, D), 11), O.normal((B, T, H, d), 12), O.normal((B, T, H, d), 13),
-            O.normal((D, D), 14, 0, 0.02), np.zeros(D, np.float32), O.normal((D, D), 15, 0, 0.02),
-            np.zeros(D, np.float32), O.normal((D, D), 16, 0, 0.02), np.zeros(D, np.float32),
-            O.normal((D, D), 17, 0, 0.02), np.zeros(D, np.float32)]
+    args = [O.normal((B, 1, D), 201), O.normal((B, T, H, d), 202), O.normal((B, T, H, d), 203),
+            O.normal((D, D), 204, 0, 0.02), np.zeros(D, np.float32), O.normal((D, D), 206, 0, 0.02),
+            np.zeros(D, np.float32), O.normal((D, D), 208, 0, 0.02), np.zeros(D, np.float32),
+            O.normal((D, D), 210, 0, 0.02), np.zeros(D, np.float32)]
     p = O.decode_params(B, D, H, H, d, T - 1, T)
     sec, n = _cpu_time(lambda: O.mha_decode(*args, p), budget_s / 4, 3)
     alg = (2 * B * T * H * d + 4 * D * D + 4 * D + 2 * B * D + 2 * B * H * d) * 4
@@ -328,7 +371,7 @@ def cpu_baseline_configs(budget_s: float) -> dict:
                                          "sample": f"{n} whole steps (includes the reference's per-call cache copy)"}
     # Config 4: ragged core, one batch row (length 10639 of the seed-404 draw), scaled by
     # the total attended length.
-    lens = np.random.default_rng(404).integers(1024, 32768 + 1, size=4).astype(np.int64)
+    lens = ragged_lengths()
     L = int(lens[1])
     Q = O.round_f16(O.normal((1, 32, 128), 401))
     K = O.round_f16(O.normal((1, L, 8, 128), 402))
@@ -342,11 +385,11 @@ def cpu_baseline_configs(budget_s: float) -> dict:
                                          "sample": f"{n} x batch row 1 (L={L}) of 4, scaled by sum(L)/L = "
                                                    f"{float(lens.sum()) / L:.3f}"}
     # Configs 3 and 5: the fused op on one batch row, scaled by B.
-    for key, (Bc, S, H, d, causal) in {"config3_prefill_bert_base": (8, 512, 12, 64, False),
-                                       "config5_prefill_causal_gpt2_medium": (4, 1024, 16, 64, True)}.items():
+    for key, (Bc, S, H, d, causal, base) in {"config3_prefill_bert_base": (8, 512, 12, 64, False, 300),
+                                             "config5_prefill_causal_gpt2_medium": (4, 1024, 16, 64, True, 500)}.items():
         D = H * d
-        X = O.round_f16(O.normal((1, S, D), 31))
-        Ws = [O.round_f16(O.normal((D, D), 32 + i, 0, 0.02)) for i in range(4)]
+        X = O.round_f16(O.normal((1, S, D), base + 1))
+        Ws = [O.round_f16(O.normal((D, D), base + 2 + i, 0, 0.02)) for i in range(4)]
         z = np.zeros(D, np.float32)
         pf = O.fused_params(1, S, D, H, H, d, False, causal)
         sec, n = _cpu_time(lambda: O.mha_fused(X, None, Ws[0], z, Ws[1], z, Ws[2], z, Ws[3], z, pf), 0.0, 1)
@@ -491,23 +534,29 @@ def main() -> int:
         return 0
 
     log("decode core, config 2")
-    ms, ms_split, ms_merge, alg_bytes, cfg = bench_decode_core(cf, stream, steps, warmup)
+    ms, (ms_med, ms_min), ms_split, ms_merge, alg_bytes, cfg = bench_decode_core(cf, stream, steps, warmup)
     gbs = alg_bytes / (ms * 1e-3) / 1e9
     gbs_split = alg_bytes / (ms_split * 1e-3) / 1e9
-    log(f"  {ms * 1e3:.2f} us/step  {gbs:.0f} GB/s; split kernel {ms_split * 1e3:.2f} us "
-        f"({gbs_split:.0f} GB/s), merge kernel {ms_merge * 1e3:.2f} us")
+    log(f"  {ms * 1e3:.2f} us/step (median {ms_med * 1e3:.2f}, min {ms_min * 1e3:.2f})  {gbs:.0f} GB/s; "
+        f"split kernel {ms_split * 1e3:.2f} us ({gbs_split:.0f} GB/s), merge kernel {ms_merge * 1e3:.2f} us")
     extra = {}
     if not args.only_core:
         log("decode full op, config 2")
-        ms_f, alg_f = bench_decode_full(cf, stream, steps, warmup, n_sets=KV_SETS)
+        ms_f, alg_f, st_f = bench_decode_full(cf, stream, steps, warmup, n_sets=KV_SETS)
         extra["decode_full_op_config2_f16"] = {"us_per_step": round(ms_f * 1e3, 2),
+                                               "us_per_step_median": round(st_f[0] * 1e3, 2),
+                                               "us_per_step_min": round(st_f[1] * 1e3, 2),
                                                "GB_s": round(alg_f / (ms_f * 1e-3) / 1e9, 1),
+                                               "hbm_frac": round(alg_f / (ms_f * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                                                "alg_bytes": alg_f}
         log(f"  {ms_f * 1e3:.2f} us/step")
         log("decode full op with RoPE (base 500000), config 2")
-        ms_fr, _ = bench_decode_full(cf, stream, steps, warmup, n_sets=KV_SETS, rope_base=500000.0)
+        ms_fr, _, st_fr = bench_decode_full(cf, stream, steps, warmup, n_sets=KV_SETS, rope_base=500000.0)
         extra["decode_full_op_config2_f16_rope"] = {"us_per_step": round(ms_fr * 1e3, 2),
+                                                    "us_per_step_median": round(st_fr[0] * 1e3, 2),
+                                                    "us_per_step_min": round(st_fr[1] * 1e3, 2),
                                                     "GB_s": round(alg_f / (ms_fr * 1e-3) / 1e9, 1),
+                                                    "hbm_frac": round(alg_f / (ms_fr * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                                                     "alg_bytes": alg_f}
         log(f"  {ms_fr * 1e3:.2f} us/step")
         log("decode through graph_execute, config 2 (host X/Y)")
@@ -517,13 +566,18 @@ def main() -> int:
                                                      "host wall-clock, KV caches device-resident"}
         log(f"  {ms_g * 1e3:.2f} us/step")
         log("decode full op, config 1 (fp32)")
-        ms_1, alg_1 = bench_decode_full(cf, stream, steps, warmup, f16=False, B=1, H=12, H_kv=12, d=64, T=1024)
+        ms_1, alg_1, st_1 = bench_decode_full(cf, stream, steps, warmup, f16=False, B=1, H=12, H_kv=12, d=64,
+                                              T=1024)
         extra["decode_full_op_config1_f32"] = {"us_per_step": round(ms_1 * 1e3, 2),
+                                               "us_per_step_median": round(st_1[0] * 1e3, 2),
+                                               "us_per_step_min": round(st_1[1] * 1e3, 2),
                                                "GB_s": round(alg_1 / (ms_1 * 1e-3) / 1e9, 1),
                                                "alg_bytes": alg_1}
         log("decode ragged, config 4")
-        ms_r, alg_r, lens, ms_rs, ms_rm = bench_decode_ragged(cf, stream, steps, warmup)
+        ms_r, alg_r, lens, ms_rs, ms_rm, st_r = bench_decode_ragged(cf, stream, steps, warmup)
         extra["decode_core_config4_ragged"] = {"us_per_step": round(ms_r * 1e3, 2),
+                                               "us_per_step_median": round(st_r[0] * 1e3, 2),
+                                               "us_per_step_min": round(st_r[1] * 1e3, 2),
                                                "GB_s": round(alg_r / (ms_r * 1e-3) / 1e9, 1),
                                                "alg_bytes": alg_r, "lengths": lens,
                                                "hbm_frac": round(alg_r / (ms_r * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -556,19 +610,28 @@ def main() -> int:
         "warmup": warmup,
         "ms_per_step": round(ms, 5),
         "us_per_step": round(ms * 1e3, 2),
+        "us_per_step_median": round(ms_med * 1e3, 2),
+        "us_per_step_min": round(ms_min * 1e3, 2),
+        "step_stats": f"median and min of the per-step mean over {STAT_REPS} further timed loops of "
+                      f"{steps} back-to-back steps",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
-        "data": f"synthetic (seeded N(0,1) fp16 Q/K/V; resident in HBM; {KV_SETS} independent KV sets "
-                "rotated per step, beyond the 256 MB Infinity Cache)",
+        "data": f"synthetic (seeded N(0,1) fp16 Q/K/V made on the device by splitmix64 + Box-Muller, seeds "
+                f"in `seeds`; resident in HBM; {KV_SETS} independent KV sets rotated per step, beyond the 256 MB "
+                "Infinity Cache)",
         "config": {"workload": "MHA_Decode GQA Llama-3-8B attention core (config 2): split-KV + LSE merge "
                                "(split kernel + merge kernel per step)", **cfg},
         "roofline": {"bound": "hbm", "achieved": round(gbs_split, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs_split / HBM_PEAK_GBS, 4), "traffic": read_traffic("split_f16"),
                      "kernel": "split_f16<128,4,2,wide> (decode_attn.hip; a workgroup per (split, batch row), a wave per KV head)", "alg_bytes_per_launch": alg_bytes,
-                     "kernel_us": round(ms_split * 1e3, 2), "merge_kernel_us": round(ms_merge * 1e3, 2)},
+                     "kernel_us": round(ms_split * 1e3, 2), "merge_kernel_us": round(ms_merge * 1e3, 2),
+                     "step": {"what": "the whole step (split + merge launches), as `value`",
+                              "achieved": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                              "us": round(ms * 1e3, 2)}},
         "cpu_baseline": cpu,
+        "seeds": SEEDS,
         "extra": extra,
         "device": {"name": caps.name.decode(), "arch": caps.arch.decode(), "cu_count": caps.cu_count},
     }

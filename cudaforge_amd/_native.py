@@ -104,6 +104,7 @@ def _proto(lib):
                                                  c_void_p, c_int, c_int, c_int, POINTER(c_float), POINTER(c_float)]),
         "mha_fused_kernel_times": (c_int, [POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_void_p, c_int, c_int,
                                            c_int, POINTER(c_float)]),
+        "synthetic_fill_normal": (c_int, [c_void_p, c_int64, c_int, ctypes.c_uint64, c_float, c_float, c_void_p]),
         # decode planning knobs
         "mha_decode_set_split_chunk": (None, [c_int64]),
         "cf_gemv_set_dma_tile": (None, [c_int32]),

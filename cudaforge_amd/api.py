@@ -247,6 +247,19 @@ class DeviceBuffer:
                "gpu_memcpy_d2h")
         return out
 
+    @classmethod
+    def normal(cls, shape, dtype, seed: int, std: float = 1.0, mean: float = 0.0) -> "DeviceBuffer":
+        """Synthetic N(mean, std) data made on the device (synthetic_fill_normal:
+        splitmix64 + Box-Muller, the CPU oracle's generator), fp16 or fp32."""
+        buf = cls.empty(shape, dtype)
+        if buf.dtype not in (np.dtype(np.float16), np.dtype(np.float32)):
+            raise ValueError("normal() fills float16 or float32 buffers")
+        n = buf.nbytes // buf.dtype.itemsize
+        _check(buf.lib.synthetic_fill_normal(buf.ptr, n, 1 if buf.dtype == np.float16 else 0, seed & (2**64 - 1),
+                                             mean, std, None), "synthetic_fill_normal")
+        _check(buf.lib.gpu_stream_synchronize(None), "gpu_stream_synchronize")
+        return buf
+
     def fill_zero(self, stream: Stream | None = None) -> None:
         _check(self.lib.gpu_memset(self.ptr, 0, self.nbytes, stream.handle if stream else None), "gpu_memset")
 

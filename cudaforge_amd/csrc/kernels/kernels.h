@@ -221,6 +221,10 @@ int cf_launch_causal_mask(float* mask, int64_t S, void* stream);
  * device reads and writes directly): small stream-ordered transfers between kernels. */
 int cf_launch_copy_bytes(void* dst, const void* src, size_t bytes, void* stream);
 
+/* n elements (CF_ELEM_F16 or CF_ELEM_F32) of N(mean, stddev) from splitmix64 seeded with
+ * `seed` and Box-Muller (synthetic benchmark inputs; misc.hip). */
+int cf_launch_fill_normal(void* out, size_t n, int elem, uint64_t seed, float mean, float stddev, void* stream);
+
 /* v[0..n) = value (add = 0) or += value (add = 1), as a kernel (graph decode lengths). */
 int cf_launch_i32_update(int32_t* v, int32_t n, int32_t value, int32_t add, void* stream);
 

@@ -41,7 +41,48 @@ __global__ void copy_bytes_kernel(uint8_t* __restrict__ dst, const uint8_t* __re
     }
 }
 
+// Synthetic benchmark inputs: N(mean, stddev) by splitmix64 and Box-Muller, the
+// generator the CPU baseline's inputs come from, evaluated by counter so that every pair
+// is independent.  The sequence seeded with s has state s + k * 0x9E3779B97F4A7C15 after
+// k steps; pair i takes outputs 2i+1 and 2i+2 as uniforms u1, u2 in (0, 1] (top 53 bits
+// plus one, times 2^-53), and elements 2i, 2i+1 are mean + stddev * r * (cos, sin)(2 pi u2)
+// with r = sqrt(-2 ln u1), in double, rounded to float and then (fp16) to half, both by
+// round-to-nearest-even.
+__device__ __forceinline__ double splitmix_unit(uint64_t seed, uint64_t k) {
+    uint64_t z = seed + k * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return ((double)(z >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+}
+
+template <typename T>
+__global__ void fill_normal_kernel(T* __restrict__ out, size_t n, uint64_t seed, float mean, float stddev) {
+    const size_t pairs = (n + 1) / 2;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < pairs; i += (size_t)gridDim.x * blockDim.x) {
+        const double u1 = splitmix_unit(seed, 2 * i + 1), u2 = splitmix_unit(seed, 2 * i + 2);
+        const double r = sqrt(-2.0 * log(u1)), a = 6.283185307179586 * u2;
+        out[2 * i] = (T)(float)(mean + stddev * r * cos(a));
+        if (2 * i + 1 < n) out[2 * i + 1] = (T)(float)(mean + stddev * r * sin(a));
+    }
+}
+
 }  // namespace
+
+extern "C" int cf_launch_fill_normal(void* out, size_t n, int elem, uint64_t seed, float mean, float stddev,
+                                     void* stream) {
+    if (n == 0) return 0;
+    if (!out || (elem != CF_ELEM_F16 && elem != CF_ELEM_F32)) return (int)hipErrorInvalidValue;
+    size_t blocks = ((n + 1) / 2 + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    if (elem == CF_ELEM_F16)
+        hipLaunchKernelGGL(fill_normal_kernel<_Float16>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                           (_Float16*)out, n, seed, mean, stddev);
+    else
+        hipLaunchKernelGGL(fill_normal_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                           (float*)out, n, seed, mean, stddev);
+    return (int)hipGetLastError();
+}
 
 extern "C" int cf_launch_copy_bytes(void* dst, const void* src, size_t bytes, void* stream) {
     if (bytes == 0) return 0;

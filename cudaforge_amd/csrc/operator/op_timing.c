@@ -1,6 +1,14 @@
 /* op_timing.c — event-timed loop over a registered operator (see include/op_timing.h). */
 #include "op_timing.h"
 #include "gpu_ops.h"
+#include "../kernels/kernels.h"
+
+int synthetic_fill_normal(void* dst, int64_t n, int elem_f16, uint64_t seed, float mean, float stddev,
+                          stream_t* stream) {
+    if (!dst || n < 0) return -1;
+    return cf_launch_fill_normal(dst, (size_t)n, elem_f16 ? CF_ELEM_F16 : CF_ELEM_F32, seed, mean, stddev,
+                                 stream ? stream->cuda_stream : NULL);
+}
 
 int operator_time(const char* name, const void* inputs[], void* outputs[],
                   const operator_params_t* params, stream_t* stream,

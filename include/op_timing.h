@@ -51,6 +51,15 @@ int mha_decode_attn_kernel_times(const void* const* input_sets, int n_inputs, in
 int mha_fused_kernel_times(const void* inputs[], void* outputs[], const operator_params_t* params,
                            stream_t* stream, int elem_f16, int warmup, int iters, float ms[3]);
 
+/* Synthetic inputs for timing runs, generated on the device: `n` elements (fp16 when
+ * elem_f16, else fp32) of N(mean, stddev) from splitmix64 seeded with `seed` and
+ * Box-Muller with both outputs used, the generator of the CPU oracle's inputs
+ * (oracle_fill_normal), so a seed names the same values on both sides up to the last bit
+ * of the device's double-precision log/cos/sin.  Enqueued on stream->cuda_stream (NULL:
+ * the default stream).  Returns 0, -1 for bad arguments, or HIP's status. */
+int synthetic_fill_normal(void* dst, int64_t n, int elem_f16, uint64_t seed, float mean, float stddev,
+                          stream_t* stream);
+
 #ifdef __cplusplus
 }
 #endif
