@@ -49,8 +49,9 @@ int mha_decode_attn_f16_cuda(const void* inputs[], void* outputs[],
  * and result bits; the split partials live in a fixed 16 MiB device array per GPU
  * (cf. cf_decode_attn_scratch_bytes) instead of the stream workspace, and no call
  * allocates or frees anything.  A plan whose partials exceed that array returns -1 with
- * a message on stderr.  Every call on one GPU shares the array, so calls that overlap
- * on one GPU (different streams, or threads) race; order them on one stream. */
+ * a message on stderr.  One caller at a time per GPU: every call on one GPU shares the
+ * array, so calls that overlap there in time (different streams, or threads) race and
+ * give undefined results; order them on one stream. */
 int mha_decode_attn_f16_noalloc(const void* inputs[], void* outputs[],
                                 const operator_params_t* params, stream_t* stream);
 
