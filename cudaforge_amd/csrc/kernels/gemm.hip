@@ -746,6 +746,440 @@ void gemm_f32(cf_gemm_args_t a, Tiling t) {
     store_tile<float, NJ>(a, seg, N, m0 + wm, n0 + wn, lr, lq, acc);
 }
 
+// ------------------------------------------------------ fp16, wave-specialised ---
+// BM x BN tiles (BM = 256 or 128) of 8 waves: waves 4-7 only issue the direct-to-LDS
+// loads, waves 0-3 only read LDS and run MFMAs, and one barrier per 64-k stage orders the
+// two.  A wave that both issues a stage's DMA instructions and multiplies stalls at the
+// issue (measured ~650 clocks of every stage) and its MFMAs never overlap the loads: a
+// loop of MFMAs and DMA took the sum of the two alone.  Stages are 64 k deep so every A
+// DMA instruction reads 8 rows x 128 B, whole cache lines: per CU the load path moves ~50
+// B/clk for whole lines and ~15 B/clk for the 16 rows x 64 B that one MFMA fragment's
+// rows are.  A rows in LDS are 128 B with chunk c of row r at c ^ ((r >> 1) & 7), so the
+// A fragment reads (ds_read_b128, 16 rows x one chunk) are conflict-free; W rows (BN
+// columns of one k) are padded by one 16-byte chunk, which the transposing B reads
+// (ds_read_b64_tr_b16) measure at the ds_read_b64 rate.  A compute wave owns 64 rows x
+// BN / NWN columns (NWN = 256 / BM waves along N).
+//
+// Columns are the concatenation of the segments (Q | K | V for the projection), and a
+// tile may straddle a segment boundary: every 8-column chunk belongs to one segment (the
+// launcher checks n[s] % 8), so loads and stores are routed per chunk.  The epilogue
+// stages the tile in the (then idle) LDS, bias added in fp32 and, without a residual,
+// rounded once to fp16; with a residual the fp32 sum is staged and the residual added
+// before the single rounding, as in the other kernels.  All 8 waves then store 16-byte
+// chunks: along n for row-major C and head-major q / k, along s (8 rows of one column,
+// read down the staged column) for v^T.
+constexpr int WS_BK = 64;
+
+template <int BM, int BN>
+struct WsShape {
+    static constexpr int NWN = 256 / BM;           // compute waves along N
+    static constexpr int WN = BN / NWN;            // columns per compute wave
+    static constexpr int NJ = WN / 16;             // 16-column MFMA blocks per compute wave
+    static constexpr int A_ST = BM * WS_BK;        // halves per stage of A
+    static constexpr int WCPR = BN / 8 + 1;        // 16-byte chunks per padded W row
+    static constexpr int LDW = WCPR * 8;           // halves per W row in LDS
+    static constexpr int W_CH = WS_BK * WCPR;      // chunks per W stage
+    static constexpr int W_INSTR = (W_CH + 63) / 64;
+    static constexpr int W_ST = W_INSTR * 512;     // halves per stage of W (whole DMA instructions)
+    static constexpr int ST = A_ST + W_ST;
+    static constexpr int A_PW = A_ST * 2 / 1024 / 4;   // A DMA instructions per loader wave
+    static constexpr int W_PW = (W_INSTR + 3) / 4;     // W DMA instructions per loader wave, at most
+    static_assert(WN % 16 == 0 && BN % 8 == 0, "tile width");
+};
+
+template <int BM, int BN, int S>
+constexpr unsigned ws_lds_bytes() { return (unsigned)S * WsShape<BM, BN>::ST * 2u; }
+
+// What the epilogue reads of the launch arguments, loaded into registers at kernel start:
+// reading them from the argument block after the main loop cost ~1 us per group of fields
+// (config-3 QKV product, 22.8 -> 19 us without those late reads).
+struct WsEpi {
+    _Float16* out0;
+    _Float16* out1;
+    _Float16* out2;
+    const _Float16* bias0;
+    const _Float16* bias1;
+    const _Float16* bias2;
+    const _Float16* res;
+    int S, Hq, Hkv, d, n0w;
+    // Per-segment pointers as the first one plus a selected distance: a select among the
+    // pointers themselves is turned into an indexed load of the struct, which then lives
+    // in scratch memory.
+    __device__ _Float16* out(int s) const {
+        return out0 + (s == 1 ? out1 - out0 : (ptrdiff_t)0) + (s == 2 ? out2 - out0 : (ptrdiff_t)0);
+    }
+    __device__ const _Float16* bias(int s) const {
+        return bias0 + (s == 1 ? bias1 - bias0 : (ptrdiff_t)0) + (s == 2 ? bias2 - bias0 : (ptrdiff_t)0);
+    }
+};
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ WsEpi ws_epi(const cf_gemm_args_t& a) {
+    WsEpi e;
+    e.out0 = (_Float16*)a.out[0];
+    e.out1 = (_Float16*)a.out[1];
+    e.out2 = (_Float16*)a.out[2];
+    e.bias0 = (const _Float16*)a.bias[0];
+    e.bias1 = (const _Float16*)a.bias[1];
+    e.bias2 = (const _Float16*)a.bias[2];
+    e.res = (const _Float16*)a.residual;
+    e.S = a.S;
+    e.Hq = a.H_q;
+    e.Hkv = a.H_kv;
+    e.d = a.d;
+    e.n0w = a.n[0];
+    // Empty asm that "modifies" every field: the loads happen here, not where first used.
+    asm volatile("" : "+s"(e.out0), "+s"(e.out1), "+s"(e.out2), "+s"(e.bias0), "+s"(e.bias1), "+s"(e.bias2),
+                 "+s"(e.res));
+    asm volatile("" : "+s"(e.S), "+s"(e.Hq), "+s"(e.Hkv), "+s"(e.d), "+s"(e.n0w));
+    return e;
+}
+#pragma clang diagnostic pop
+
+// Destination offsets of gemm_f16_ws's Q|K|V scatter (row_part + col_part) without an
+// integer division per chunk: the tile's first row is split into (batch, position) once
+// per thread and a row r rows further carries over at most a few sequence ends; a
+// power-of-two head size splits columns with a shift (the split by division measured
+// ~1 us of the config-3 QKV product).
+struct WsRows {
+    int m0, b0, s0;       // the tile's first row and its (batch, position)
+    int dsh;              // log2(d) when d is a power of two, else -1
+};
+__device__ __forceinline__ WsRows ws_rows(const WsEpi& e, int m0) {
+    WsRows w;
+    w.m0 = m0;
+    w.b0 = m0 / e.S;
+    w.s0 = m0 - w.b0 * e.S;
+    w.dsh = (e.d & (e.d - 1)) == 0 ? __builtin_ctz(e.d) : -1;
+    return w;
+}
+__device__ __forceinline__ size_t ws_qkv_off(const WsEpi& e, const WsRows& w, int seg, int m, int n) {
+    int s = w.s0 + (m - w.m0), b = w.b0;
+    while (s >= e.S) {
+        s -= e.S;
+        ++b;
+    }
+    const int H = seg == 0 ? e.Hq : e.Hkv;
+    if (seg == 2) return (size_t)b * H * e.d * e.S + s + (size_t)n * e.S;
+    const int h = w.dsh >= 0 ? n >> w.dsh : n / e.d;
+    return ((size_t)b * H * e.S + s) * e.d + (size_t)h * e.S * e.d + (n - h * e.d);
+}
+
+// Segment of concatenated column gc (a multiple of 8) and its column inside it.
+__device__ __forceinline__ int ws_seg_n(int nseg, const int (&start)[4], int gc, int& col) {
+    const int s = (nseg > 1 && gc >= start[1]) ? ((nseg > 2 && gc >= start[2]) ? 2 : 1) : 0;
+    col = gc - start[s];
+    return s;
+}
+__device__ __forceinline__ int ws_seg(const cf_gemm_args_t& a, const int (&start)[4], int gc, int& col) {
+    return ws_seg_n(a.nseg, start, gc, col);
+}
+
+// Epilogue kinds of gemm_f16_ws, a template parameter so that each launch carries only its
+// own staging and store code (a run-time switch between them measured ~1 us per switch
+// on the config-3 QKV product).
+enum { WS_EPI_ROWMAJOR = 0, WS_EPI_RESIDUAL = 1, WS_EPI_QKV = 2 };
+
+template <int BM, int BN, int EPI>
+__device__ __forceinline__ void ws_store(const WsEpi& e, const int (&start)[4], int nseg, int m0, int n0, int tid,
+                                         const _Float16* smem, bool vt_tile);
+
+template <int BM, int BN, int S, int EPI>
+__global__ __launch_bounds__(512, 1)
+void gemm_f16_ws(cf_gemm_args_t a, Tiling t) {
+    using SH = WsShape<BM, BN>;
+    constexpr int NJ = SH::NJ, A_ST = SH::A_ST, LDW = SH::LDW, ST = SH::ST, A_PW = SH::A_PW, W_PW = SH::W_PW;
+    constexpr int WCPR = SH::WCPR, W_CH = SH::W_CH, W_INSTR = SH::W_INSTR;
+    extern __shared__ __attribute__((aligned(16))) _Float16 smem_ws[];
+    _Float16* const smem = smem_ws;
+
+    const WsEpi epi = ws_epi(a);
+    // Column space: segment s covers [start[s], start[s] + n[s]).
+    int start[4];
+    start[0] = 0;
+    start[1] = a.n[0];
+    start[2] = a.n[0] + (a.nseg > 1 ? a.n[1] : 0);
+    start[3] = start[2] + (a.nseg > 2 ? a.n[2] : 0);
+    int tile_m, tile_n;
+    tile_of_block(blockIdx.x, t.n_tiles_m, start[3] / BN, t.group_m, tile_m, tile_n);
+    const int m0 = tile_m * BM, n0 = tile_n * BN;
+    const int K = a.K, nk = K / WS_BK;
+    // Every column of the tile goes to v^T: accumulate C and stage it column-major.
+    const bool vt_tile = EPI == WS_EPI_QKV && a.nseg == 3 && n0 >= start[2];
+    const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15, lq = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int cw = wave & 3;
+
+    if (wave >= 4) {
+        // Loader waves.  A: instruction u of a stage covers rows 8u .. 8u+7 (lane L: row
+        // 8u + L/8, stored chunk L%8 holding k-chunk (L%8) ^ swz(row)), a uniform base (the
+        // stage's first k) plus per-lane 32-bit offsets.  W: instruction u covers padded
+        // chunks 64u .. 64u+63 of the stage; a lane keeps its chunk's 64-bit address and
+        // steps it by 64 rows of its segment per stage (pad chunks re-read the row's last).
+        const _Float16* __restrict__ A = (const _Float16*)a.a;
+        uint32_t a_off[A_PW];
+#pragma unroll
+        for (int v = 0; v < A_PW; v++) {
+            const int row = 8 * (A_PW * cw + v) + (lane >> 3), pc = lane & 7;
+            a_off[v] = ((uint32_t)(m0 + row) * (uint32_t)K + 8u * (uint32_t)(pc ^ ((row >> 1) & 7))) * 2u;
+        }
+        const _Float16* w_ptr[W_PW];
+        uint32_t w_step[W_PW];
+        int nw = 0;
+#pragma unroll
+        for (int v = 0; v < W_PW; v++) {
+            const int u = cw + 4 * v;
+            nw += u < W_INSTR ? 1 : 0;
+            const int q = min(64 * u + lane, W_CH - 1);
+            const int r = q / WCPR, c = min(q % WCPR, BN / 8 - 1);
+            int col;
+            const int s = ws_seg(a, start, n0 + 8 * c, col);
+            // Offsets from segment 0, not a.w[s] / a.n[s]: a per-lane index into the
+            // argument block would copy it to scratch memory.
+            const _Float16* w0 = (const _Float16*)a.w[0];
+            const _Float16* wbase = w0 + (s == 1 ? (const _Float16*)a.w[1] - w0 : (ptrdiff_t)0) +
+                                    (s == 2 ? (const _Float16*)a.w[2] - w0 : (ptrdiff_t)0);
+            const int ns = a.n[0] + (s == 1 ? a.n[1] - a.n[0] : 0) + (s == 2 ? a.n[2] - a.n[0] : 0);
+            w_ptr[v] = wbase + (size_t)r * ns + col;
+            w_step[v] = (uint32_t)(WS_BK * ns);
+        }
+        const uint32_t lds0 = lds_offset(smem);
+        const uint32_t a_lds = __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)(A_PW * cw) * 1024u);
+        const uint32_t w_lds = __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)A_ST * 2u + (uint32_t)cw * 1024u);
+        auto issue = [&](int kt, int stage) {
+            const _Float16* ab = A + kt * WS_BK;
+            const uint32_t so = (uint32_t)stage * ST * 2u;
+#pragma unroll
+            for (int v = 0; v < A_PW; v++) lds_dma16_s(a_off[v], ab, a_lds + so + v * 1024u);
+#pragma unroll
+            for (int v = 0; v < W_PW; v++)
+                if (v < nw) {
+                    lds_dma16(w_ptr[v], w_lds + so + 4u * v * 1024u);
+                    w_ptr[v] += w_step[v];
+                }
+        };
+        for (int s = 0; s < S - 1 && s < nk; s++) issue(s, s);
+        if (nw == W_PW) wait_ahead<A_PW + W_PW, S - 2>(min(S - 2, nk - 1));
+        else wait_ahead<A_PW + W_PW - 1, S - 2>(min(S - 2, nk - 1));
+        ring_barrier();
+        for_each_stage<S>(nk, [&](int kt, auto stage_c) {
+            constexpr int stage = decltype(stage_c)::value;
+            // Stage (kt - 1) % S was read in step kt - 1, finished before this barrier.
+            if (kt + S - 1 < nk) issue(kt + S - 1, (stage + S - 1) % S);
+            // Stage kt + 1 is complete at the next barrier; later ones may stay in flight.
+            if (kt + 1 < nk) {
+                const int after = min(S - 2, nk - 2 - kt);
+                if (nw == W_PW) wait_ahead<A_PW + W_PW, S - 2>(after);
+                else wait_ahead<A_PW + W_PW - 1, S - 2>(after);
+            }
+            ring_barrier();
+        });
+    } else {
+        // Compute waves: rows wm .. wm+63, columns wn .. wn + BN/NWN - 1 of the tile.
+        const int wm = 64 * (cw % (4 / SH::NWN)), wn = SH::WN * (cw / (4 / SH::NWN));
+        int a_rd[2][4], w_rd[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int row = wm + 16 * i + lr;
+                a_rd[h][i] = row * WS_BK + 8 * ((4 * h + lq) ^ ((row >> 1) & 7));
+            }
+#pragma unroll
+        for (int e = 0; e < 2; e++) w_rd[e] = A_ST + (8 * lq + 4 * e + (lr >> 2)) * LDW + wn + 4 * (lr & 3);
+        // CT: accumulate C^T (operands swapped), acc[i][j][e] = C[wm + 16i + lr][wn + 16j + 4lq + e],
+        // for destinations contiguous along n; otherwise C, acc[i][j][e] = C[wm + 16i + 4lq + e]
+        // [wn + 16j + lr], for tiles whose every column goes to v^T (contiguous along s).
+        auto run = [&](auto ct_c) {
+            constexpr bool CT = decltype(ct_c)::value;
+            f4_t acc[4][NJ];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < NJ; j++) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+            ring_barrier();
+            for_each_stage<S>(nk, [&](int kt, auto stage_c) {
+                constexpr int stage = decltype(stage_c)::value;
+                const _Float16* st = smem + stage * ST;
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    h8_t af[4], bf[NJ];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) af[i] = *(const h8_t*)(st + a_rd[h][i]);
+#pragma unroll
+                    for (int j = 0; j < NJ; j++)
+                        bf[j] = b_frag_tr(st + 32 * h * LDW + w_rd[0] + 16 * j, st + 32 * h * LDW + w_rd[1] + 16 * j);
+#pragma unroll
+                    for (int j = 0; j < NJ; j++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            acc[i][j] = CT ? __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[j], af[i], acc[i][j], 0, 0, 0)
+                                           : __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                }
+                ring_barrier();
+            });
+            if constexpr (CT) {
+                // Stage [BM][BN]: bias added in fp32; fp16 (one rounding) without a residual,
+                // fp32 with one.  A lane's four columns lie in one segment (n[s] % 8 == 0);
+                // every bias load is issued before the first is used.
+                constexpr bool f32s = EPI == WS_EPI_RESIDUAL;
+                h4_t b4[NJ];
+#pragma unroll
+                for (int j = 0; j < NJ; j++) {
+                    int col;
+                    const int sg = ws_seg(a, start, n0 + wn + 16 * j + 4 * lq, col);
+                    const _Float16* bias = epi.bias(sg);
+                    b4[j] = bias ? *(const h4_t*)(bias + col) : h4_t{0, 0, 0, 0};
+                }
+#pragma unroll
+                for (int j = 0; j < NJ; j++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int r = wm + 16 * i + lr, c = wn + 16 * j + 4 * lq;
+                        const float v0 = acc[i][j][0] + (float)b4[j][0], v1 = acc[i][j][1] + (float)b4[j][1];
+                        const float v2 = acc[i][j][2] + (float)b4[j][2], v3 = acc[i][j][3] + (float)b4[j][3];
+                        if constexpr (f32s) *(f4_t*)((float*)smem + r * (BN + 4) + c) = f4_t{v0, v1, v2, v3};
+                        else *(uint2*)(smem + r * (BN + 8) + c) = pack4(v0, v1, v2, v3);
+                    }
+            } else {
+                // A v^T tile: stage [BN][BM] (column-major), bias of column n added in fp32.
+                _Float16 bc[NJ];
+#pragma unroll
+                for (int j = 0; j < NJ; j++) bc[j] = epi.bias2 ? epi.bias2[n0 + wn + 16 * j + lr - start[2]] : (_Float16)0;
+#pragma unroll
+                for (int j = 0; j < NJ; j++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const float bv = (float)bc[j];
+                        *(uint2*)(smem + (wn + 16 * j + lr) * (BM + 8) + wm + 16 * i + 4 * lq) =
+                            pack4(acc[i][j][0] + bv, acc[i][j][1] + bv, acc[i][j][2] + bv, acc[i][j][3] + bv);
+                    }
+            }
+        };
+        if constexpr (EPI == WS_EPI_QKV) {
+            if (vt_tile) run(std::false_type{});
+            else run(std::true_type{});
+        } else {
+            run(std::true_type{});
+        }
+    }
+    ring_barrier();   // every loader is past its last stage and the tile is staged
+    ws_store<BM, BN, EPI>(epi, start, a.nseg, m0, n0, tid, smem, vt_tile);
+}
+
+// Store phase of gemm_f16_ws (all 512 threads): the staged tile goes out as 16-byte chunks,
+// 8 columns of one row (row-major C, head-major q and k; consecutive threads along the
+// row) or, for v^T columns, 8 rows of one column read down the staged column.  Each pass
+// has a fixed trip count, and all of a thread's LDS reads are issued before its stores.
+template <int BM, int BN, int EPI>
+__device__ __forceinline__ void ws_store(const WsEpi& e, const int (&start)[4], int nseg, int m0, int n0, int tid,
+                                         const _Float16* smem, bool vt_tile) {
+    constexpr int CPR = BN / 8, NCH = BM * CPR, IT = (NCH + 511) / 512;
+    constexpr bool qkv = EPI == WS_EPI_QKV;
+    const WsRows wr = ws_rows(e, m0);
+    if constexpr (EPI == WS_EPI_ROWMAJOR) {
+        // Row-major C: consecutive threads along a row.
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            const int id = tid + 512 * it;
+            if (id < NCH) {
+                const int r = id / CPR, c8 = id - r * CPR;
+                *(h8_t*)(e.out0 + (size_t)(m0 + r) * e.n0w + n0 + 8 * c8) = *(const h8_t*)(smem + r * (BN + 8) + 8 * c8);
+            }
+        }
+        return;
+    }
+    if (qkv && vt_tile) {
+        // Staged [BN][BM + 8]: chunks of 8 consecutive rows (positions s) of one column.
+        constexpr int RPC = BM / 8, NV = BN * RPC, ITV = (NV + 511) / 512;
+        h8_t v[ITV];
+        size_t off[ITV];
+#pragma unroll
+        for (int it = 0; it < ITV; it++) {
+            const int id = min(tid + 512 * it, NV - 1), c = id / RPC, r8 = 8 * (id - c * RPC);
+            v[it] = *(const h8_t*)(smem + c * (BM + 8) + r8);
+            off[it] = ws_qkv_off(e, wr, 2, m0 + r8, n0 + c - start[2]);
+        }
+#pragma unroll
+        for (int it = 0; it < ITV; it++)
+            if (tid + 512 * it < NV) *(h8_t*)(e.out2 + off[it]) = v[it];
+        return;
+    }
+    if constexpr (EPI == WS_EPI_RESIDUAL) {
+        const _Float16* __restrict__ res = e.res;
+        f4_t lo[IT], hi[IT];
+        h8_t rv[IT];
+        size_t off[IT];
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            const int id = min(tid + 512 * it, NCH - 1), r = id / CPR, c8 = id - r * CPR;
+            const float* sp = (const float*)smem + r * (BN + 4) + 8 * c8;
+            off[it] = (size_t)(m0 + r) * e.n0w + n0 + 8 * c8;
+            lo[it] = *(const f4_t*)sp;
+            hi[it] = *(const f4_t*)(sp + 4);
+            rv[it] = *(const h8_t*)(res + off[it]);
+        }
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            if (tid + 512 * it >= NCH) continue;
+            const float f[8] = {lo[it][0], lo[it][1], lo[it][2], lo[it][3], hi[it][0], hi[it][1], hi[it][2], hi[it][3]};
+            h8_t v;
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = (_Float16)(f[e] + (float)rv[it][e]);
+            *(h8_t*)(e.out0 + off[it]) = v;
+        }
+        return;
+    }
+    {
+        h8_t v[IT];
+        size_t off[IT];
+        int sg[IT];
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            const int id = min(tid + 512 * it, NCH - 1), r = id / CPR, c8 = id - r * CPR;
+            int col;
+            sg[it] = ws_seg_n(nseg, start, n0 + 8 * c8, col);
+            off[it] = ws_qkv_off(e, wr, sg[it], m0 + r, col);
+            v[it] = *(const h8_t*)(smem + r * (BN + 8) + 8 * c8);
+        }
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            if (tid + 512 * it >= NCH || (qkv && sg[it] == 2)) continue;   // v^T: below
+            *(h8_t*)(e.out(sg[it]) + off[it]) = v[it];
+        }
+    }
+    if (qkv && n0 + BN > start[2]) {
+        // The tile's columns in the V segment, [max(n0, start[2]), n0 + BN): chunks of 8 rows.
+        const int c_lo = max(n0, start[2]) - n0, ncol = BN - c_lo, nv = ncol * (BM / 8);
+        constexpr int ITV = (BN * (BM / 8) + 511) / 512;
+        h8_t v[ITV];
+        size_t off[ITV];
+#pragma unroll
+        for (int it = 0; it < ITV; it++) {
+            const int id = min(tid + 512 * it, nv - 1);
+            const int c = c_lo + id % ncol, r8 = 8 * (id / ncol);
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[it][e] = smem[(r8 + e) * (BN + 8) + c];
+            off[it] = ws_qkv_off(e, wr, 2, m0 + r8, n0 + c - start[2]);
+        }
+#pragma unroll
+        for (int it = 0; it < ITV; it++)
+            if (tid + 512 * it < nv) *(h8_t*)(e.out2 + off[it]) = v[it];
+    }
+}
+
+// Per-tile cost model of the wave-specialised kernel, in CU clocks: the larger of its DMA
+// (~32 B/clk per CU with whole A lines) and its MFMA work at ~60 % of the CU's 4096
+// FLOP/clk (one compute wave per SIMD), times the rounds of tiles over the CUs.
+inline double ws_cost(long long M, long long Ntot, long long K, int bm, int bn, int cus) {
+    const long long tiles = (M / bm) * (Ntot / bn);
+    const double dma = (double)(bm + bn) * (double)K * 2.0 / 32.0;
+    const double mfma = 2.0 * bm * bn * (double)K / 2500.0;
+    const long long rounds = (tiles + cus - 1) / cus;
+    return (double)rounds * (dma > mfma ? dma : mfma);
+}
+
 int g_gemm_stages = 0;   // tuning override of the direct-to-LDS kernel's ring depth (3, 4; 0 = automatic)
 int g_gemm_bn = 0;       // tuning override of its tile width (96, 128; 0 = automatic)
 
@@ -785,6 +1219,91 @@ void launch_async_192(dim3 grid, hipStream_t s, const cf_gemm_args_t& a, const T
     hipLaunchKernelGGL((gemm_f16_async<3, 192, 32>), grid, dim3(kThreads), 0, s, a, t);
 }
 
+int g_gemm_ws = 0;        // 0: wave-specialised kernel where it applies; 1: never
+int g_gemm_ws_bm = 0;     // tuning/test override of its tile (both 0 = cost model)
+int g_gemm_ws_bn = 0;
+
+// The wave-specialised kernel's dynamic LDS above 64 KB is enabled once per device and
+// instantiation (a bit per device id below 64, every launch above).
+template <int BM, int BN, int S, int EPI>
+hipError_t launch_ws_epi(dim3 grid, hipStream_t st, const cf_gemm_args_t& a, const Tiling& t) {
+    constexpr unsigned lds = ws_lds_bytes<BM, BN, S>();
+    static std::atomic<uint64_t> raised{0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev >= 64 || !((raised.load(std::memory_order_acquire) >> dev) & 1u)) {
+        e = hipFuncSetAttribute((const void*)gemm_f16_ws<BM, BN, S, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds);
+        if (e != hipSuccess) return e;
+        if (dev < 64) raised.fetch_or(1ull << dev, std::memory_order_release);
+    }
+    hipLaunchKernelGGL((gemm_f16_ws<BM, BN, S, EPI>), grid, dim3(512), lds, st, a, t);
+    return hipSuccess;
+}
+
+template <int BM, int BN, int S>
+hipError_t launch_ws(dim3 grid, hipStream_t st, const cf_gemm_args_t& a, const Tiling& t) {
+    if (a.out_kind == CF_GEMM_OUT_QKV) return launch_ws_epi<BM, BN, S, WS_EPI_QKV>(grid, st, a, t);
+    if (a.residual) return launch_ws_epi<BM, BN, S, WS_EPI_RESIDUAL>(grid, st, a, t);
+    return launch_ws_epi<BM, BN, S, WS_EPI_ROWMAJOR>(grid, st, a, t);
+}
+
+struct WsCandidate {
+    int bm, bn;
+    unsigned lds;
+    hipError_t (*launch)(dim3, hipStream_t, const cf_gemm_args_t&, const Tiling&);
+};
+// 256-row tiles hold 192 columns on 2 stages (LDS), narrower ones on 3; 128-row tiles on 3.
+const WsCandidate kWsShapes[] = {
+    {256, 192, ws_lds_bytes<256, 192, 2>(), launch_ws<256, 192, 2>},
+    {256, 144, ws_lds_bytes<256, 144, 3>(), launch_ws<256, 144, 3>},
+    {256, 128, ws_lds_bytes<256, 128, 3>(), launch_ws<256, 128, 3>},
+    {256, 96, ws_lds_bytes<256, 96, 3>(), launch_ws<256, 96, 3>},
+    {256, 64, ws_lds_bytes<256, 64, 3>(), launch_ws<256, 64, 3>},
+    {256, 48, ws_lds_bytes<256, 48, 3>(), launch_ws<256, 48, 3>},
+    {128, 192, ws_lds_bytes<128, 192, 3>(), launch_ws<128, 192, 3>},
+    {128, 128, ws_lds_bytes<128, 128, 3>(), launch_ws<128, 128, 3>},
+    {128, 96, ws_lds_bytes<128, 96, 3>(), launch_ws<128, 96, 3>},
+    {128, 64, ws_lds_bytes<128, 64, 3>(), launch_ws<128, 64, 3>},
+};
+
+// The wave-specialised shape for this product, or nullptr where the kernel does not apply
+// (fp16 only; 16-byte aligned rows and stores; M a multiple of the tile height; K a
+// multiple of 64; every segment width a multiple of 8; 32-bit A offsets).
+const WsCandidate* ws_pick(const cf_gemm_args_t* a, const Tiling& t) {
+    if (g_gemm_ws == 1 || a->elem != CF_ELEM_F16 || !t.epi_vec || !t.a_vec) return nullptr;
+    // Row-major outputs only by default: with the Q|K|V scatter the kernel measured no
+    // faster than the pipelined one (BERT-base 4096 x 2304 x 768: 23.8 vs 23.2 us with
+    // biases; the same product stored row-major takes 19.2 us), while the output
+    // projections gain (4096 x 768 x 768: 8.4 vs 9.9 us; 4096 x 1024 x 1024: 12.1 vs
+    // 13.3 us).  A tile override (cf_gemm_set_ws_shape) still routes the scatter here.
+    if (a->out_kind != CF_GEMM_OUT_ROWMAJOR && g_gemm_ws_bm == 0) return nullptr;
+    if (a->K % WS_BK != 0 || (long long)a->M * a->K * 2 >= (1LL << 32)) return nullptr;
+    long long ntot = 0;
+    for (int s = 0; s < a->nseg; s++) {
+        if (!t.w_vec[s] || a->n[s] % 8 != 0 || (uintptr_t)a->bias[s] % 16 != 0) return nullptr;
+        ntot += a->n[s];
+    }
+    const bool res32 = a->residual != nullptr && a->out_kind == CF_GEMM_OUT_ROWMAJOR;
+    const WsCandidate* best = nullptr;
+    double best_cost = 0.0;
+    for (const WsCandidate& c : kWsShapes) {
+        if (a->M % c.bm != 0 || ntot % c.bn != 0) continue;
+        // The staged tile (fp32 with a residual, else fp16) fits in the rings.
+        const unsigned staged = res32 ? (unsigned)c.bm * (c.bn + 4) * 4u : (unsigned)c.bm * (c.bn + 8) * 2u;
+        const unsigned staged_vt = (unsigned)c.bn * (c.bm + 8) * 2u;     // v^T tiles, column-major
+        if (staged > c.lds || staged_vt > c.lds) continue;
+        if (c.bm == g_gemm_ws_bm && c.bn == g_gemm_ws_bn) return &c;   // an override that fits
+        const double cost = ws_cost(a->M, ntot, a->K, c.bm, c.bn, cu_count());
+        if (!best || cost < best_cost) {
+            best = &c;
+            best_cost = cost;
+        }
+    }
+    return best;
+}
+
 }  // namespace
 
 extern "C" void cf_gemm_set_stages(int32_t stages) { g_gemm_stages = stages; }
@@ -794,6 +1313,13 @@ extern "C" void cf_gemm_set_bk(int32_t bk) { g_gemm_bk = bk == 32 || bk == 64 ? 
 extern "C" void cf_gemm_set_ksplit(int32_t ks) { g_gemm_ksplit = ks == 1 || ks == 2 ? ks : 0; }
 
 extern "C" void cf_gemm_set_bn(int32_t bn) { g_gemm_bn = bn == 96 || bn == 128 || bn == 192 ? bn : 0; }
+
+extern "C" void cf_gemm_set_ws(int32_t mode) { g_gemm_ws = mode == 1 ? 1 : 0; }
+
+extern "C" void cf_gemm_set_ws_shape(int32_t bm, int32_t bn) {
+    g_gemm_ws_bm = bm > 0 ? bm : 0;
+    g_gemm_ws_bn = bn > 0 ? bn : 0;
+}
 
 int g_gemm_group_m = 0;  // tuning override of the tile-order group height (0 = kGroupM)
 
@@ -816,6 +1342,17 @@ extern "C" int cf_launch_gemm(const cf_gemm_args_t* a, void* stream) {
     else ev = ev && a->d % 8 == 0 && a->S % 8 == 0;
     t.epi_vec = ev;
     t.group_m = g_gemm_group_m > 0 ? g_gemm_group_m : kGroupM;
+    // The wave-specialised kernel where it applies (its tile chosen by the cost model).
+    if (const WsCandidate* c = ws_pick(a, t)) {
+        long long ntot = 0;
+        for (int s = 0; s < a->nseg; s++) ntot += a->n[s];
+        t.n_tiles_m = a->M / c->bm;
+        const long long blocks = (long long)t.n_tiles_m * (ntot / c->bn);
+        if (blocks <= 0 || blocks > 0x7fffffffLL) return (int)hipErrorInvalidValue;
+        const hipError_t e = c->launch(dim3((unsigned)blocks), (hipStream_t)stream, *a, t);
+        if (e != hipSuccess) return (int)e;
+        return (int)hipGetLastError();
+    }
     // Full tiles with aligned rows take the pipelined direct-to-LDS kernel.  Its tile is
     // 128 columns wide unless that leaves CUs idle and 96 columns fills more of them
     // (BERT-base's 4096 x 768 output projection: 192 tiles of 128 x 128 on 256 CUs, 256 of

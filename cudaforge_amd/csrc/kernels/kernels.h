@@ -192,6 +192,12 @@ void cf_gemm_set_bk(int32_t bk);
  * tile; 2: two groups of 4 waves, each over half of K, where K % 128 == 0; 0 = automatic:
  * two groups when the grid has at most one tile per CU). */
 void cf_gemm_set_ksplit(int32_t ks);
+/* The fp16 wave-specialised GEMM (256- or 128-row tiles; 4 loader and 4 compute waves):
+ * mode 0 = used wherever it applies, 1 = never (the other kernels run). */
+void cf_gemm_set_ws(int32_t mode);
+/* Tuning/test override of that kernel's tile (BM 256 or 128, BN among its widths; 0, 0 =
+ * the cost model's choice).  A product the tile does not fit takes the cost model's. */
+void cf_gemm_set_ws_shape(int32_t bm, int32_t bn);
 
 /* ---------------------------------------------------------------------------------
  * Prefill attention (flash style, online softmax): q (B, H_q, S, d), k (B, H_kv, S, d),

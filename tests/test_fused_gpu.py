@@ -167,6 +167,44 @@ def test_flash_kernel_variants_agree(gpu, native, causal):
         assert max_abs(outs[0], o) <= 1e-2
 
 
+WS_SHAPES = [(256, 192), (256, 144), (256, 128), (256, 96), (256, 64), (256, 48), (128, 192), (128, 128),
+             (128, 96), (128, 64)]
+
+
+@pytest.mark.parametrize("H,H_kv", [(6, 6), (6, 2)])
+def test_gemm_wave_specialised_shapes_agree(gpu, native, H, H_kv):
+    """The wave-specialised fp16 projection GEMM at each of its tiles (a tile that does not
+    fit a product leaves that product to the cost model's choice).  D = 384, M = 256: the
+    QKV product's 144-column tiles straddle the Q|K and K|V boundaries; WO carries a bias
+    and a residual (fp32 staging); H_kv = 2 gives K and V segments narrower than Q.  Every
+    run within the FP16 bound of the oracle and bit-identical to the others (each output
+    element sums the same 32-k MFMA steps in the same order), and within a few fp16 ulps
+    of the kernels it replaces and of the default choice (the QKV product keeps the
+    pipelined kernel unless a tile is forced)."""
+    c = FusedCase(2, 128, H, H_kv, 64, seed=95, f16=True, causal=True, residual=True, bias_std=0.02)
+    want = c.oracle()
+    outs = []
+    try:
+        for bm, bn in WS_SHAPES:
+            native.cf_gemm_set_ws_shape(bm, bn)
+            outs.append(run_fused_gpu(c))
+        native.cf_gemm_set_ws_shape(0, 0)
+        auto = run_fused_gpu(c)
+        native.cf_gemm_set_ws(1)
+        native.cf_gemm_set_ksplit(1)
+        old = run_fused_gpu(c)
+    finally:
+        native.cf_gemm_set_ws_shape(0, 0)
+        native.cf_gemm_set_ws(0)
+        native.cf_gemm_set_ksplit(0)
+    for o in outs + [auto, old]:
+        assert max_abs(want, o) <= TOL16
+    for o in outs[1:]:
+        assert np.array_equal(outs[0], o)
+    assert max_abs(outs[0], old) <= 1e-2
+    assert max_abs(outs[0], auto) <= 1e-2
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_gemm_tile_widths_agree(gpu, native, causal):
     """The fp16 projection GEMM with 128-, 96- and 192-column tiles on a shape all fit
@@ -177,11 +215,13 @@ def test_gemm_tile_widths_agree(gpu, native, causal):
     want = c.oracle()
     outs = []
     try:
+        native.cf_gemm_set_ws(1)       # the kernels this test is about
         native.cf_gemm_set_ksplit(1)   # one k group everywhere, so the sums match bit for bit
         for bn in (128, 96, 192, 0):
             native.cf_gemm_set_bn(bn)
             outs.append(run_fused_gpu(c))
     finally:
+        native.cf_gemm_set_ws(0)
         native.cf_gemm_set_bn(0)
         native.cf_gemm_set_ksplit(0)
     for o in outs:
@@ -199,12 +239,14 @@ def test_gemm_stage_depths_agree(gpu, native):
     want = c.oracle()
     outs = []
     try:
+        native.cf_gemm_set_ws(1)       # the kernels this test is about
         native.cf_gemm_set_ksplit(1)
         for bk, stages in ((32, 3), (32, 4), (64, 0), (0, 0)):
             native.cf_gemm_set_bk(bk)
             native.cf_gemm_set_stages(stages)
             outs.append(run_fused_gpu(c))
     finally:
+        native.cf_gemm_set_ws(0)
         native.cf_gemm_set_bk(0)
         native.cf_gemm_set_stages(0)
         native.cf_gemm_set_ksplit(0)
@@ -225,11 +267,13 @@ def test_gemm_two_k_groups(gpu, native, bn):
         want = case.oracle()
         outs = []
         try:
+            native.cf_gemm_set_ws(1)
             native.cf_gemm_set_bn(bn)
             for ks in (1, 2):
                 native.cf_gemm_set_ksplit(ks)
                 outs.append(run_fused_gpu(case))
         finally:
+            native.cf_gemm_set_ws(0)
             native.cf_gemm_set_ksplit(0)
             native.cf_gemm_set_bn(0)
         for o in outs:
