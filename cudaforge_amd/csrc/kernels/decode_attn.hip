@@ -357,6 +357,206 @@ __device__ __forceinline__ void split_range(const cf_decode_attn_args_t& a, _Flo
     }
 }
 
+// K in registers (grouped kernel): the score MFMA's A operand is 16 contiguous bytes of
+// one K row per lane (row lr, dims 32kt + 8lq .. +7), so K goes straight from HBM into
+// VGPRs with ordinary loads and only V, which the value MFMA needs transposed, takes the
+// LDS ring.  That frees the ring for V alone: NSV stages of 16 positions, NV = NSV - 1
+// blocks of V in flight, and K runs NK = P - 1 blocks ahead in P rotating register sets.
+// Per block a wave issues KT K loads (compiler-visible) then NI V DMAs (inline asm).
+// Waits: vmcnt counts both kinds, but a DMA into LDS and a load into VGPRs issued after
+// it do not complete in issue order relative to each other (measured: counting the K
+// loads issued after V[j] as complete let the value MFMA read a stage before its DMA had
+// landed), while each kind completes in order within itself.  So the wait for V[j]
+// allows only the V DMAs issued after it to be outstanding, vmcnt(NI * ahead), whatever
+// the K loads are doing; that also leaves at most NI * NV <= KT * NK of the K loads issued
+// after K[j] outstanding, so K[j] has landed too.  The compiler's own wait before K[j]'s
+// first use counts only K loads and is then already met.
+// f(std::integral_constant<int, i>) for i = 0 .. N-1, unrolled.
+template <typename F, int... S>
+__device__ __forceinline__ void static_for_seq(F& f, std::integer_sequence<int, S...>) {
+    (f(std::integral_constant<int, S>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_seq(f, std::make_integer_sequence<int, N>{});
+}
+
+template <int D>
+struct KvRing {
+    static constexpr int KT = D / 32;        // 32-dim MFMA steps (K loads per block per lane)
+    static constexpr int CPR = D / 8;        // 16-byte chunks per row
+    static constexpr int RPI = 64 / CPR;     // rows per V DMA instruction (1 KB)
+    static constexpr int NI = 16 / RPI;      // V DMA instructions per 16-position block
+    static constexpr int TILE = 16 * D;      // halves of one V stage
+    static constexpr int NT = D / 16;        // output tiles of 16 dims
+};
+
+template <int D, int G, int NSV, int P>
+__device__ __forceinline__ void split_range_kv(const cf_decode_attn_args_t& a, _Float16* ring, int b, int kvh,
+                                               int t0, int t1, float* part) {
+    using R = KvRing<D>;
+    constexpr int KT = R::KT, CPR = R::CPR, RPI = R::RPI, NI = R::NI, TILE = R::TILE, NT = R::NT;
+    constexpr int NV = NSV - 1, NK = P - 1;
+    constexpr int HDR = part_hdr(G);
+    static_assert(NI * NV <= KT * NK, "the V wait also covers K[j]");
+    static_assert(NI * NV < 64, "vmcnt range");
+    const int nblk = (t1 - t0 + 15) / 16;
+    const int lane = threadIdx.x & 63, lr = lane & 15, lq = lane >> 4;
+    wait_lds_reads();                                     // a previous range's reads of the ring
+
+    const uint32_t row_stride = (uint32_t)a.H_kv * D;     // halves
+    const size_t unit_off = ((size_t)b * a.max_seq * a.H_kv + kvh) * D;
+    const _Float16* __restrict__ kg = (const _Float16*)a.k + unit_off;
+    const _Float16* __restrict__ vg = (const _Float16*)a.v + unit_off;
+    const int h0 = kvh * G;
+    const float qk_scale = a.scale * kLog2e;
+
+    // Q^T (B operand): lane (lr, lq) holds Q[head lr][32kt + 8lq .. +7]; heads >= G are 0.
+    h8_t qf[KT];
+    {
+        const _Float16* qs = (const _Float16*)a.q + ((size_t)b * a.H_q + h0 + min(lr, G - 1)) * D + 8 * lq;
+#pragma unroll
+        for (int kt = 0; kt < KT; kt++) qf[kt] = *(const h8_t*)(qs + 32 * kt);
+#pragma unroll
+        for (int kt = 0; kt < KT; kt++)
+            if (lr >= G) qf[kt] = h8_t{};
+    }
+
+    // K rows as a uniform base plus a 32-bit per-lane byte offset (the saddr form of
+    // global_load_dwordx4: no per-lane 64-bit addresses held across the loop).
+    h8_t kf[P][KT];
+    const char* kgb = (const char*)kg;
+    auto load_k = [&](int blk, auto set_c) {
+        constexpr int set = decltype(set_c)::value;
+        const uint32_t row = (uint32_t)min(t0 + 16 * blk + lr, t1 - 1);
+        const uint32_t off = row * row_stride * 2u + 16u * (uint32_t)lq;
+#pragma unroll
+        for (int kt = 0; kt < KT; kt++) kf[set][kt] = *(const h8_t*)(kgb + off + 64u * kt);
+    };
+
+    const uint32_t ring_base = lds_offset(ring);
+    const int drow = lane / CPR, dchunk = lane % CPR;
+    uint32_t voff[NI];
+#pragma unroll
+    for (int u = 0; u < NI; u++) {
+        const int row = RPI * u + drow;
+        voff[u] = (uint32_t)row * row_stride * 2u + 16u * (uint32_t)(dchunk ^ vswz<D>(row));
+    }
+    auto issue_v = [&](int blk, int stage) {
+        const int p0 = t0 + 16 * blk;
+        const uint32_t vbase = ring_base + (uint32_t)(stage * TILE) * 2u;
+        if (p0 + 16 <= t1) {
+            const _Float16* vblk = vg + (size_t)p0 * row_stride;
+#pragma unroll
+            for (int u = 0; u < NI; u++) lds_dma16_s(voff[u], vblk, vbase + u * 1024u);
+        } else {
+#pragma unroll
+            for (int u = 0; u < NI; u++) {
+                const int row = RPI * u + drow;
+                const size_t g_row = (size_t)min(p0 + row, t1 - 1) * row_stride;
+                lds_dma16(vg + g_row + 8 * (dchunk ^ vswz<D>(row)), vbase + u * 1024u);
+            }
+        }
+    };
+    int v_rd[NT];
+#pragma unroll
+    for (int n = 0; n < NT; n++) {
+        const int row = 4 * lq + (lr >> 2);
+        const int col = 16 * n + 4 * (lr & 3);
+        v_rd[n] = row * D + 8 * ((col >> 3) ^ vswz<D>(row)) + (col & 7);
+    }
+
+    f4_t acc[NT];
+#pragma unroll
+    for (int n = 0; n < NT; n++) acc[n] = f4_t{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    // Prologue: the issue order of steps -NK .. -1 (K of blocks 0 .. NK-1, V of 0 .. NV-1).
+    static_for<NK>([&](auto s_c) {
+        constexpr int S = decltype(s_c)::value;
+        load_k(S, s_c);
+        if (S >= NK - NV && S - (NK - NV) < nblk) issue_v(S - (NK - NV), S - (NK - NV));
+    });
+
+    // The V stage is a runtime index (blk % NSV, kept in an SGPR), so the K register
+    // rotation P need not be a multiple of NSV.
+    int stage = 0;
+    auto step = [&](int blk, auto set_c) {
+        constexpr int set = decltype(set_c)::value;           // == blk % P
+        load_k(blk + NK, std::integral_constant<int, (set + NK) % P>{});
+        if (blk + NV < nblk) {
+            wait_lds_reads();                                  // block blk - 1's reads of that stage
+            issue_v(blk + NV, stage == 0 ? NV : stage - 1);    // (blk + NV) % NSV
+        }
+        wait_ahead<NI, NV>(min(NV, nblk - 1 - blk));
+
+        f4_t s = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kt = 0; kt < KT; kt++) s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[set][kt], qf[kt], s, 0, 0, 0);
+        const int p0 = t0 + 16 * blk;
+        float x[4] = {s[0], s[1], s[2], s[3]};
+        if (p0 + 16 > t1) {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (p0 + 4 * lq + j >= t1) x[j] = -INFINITY;
+        }
+        float mb = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+        mb = max_xor32(max_xor16(mb)) * qk_scale;
+        const bool grow = mb > m_run + kLazyMax;
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+            const float m_new = grow ? mb : m_run;
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+            l_run *= alpha;
+#pragma unroll
+            for (int n = 0; n < NT; n++) acc[n] *= alpha;
+        }
+        float ps = 0.0f;
+        _Float16 pv[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(x[i], qk_scale, -m_run));
+            ps += p;
+            pv[i] = (_Float16)p;
+        }
+        l_run += ps;
+        const h4_t pf = {pv[0], pv[1], pv[2], pv[3]};
+        const _Float16* st = ring + stage * TILE;
+#pragma unroll
+        for (int n = 0; n < NT; n++)
+            acc[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(ds_read_tr4(st + v_rd[n]), pf, acc[n], 0, 0, 0);
+        stage = stage == NSV - 1 ? 0 : stage + 1;
+    };
+    // Whole groups of P blocks unconditionally (the same loads on every path, so the
+    // compiler's waits hold across the back edge), then the last nblk % P blocks.
+    int i0 = 0;
+    for (; i0 + P <= nblk; i0 += P) static_for<P>([&](auto s_c) { step(i0 + decltype(s_c)::value, s_c); });
+    static_for<P - 1>([&](auto s_c) {
+        if (i0 + decltype(s_c)::value < nblk) step(i0 + decltype(s_c)::value, s_c);
+    });
+
+    l_run = add_xor32(add_xor16(l_run));
+    if (lr >= G) return;
+    if (!part) {
+        const float inv = 1.0f / l_run;
+        _Float16* out = (_Float16*)a.o + ((size_t)b * a.H_q + h0 + lr) * D + 4 * lq;
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+            h4_t o;
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[i] = (_Float16)(acc[n][i] * inv);
+            *(h4_t*)(out + 16 * n) = o;
+        }
+        return;
+    }
+#pragma unroll
+    for (int n = 0; n < NT; n++) *(f4_t*)(part + HDR + lr * D + 16 * n + 4 * lq) = acc[n];
+    if (lq == 0) {
+        part[lr] = m_run;
+        part[G + lr] = l_run;
+    }
+}
+
 template <int D, int G, int NS, bool WIDE = false>
 __global__ __launch_bounds__(WIDE ? 512 : 64)
 void split_f16(cf_decode_attn_args_t a) {
@@ -395,6 +595,45 @@ void split_f16(cf_decode_attn_args_t a) {
     const int nsplit_b = (T_b + a.chunk - 1) / a.chunk;
     split_range<D, G, NS, WIDE>(a, ring, b, kvh, t0, min(t0 + a.chunk, T_b),
                                 nsplit_b == 1 ? nullptr : partial_at(a, b * a.H_kv + kvh, split, G, D));
+}
+
+// The grouped kernel with K in registers (split_range_kv): a wave per KV head, each with
+// an NSV-stage V ring; otherwise the same grid and ranges as split_f16<..., WIDE>.
+// Config 2 (rotating KV sets, one box): split 44.85-44.88 us at 4 stages and 7 sets,
+// 45.2-45.5 us at 5 stages (all 160 KB of LDS), 45.2 us with 5 sets; the K-and-V ring
+// kernel 46.2 us.
+constexpr int kKvStages = 4;    // V ring stages per wave (4 KB each at d = 128)
+constexpr int kKvSets = 7;      // K register sets per wave (K runs 6 blocks ahead)
+template <int D, int G, int NSV = kKvStages, int NSETS = kKvSets>
+__global__ __launch_bounds__(512)
+void split_f16_kv(cf_decode_attn_args_t a) {
+    constexpr int WAVE_LDS = NSV * KvRing<D>::TILE;
+    __shared__ __attribute__((aligned(16))) _Float16 ring_all[8 * WAVE_LDS];
+    const int kvh = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    _Float16* ring = ring_all + kvh * WAVE_LDS;
+    if (a.balanced) {
+        const BalancedGeom geo = balanced_geom(a);
+        const int lo = (int)blockIdx.x * geo.R, hi = min(lo + geo.R, geo.W);
+        for (int b = 0; b < a.B; b++) {
+            const int P = __builtin_amdgcn_readlane(geo.P, b), T = __builtin_amdgcn_readlane(geo.T, b);
+            if (P >= hi) break;
+            if (P + T <= lo) continue;
+            const int first = P / geo.R, ns = __builtin_amdgcn_readlane(geo.ns, b);
+            float* part = ns == 1 ? nullptr
+                                  : a.partials + ((size_t)(__builtin_amdgcn_readlane(geo.pieces, b) +
+                                                           (int)blockIdx.x - first) * a.H_kv + kvh) *
+                                                     part_stride(G, D);
+            split_range_kv<D, G, NSV, NSETS>(a, ring, b, kvh, max(lo - P, 0), min(hi - P, T), part);
+        }
+        return;
+    }
+    const int split = blockIdx.x, b = blockIdx.y;
+    const int T_b = attended(a, b);
+    const int t0 = split * a.chunk;
+    if (t0 >= T_b) return;
+    const int nsplit_b = (T_b + a.chunk - 1) / a.chunk;
+    split_range_kv<D, G, NSV, NSETS>(a, ring, b, kvh, t0, min(t0 + a.chunk, T_b),
+                                             nsplit_b == 1 ? nullptr : partial_at(a, b * a.H_kv + kvh, split, G, D));
 }
 
 // ------------------------------------------------------------------ fp32 split ---
@@ -856,6 +1095,7 @@ int merge_rows_dsplit(int d) {
 int g_merge_wave_wg = 2; // rows (waves) per merge_wave workgroup (2 and 1 measured 0.15-0.2 us faster than 4)
 
 int g_wide = 1;     // 0: one workgroup per (split, KV head) even where the grouped kernel applies
+int g_kreg = 1;     // 0: the grouped kernel keeps K in its LDS ring too (d = 128)
 
 int f16_stages() { return g_stages >= 2 && g_stages <= 4 ? g_stages : kDecodeStages; }
 
@@ -881,12 +1121,32 @@ bool use_wide(const cf_decode_attn_args_t* a) {
            a->H_kv <= kWideMaxHeads && use_fast(a);
 }
 
+// split_f16_kv's vmcnt waits count the loads the kernel itself issues; a register
+// spill would add scratch loads between them.  The build has none (checked once here,
+// from the code object), else the K-and-V ring kernel runs instead.
+template <int D, int G>
+bool kv_kernel_ok() {
+    static const bool ok = [] {
+        hipFuncAttributes at;
+        return hipFuncGetAttributes(&at, reinterpret_cast<const void*>(&split_f16_kv<D, G>)) == hipSuccess &&
+               at.localSizeBytes == 0;
+    }();
+    return ok;
+}
+
 template <int D, int G>
 hipError_t launch_split_fast(const cf_decode_attn_args_t& a, hipStream_t s) {
     dim3 grid((unsigned)a.n_split, (unsigned)a.H_kv, (unsigned)a.B);
     if (use_wide(&a)) {
         const dim3 wgrid = a.balanced ? dim3((unsigned)a.n_split) : dim3((unsigned)a.n_split, (unsigned)a.B);
-        hipLaunchKernelGGL((split_f16<D, G, kWideStages, true>), wgrid, dim3(64 * (unsigned)a.H_kv), 0, s, a);
+        bool kreg = false;
+        if constexpr (D == 128) {
+            if (g_kreg && kv_kernel_ok<D, G>()) {
+                kreg = true;
+                hipLaunchKernelGGL((split_f16_kv<D, G>), wgrid, dim3(64 * (unsigned)a.H_kv), 0, s, a);
+            }
+        }
+        if (!kreg) hipLaunchKernelGGL((split_f16<D, G, kWideStages, true>), wgrid, dim3(64 * (unsigned)a.H_kv), 0, s, a);
     } else if (a.elem == CF_ELEM_F16) {
         switch (f16_stages()) {
             case 2: hipLaunchKernelGGL((split_f16<D, G, 2>), grid, dim3(64), 0, s, a); break;
@@ -925,6 +1185,18 @@ extern "C" void cf_decode_attn_set_merge_rows_split(int32_t ds) { g_merge_rows_d
 extern "C" void cf_decode_attn_set_merge_wave_wg(int32_t rows) { g_merge_wave_wg = rows >= 1 && rows <= 4 ? rows : 2; }
 
 extern "C" void cf_decode_attn_set_wide(int32_t on) { g_wide = on != 0; }
+
+extern "C" void cf_decode_attn_set_kreg(int32_t on) { g_kreg = on != 0; }
+
+extern "C" int32_t cf_decode_attn_kreg_ok(int32_t group) {
+    switch (group) {
+        case 1: return kv_kernel_ok<128, 1>();
+        case 2: return kv_kernel_ok<128, 2>();
+        case 4: return kv_kernel_ok<128, 4>();
+        case 8: return kv_kernel_ok<128, 8>();
+        default: return 0;
+    }
+}
 
 extern "C" int32_t cf_decode_attn_wide_wgs_per_cu(int32_t elem, int32_t d, int32_t group, int32_t h_kv) {
     if (!g_wide || elem != CF_ELEM_F16 || h_kv > kWideMaxHeads || !fast_supported(elem, d, group)) return 0;

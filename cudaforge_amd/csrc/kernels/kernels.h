@@ -59,6 +59,12 @@ void    cf_decode_attn_set_stages(int32_t stages);
  * head) kernel everywhere (tests and measurements; default 1). */
 int32_t cf_decode_attn_wide_wgs_per_cu(int32_t elem, int32_t d, int32_t group, int32_t h_kv);
 void    cf_decode_attn_set_wide(int32_t on);
+/* The grouped kernel at d = 128 loads K straight into registers and keeps only V in its
+ * LDS ring (default 1); 0 selects the K-and-V ring (tests and measurements). */
+void    cf_decode_attn_set_kreg(int32_t on);
+/* 1 when that kernel's build for GQA group `group` (1, 2, 4, 8) holds no register spills,
+ * which its load counting needs; else the K-and-V ring kernel runs in its place. */
+int32_t cf_decode_attn_kreg_ok(int32_t group);
 /* Tests: 1 selects the workgroup-per-row merge for every head size (0 = the one-wave
  * merge for d = 64 / 128). */
 void    cf_decode_attn_set_merge_rows(int32_t on);

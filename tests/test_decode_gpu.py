@@ -456,6 +456,38 @@ def test_grouped_and_one_wave_split_kernels_agree(gpu, native, d, G, H_kv, T):
     assert max_abs(outs[0], outs[1]) <= TOL16
 
 
+@pytest.mark.parametrize("G,H_kv", [(4, 8), (1, 2), (2, 4), (8, 2)])
+@pytest.mark.parametrize("chunk", [0, 32, 96, 128, 160, 256])
+def test_grouped_kernel_k_in_registers_matches_lds_ring(gpu, native, G, H_kv, chunk):
+    """The grouped kernel at d = 128 loads K straight into registers (seven 16-position
+    blocks ahead, eight register sets) and keeps only V in its LDS ring;
+    cf_decode_attn_set_kreg(0) selects the kernel with K in the ring too.  Same MFMA
+    operands in the same order, so bit-identical outputs: uniform lengths cut into
+    splits of fewer, exactly and more than eight blocks (the unrolled group), lengths
+    that end inside a block, and ragged lengths on the balanced partition."""
+    assert native.cf_decode_attn_kreg_ok(G) == 1
+    B, d, T = 3, 128, 1000
+    H = H_kv * G
+    Q, K, V = (O.round_f16(O.normal(s, 530 + i)) for i, s in enumerate([(B, H, d), (B, T, H_kv, d), (B, T, H_kv, d)]))
+    lens = np.array([T - 1, 17, 513], np.int32)
+    outs = []
+    try:
+        native.mha_decode_set_split_chunk(chunk)
+        for kreg in (1, 0):
+            native.cf_decode_attn_set_kreg(kreg)
+            outs.append((run_decode_attn_gpu(Q, K, V, T - 1, H_kv, True),
+                         run_decode_attn_gpu(Q, K, V, None, H_kv, True, seq_lens=lens - 1)))
+    finally:
+        native.cf_decode_attn_set_kreg(1)
+        native.mha_decode_set_split_chunk(0)
+    want = O.decode_attn(Q, K, V, np.full(B, T, np.int32), float(1 / np.sqrt(d)), H_kv)
+    assert max_abs(want, outs[0][0]) <= TOL16
+    want = O.decode_attn(Q, K, V, lens, float(1 / np.sqrt(d)), H_kv)
+    assert max_abs(want, outs[0][1]) <= TOL16
+    assert np.array_equal(outs[0][0], outs[1][0])
+    assert np.array_equal(outs[0][1], outs[1][1])
+
+
 @pytest.mark.parametrize("f16", [False, True])
 def test_graph_decode_replay(gpu, native, f16):
     """A decode graph executed repeatedly at one cache_len (each execution rewrites row
