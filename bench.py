@@ -491,7 +491,7 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU oracle timing")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-core", action="store_true", help="time only the headline kernel (for profiling)")
@@ -624,8 +624,10 @@ def main() -> int:
         "config": {"workload": "MHA_Decode GQA Llama-3-8B attention core (config 2): split-KV + LSE merge "
                                "(split kernel + merge kernel per step)", **cfg},
         "roofline": {"bound": "hbm", "achieved": round(gbs_split, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs_split / HBM_PEAK_GBS, 4), "traffic": read_traffic("split_f16"),
-                     "kernel": "split_f16<128,4,2,wide> (decode_attn.hip; a workgroup per (split, batch row), a wave per KV head)", "alg_bytes_per_launch": alg_bytes,
+                     "frac": round(gbs_split / HBM_PEAK_GBS, 4), "traffic": read_traffic("split_f16_kv"),
+                     "kernel": "split_f16_kv<128,4> (decode_attn.hip; a workgroup per (split, batch row), a wave per KV "
+                               "head, K loaded into registers, V through a 4-stage LDS ring)",
+                     "alg_bytes_per_launch": alg_bytes,
                      "kernel_us": round(ms_split * 1e3, 2), "merge_kernel_us": round(ms_merge * 1e3, 2),
                      "step": {"what": "the whole step (split + merge launches), as `value`",
                               "achieved": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
