@@ -251,8 +251,10 @@ constexpr float kLazy = 8.0f;
 __device__ __forceinline__ int fswz(int row) { return (row >> 1) & 7; }
 __device__ __forceinline__ int vswz(int row) { return ((row >> 1) ^ (row >> 4)) & 7; }
 
+// Waves per SIMD the build must allow: three 16-query workgroups per CU; the 32-query
+// build (taken with at least two workgroups per CU) at three would spill registers.
 template <int NJ>
-__global__ __launch_bounds__(kThreads, 3)
+__global__ __launch_bounds__(kThreads, NJ == 1 ? 3 : 2)
 void flash_f16_dma64(cf_flash_args_t a) {
     constexpr int D = 64;
     constexpr int QW = 16 * NJ;                   // queries per wave
