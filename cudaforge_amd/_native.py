@@ -107,6 +107,7 @@ def _proto(lib):
         "synthetic_fill_normal": (c_int, [c_void_p, c_int64, c_int, ctypes.c_uint64, c_float, c_float, c_void_p]),
         # decode planning knobs
         "mha_decode_set_split_chunk": (None, [c_int64]),
+        "mha_fused_set_rowcat": (None, [c_int]),
         "cf_gemv_set_dma_tile": (None, [c_int32]),
         "cf_gemv_set_dma_ksplit": (None, [c_int32]),
         "cf_gemv_set_small": (None, [c_int32]),

@@ -251,9 +251,15 @@ constexpr float kLazy = 8.0f;
 __device__ __forceinline__ int fswz(int row) { return (row >> 1) & 7; }
 __device__ __forceinline__ int vswz(int row) { return ((row >> 1) ^ (row >> 4)) & 7; }
 
+// V rows [key][dim] (the row-concatenated input), read transposed by ds_read_b64_tr_b16:
+// rows of one 32-lane half of a read (keys kb .. kb+7) land in distinct banks.
+__device__ __forceinline__ int trswz(int row) { return 2 * ((row >> 1) & 3); }
+
+// RC: Q, K and V come from the row-concatenated (B*S, qkv_ld) matrix (K and V rows as
+// they are; V read transposed from LDS), else from q / k / vt laid out head-major.
 // Waves per SIMD the build must allow: three 16-query workgroups per CU; the 32-query
 // build (taken with at least two workgroups per CU) at three would spill registers.
-template <int NJ>
+template <int NJ, bool RC = false>
 __global__ __launch_bounds__(kThreads, NJ == 1 ? 3 : 2)
 void flash_f16_dma64(cf_flash_args_t a) {
     constexpr int D = 64;
@@ -285,9 +291,16 @@ void flash_f16_dma64(cf_flash_args_t a) {
     const int lr = lane & 15, lq = lane >> 4;
     const int qw = q0 + QW * wave;                 // first query of this wave
 
-    const _Float16* __restrict__ qp = (const _Float16*)a.q + (((size_t)b * a.H_q + h) * S) * D;
-    const _Float16* __restrict__ kp = (const _Float16*)a.k + (((size_t)b * a.H_kv + kvh) * S) * D;
-    const _Float16* __restrict__ vp = (const _Float16*)a.vt + (((size_t)b * a.H_kv + kvh) * D) * (size_t)S;
+    // Row strides (halves) of Q and K (and of V when RC).
+    const size_t ld = RC ? (size_t)a.qkv_ld : (size_t)D;
+    const _Float16* __restrict__ rc0 = (const _Float16*)a.q + (size_t)b * S * ld;
+    const _Float16* __restrict__ qp =
+        RC ? rc0 + (size_t)h * D : (const _Float16*)a.q + (((size_t)b * a.H_q + h) * S) * D;
+    const _Float16* __restrict__ kp =
+        RC ? rc0 + (size_t)(a.H_q + kvh) * D : (const _Float16*)a.k + (((size_t)b * a.H_kv + kvh) * S) * D;
+    const _Float16* __restrict__ vp =
+        RC ? rc0 + (size_t)(a.H_q + a.H_kv + kvh) * D
+           : (const _Float16*)a.vt + (((size_t)b * a.H_kv + kvh) * D) * (size_t)S;
 
     int query[NJ];
 #pragma unroll
@@ -304,8 +317,9 @@ void flash_f16_dma64(cf_flash_args_t a) {
 #pragma unroll
     for (int u = 0; u < 2; u++) {
         const int row = drow0 + 8 * u;
-        koff[u] = (uint32_t)(row * D + 8 * (dch ^ fswz(row))) * 2u;
-        voff[u] = ((uint32_t)row * (uint32_t)S + 8u * (uint32_t)(dch ^ vswz(row))) * 2u;
+        koff[u] = ((uint32_t)row * (uint32_t)ld + 8u * (uint32_t)(dch ^ fswz(row))) * 2u;
+        voff[u] = RC ? ((uint32_t)row * (uint32_t)ld + 8u * (uint32_t)(dch ^ trswz(row))) * 2u
+                     : ((uint32_t)row * (uint32_t)S + 8u * (uint32_t)(dch ^ vswz(row))) * 2u;
     }
     auto issue = [&](int blk, auto stage_c) {
         constexpr int stage = decltype(stage_c)::value;
@@ -313,8 +327,8 @@ void flash_f16_dma64(cf_flash_args_t a) {
         const uint32_t kb = wave_lds + (uint32_t)(stage * 2 * TILE) * 2u;
         const uint32_t vb = kb + (uint32_t)TILE * 2u;
         if (k0 + kKB <= S) {
-            const _Float16* kblk = kp + (size_t)k0 * D;
-            const _Float16* vblk = vp + k0;
+            const _Float16* kblk = kp + (size_t)k0 * ld;
+            const _Float16* vblk = RC ? vp + (size_t)k0 * ld : vp + k0;
 #pragma unroll
             for (int u = 0; u < 2; u++) {
                 lds_dma16_s(koff[u], kblk, kb + (uint32_t)(8 * u) * 128u);
@@ -325,9 +339,14 @@ void flash_f16_dma64(cf_flash_args_t a) {
             for (int u = 0; u < 2; u++) {
                 const int row = drow0 + 8 * u;
                 const int kc = dch ^ fswz(row);
-                lds_dma16(kp + (size_t)min(k0 + row, S - 1) * D + 8 * kc, kb + (uint32_t)(8 * u) * 128u);
-                const int vcol = min(k0 + 8 * (dch ^ vswz(row)), S - 8);
-                lds_dma16(vp + (size_t)row * S + vcol, vb + (uint32_t)(8 * u) * 128u);
+                lds_dma16(kp + (size_t)min(k0 + row, S - 1) * ld + 8 * kc, kb + (uint32_t)(8 * u) * 128u);
+                if constexpr (RC) {
+                    lds_dma16(vp + (size_t)min(k0 + row, S - 1) * ld + 8 * (dch ^ trswz(row)),
+                              vb + (uint32_t)(8 * u) * 128u);
+                } else {
+                    const int vcol = min(k0 + 8 * (dch ^ vswz(row)), S - 8);
+                    lds_dma16(vp + (size_t)row * S + vcol, vb + (uint32_t)(8 * u) * 128u);
+                }
             }
         }
     };
@@ -347,9 +366,17 @@ void flash_f16_dma64(cf_flash_args_t a) {
         for (int s2 = 0; s2 < 2; s2++)
 #pragma unroll
             for (int hh = 0; hh < 2; hh++) {
-                const int row = 16 * u + lr;
-                const int ch = 4 * s2 + 2 * hh + (lq >> 1);          // keys 32s + 16hh + 4lq
-                v_rd[u][s2][hh] = TILE + row * kKB + 8 * (ch ^ vswz(row)) + 4 * (lq & 1);
+                if constexpr (RC) {
+                    // V[key][dim]: lane (lr, lq) addresses key 32s + 16hh + 4lq + lr/4, dims
+                    // 16u + 4(lr%4) .. +3, and receives dim 16u + lr of those 4 keys.
+                    const int row = 32 * s2 + 16 * hh + 4 * lq + (lr >> 2);
+                    const int col = 16 * u + 4 * (lr & 3);
+                    v_rd[u][s2][hh] = TILE + row * D + 8 * ((col >> 3) ^ trswz(row)) + (col & 7);
+                } else {
+                    const int row = 16 * u + lr;
+                    const int ch = 4 * s2 + 2 * hh + (lq >> 1);      // keys 32s + 16hh + 4lq
+                    v_rd[u][s2][hh] = TILE + row * kKB + 8 * (ch ^ vswz(row)) + 4 * (lq & 1);
+                }
             }
 
     const float c = a.scale * kLog2e;
@@ -377,7 +404,7 @@ void flash_f16_dma64(cf_flash_args_t a) {
 #pragma unroll
         for (int v = 0; v < QI; v++) {
             const int u = QI * wave + v, row = 8 * u + (lane >> 3);
-            lds_dma16(qp + (size_t)min(q0 + row, S - 1) * D + 8 * (dch ^ fswz(row)),
+            lds_dma16(qp + (size_t)min(q0 + row, S - 1) * ld + 8 * (dch ^ fswz(row)),
                       __builtin_amdgcn_readfirstlane(qb_lds + (uint32_t)u * 1024u));
         }
     }
@@ -465,8 +492,8 @@ void flash_f16_dma64(cf_flash_args_t a) {
         for (int u = 0; u < UT; u++)
 #pragma unroll
             for (int s2 = 0; s2 < 2; s2++) {
-                const h4_t lo = *(const h4_t*)(st + v_rd[u][s2][0]);
-                const h4_t hi = *(const h4_t*)(st + v_rd[u][s2][1]);
+                const h4_t lo = RC ? ds_read_tr4(st + v_rd[u][s2][0]) : *(const h4_t*)(st + v_rd[u][s2][0]);
+                const h4_t hi = RC ? ds_read_tr4(st + v_rd[u][s2][1]) : *(const h4_t*)(st + v_rd[u][s2][1]);
                 const h8_t vf = cat8(lo, hi);
 #pragma unroll
                 for (int j = 0; j < NJ; j++)
@@ -778,10 +805,17 @@ int g_flash_mode = 3;
 
 extern "C" void cf_flash_set_mode(int32_t mode) { g_flash_mode = mode >= 0 && mode <= 3 ? mode : 3; }
 
+extern "C" int32_t cf_flash_rowcat_ok(const cf_flash_args_t* a) {
+    return a->elem == CF_ELEM_F16 && a->d == 64 && a->S > 0 && a->S % 8 == 0 && a->S <= (1 << 24) &&
+           a->H_kv > 0 && a->H_q % a->H_kv == 0 && a->scale > 0.0f &&
+           a->qkv_ld == (a->H_q + 2 * a->H_kv) * 64 && ((uintptr_t)a->q | (uintptr_t)a->o) % 16 == 0;
+}
+
 extern "C" int cf_launch_flash_attn(const cf_flash_args_t* a, void* stream) {
     hipStream_t s = (hipStream_t)stream;
     if (a->S <= 0 || a->d <= 0 || a->H_kv <= 0 || a->H_q % a->H_kv != 0) return (int)hipErrorInvalidValue;
-    const bool aligned = ((uintptr_t)a->q | (uintptr_t)a->k | (uintptr_t)a->vt | (uintptr_t)a->o) % 16 == 0;
+    if (a->qkv_ld != 0 && !cf_flash_rowcat_ok(a)) return (int)hipErrorInvalidValue;
+    const bool aligned = a->qkv_ld ? true : ((uintptr_t)a->q | (uintptr_t)a->k | (uintptr_t)a->vt | (uintptr_t)a->o) % 16 == 0;
     // The fast kernel takes the row max of raw scores and scales it, valid for scale > 0.
     if (a->elem == CF_ELEM_F16 && aligned && (a->d == 64 || a->d == 128) && a->scale > 0.0f) {
         const long long nqb = (a->S + kQB - 1) / kQB;
@@ -789,7 +823,7 @@ extern "C" int cf_launch_flash_attn(const cf_flash_args_t* a, void* stream) {
         if (groups * nqb * 8 > 0x7fffffffLL) return (int)hipErrorInvalidValue;
         dim3 grid((unsigned)(groups * nqb * 8));
         // The DMA kernel addresses V^T rows with 32-bit byte offsets: 64 * S * 2 < 2^32.
-        if (a->d == 64 && a->S % 8 == 0 && a->S <= (1 << 24) && g_flash_mode != 0) {
+        if (a->d == 64 && a->S % 8 == 0 && a->S <= (1 << 24) && (g_flash_mode != 0 || a->qkv_ld)) {
             // 16 queries per wave (64 per workgroup) doubles the workgroups, and with
             // them the waves per SIMD that hide each block's latency chain; 32 per wave
             // halves the LDS traffic per query (every wave reads the whole K/V^T block),
@@ -800,7 +834,10 @@ extern "C" int cf_launch_flash_attn(const cf_flash_args_t* a, void* stream) {
             };
             const int nj = g_flash_mode == 1 ? 2 : g_flash_mode == 2 ? 1 : (groups * slots(2) * 8 < 2LL * cu_count() ? 1 : 2);
             dim3 grid2((unsigned)(groups * slots(nj) * 8));
-            if (nj == 1) hipLaunchKernelGGL(flash_f16_dma64<1>, grid2, dim3(kThreads), 0, s, *a);
+            if (a->qkv_ld) {
+                if (nj == 1) hipLaunchKernelGGL((flash_f16_dma64<1, true>), grid2, dim3(kThreads), 0, s, *a);
+                else hipLaunchKernelGGL((flash_f16_dma64<2, true>), grid2, dim3(kThreads), 0, s, *a);
+            } else if (nj == 1) hipLaunchKernelGGL(flash_f16_dma64<1>, grid2, dim3(kThreads), 0, s, *a);
             else hipLaunchKernelGGL(flash_f16_dma64<2>, grid2, dim3(kThreads), 0, s, *a);
         } else if (a->d == 64) hipLaunchKernelGGL(flash_f16<64>, grid, dim3(kThreads), 0, s, *a);
         else hipLaunchKernelGGL(flash_f16<128>, grid, dim3(kThreads), 0, s, *a);

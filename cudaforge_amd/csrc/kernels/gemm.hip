@@ -828,7 +828,7 @@ __device__ __forceinline__ WsEpi ws_epi(const cf_gemm_args_t& a) {
     e.Hq = a.H_q;
     e.Hkv = a.H_kv;
     e.d = a.d;
-    e.n0w = a.n[0];
+    e.n0w = a.out_kind == CF_GEMM_OUT_ROWCAT ? a.n[0] + a.n[1] + a.n[2] : a.n[0];
     // Empty asm that "modifies" every field: the loads happen here, not where first used.
     asm volatile("" : "+s"(e.out0), "+s"(e.out1), "+s"(e.out2), "+s"(e.bias0), "+s"(e.bias1), "+s"(e.bias2),
                  "+s"(e.res));
@@ -1278,7 +1278,8 @@ const WsCandidate* ws_pick(const cf_gemm_args_t* a, const Tiling& t) {
     // biases; the same product stored row-major takes 19.2 us), while the output
     // projections gain (4096 x 768 x 768: 8.4 vs 9.9 us; 4096 x 1024 x 1024: 12.1 vs
     // 13.3 us).  A tile override (cf_gemm_set_ws_shape) still routes the scatter here.
-    if (a->out_kind != CF_GEMM_OUT_ROWMAJOR && g_gemm_ws_bm == 0) return nullptr;
+    if (a->out_kind == CF_GEMM_OUT_QKV && g_gemm_ws_bm == 0) return nullptr;
+    if (a->out_kind == CF_GEMM_OUT_ROWCAT && a->residual) return nullptr;
     if (a->K % WS_BK != 0 || (long long)a->M * a->K * 2 >= (1LL << 32)) return nullptr;
     long long ntot = 0;
     for (int s = 0; s < a->nseg; s++) {
@@ -1316,6 +1317,17 @@ extern "C" void cf_gemm_set_bn(int32_t bn) { g_gemm_bn = bn == 96 || bn == 128 |
 
 extern "C" void cf_gemm_set_ws(int32_t mode) { g_gemm_ws = mode == 1 ? 1 : 0; }
 
+// The checks cf_launch_gemm runs before taking the wave-specialised kernel, for a
+// row-concatenated output (which only that kernel writes).
+extern "C" int32_t cf_gemm_rowcat_ok(const cf_gemm_args_t* a) {
+    if (a->out_kind != CF_GEMM_OUT_ROWCAT || a->nseg < 1 || a->nseg > 3 || a->M <= 0 || a->K <= 0) return 0;
+    Tiling t{};
+    t.a_vec = (a->K % 8 == 0) && ((uintptr_t)a->a % 16 == 0);
+    for (int s = 0; s < a->nseg; s++) t.w_vec[s] = (a->n[s] % 8 == 0) && ((uintptr_t)a->w[s] % 16 == 0);
+    t.epi_vec = (uintptr_t)a->out[0] % 16 == 0;
+    return ws_pick(a, t) ? 1 : 0;
+}
+
 extern "C" void cf_gemm_set_ws_shape(int32_t bm, int32_t bn) {
     g_gemm_ws_bm = bm > 0 ? bm : 0;
     g_gemm_ws_bn = bn > 0 ? bn : 0;
@@ -1339,9 +1351,10 @@ extern "C" int cf_launch_gemm(const cf_gemm_args_t* a, void* stream) {
     for (int s = 1; s < a->nseg; s++) ptrs |= (uintptr_t)a->out[s];
     int ev = (ptrs % 16 == 0);
     if (a->out_kind == CF_GEMM_OUT_ROWMAJOR) ev = ev && a->n[0] % 8 == 0;
-    else ev = ev && a->d % 8 == 0 && a->S % 8 == 0;
+    else if (a->out_kind == CF_GEMM_OUT_QKV) ev = ev && a->d % 8 == 0 && a->S % 8 == 0;
     t.epi_vec = ev;
     t.group_m = g_gemm_group_m > 0 ? g_gemm_group_m : kGroupM;
+    if (a->out_kind == CF_GEMM_OUT_ROWCAT && !ws_pick(a, t)) return (int)hipErrorInvalidValue;
     // The wave-specialised kernel where it applies (its tile chosen by the cost model).
     if (const WsCandidate* c = ws_pick(a, t)) {
         long long ntot = 0;

@@ -165,8 +165,12 @@ int32_t cf_gemv_fuses_rope(const cf_gemv_args_t* a);
  *                          q (B, H_q, S, d), k (B, H_kv, S, d), vt (B, H_kv, d, S)
  *                          (V transposed so attention reads keys contiguously);
  *                          M = B*S rows, W given as three segments.
+ *   CF_GEMM_OUT_ROWCAT:   the nseg segments side by side in one row-major (M, sum n[s])
+ *                          out[0], each with its own bias, no residual; fp16 on the
+ *                          wave-specialised kernel only (cf_gemm_rowcat_ok says whether a
+ *                          product can take it; cf_launch_gemm rejects it otherwise).
  * ------------------------------------------------------------------------------- */
-enum { CF_GEMM_OUT_ROWMAJOR = 0, CF_GEMM_OUT_QKV = 1 };
+enum { CF_GEMM_OUT_ROWMAJOR = 0, CF_GEMM_OUT_QKV = 1, CF_GEMM_OUT_ROWCAT = 2 };
 
 typedef struct {
     const void* a;           /* (M, K) */
@@ -204,10 +208,15 @@ void cf_gemm_set_ws(int32_t mode);
 /* Tuning/test override of that kernel's tile (BM 256 or 128, BN among its widths; 0, 0 =
  * the cost model's choice).  A product the tile does not fit takes the cost model's. */
 void cf_gemm_set_ws_shape(int32_t bm, int32_t bn);
+int32_t cf_gemm_rowcat_ok(const cf_gemm_args_t* a);
 
 /* ---------------------------------------------------------------------------------
  * Prefill attention (flash style, online softmax): q (B, H_q, S, d), k (B, H_kv, S, d),
  * vt (B, H_kv, d, S) -> o (B, S, H_q, d) == (B*S, H_q*d) row-major.
+ * With qkv_ld > 0 the inputs are instead one row-major (B*S, qkv_ld) matrix at q whose
+ * row holds Q (H_q*d) | K (H_kv*d) | V (H_kv*d) side by side, qkv_ld = (H_q + 2 H_kv) d
+ * (the CF_GEMM_OUT_ROWCAT product); k and vt are unused.  Only the fp16 d = 64 kernel
+ * with S % 8 == 0 reads that layout (cf_flash_rowcat_ok).
  * ------------------------------------------------------------------------------- */
 typedef struct {
     const void* q;
@@ -218,9 +227,11 @@ typedef struct {
     float       scale;
     int32_t     causal;
     int32_t     elem;
+    int32_t     qkv_ld;
 } cf_flash_args_t;
 
 int cf_launch_flash_attn(const cf_flash_args_t* a, void* stream);
+int32_t cf_flash_rowcat_ok(const cf_flash_args_t* a);
 /* Selects the fp16 d = 64 prefill attention kernel (tuning and tests): 0 the register-
  * staged kernel, 1 / 2 the DMA-ring kernel with 32 / 16 queries per wave, 3 (default)
  * the DMA-ring kernel where it applies (S % 8 == 0) with the width chosen by size. */

@@ -27,6 +27,12 @@ typedef struct {
     cf_gemm_args_t  wo;
 } fused_plan_t;
 
+/* 1 (default): where both kernels take it, the QKV product is written row-concatenated,
+ * (B*S, (H + 2 H_kv) d) with Q | K | V side by side, and attention reads that matrix;
+ * 0: always the head-major scatter (q, k, v^T). */
+static int g_rowcat = 1;
+void mha_fused_set_rowcat(int on) { g_rowcat = on != 0; }
+
 static int fused_plan(int elem, const void* inputs[], void* outputs[], const operator_params_t* params,
                       void* st, fused_plan_t* pl) {
     if (!inputs || !inputs[0] || !outputs || !outputs[0] || !params) return -1;
@@ -73,6 +79,24 @@ static int fused_plan(int elem, const void* inputs[], void* outputs[], const ope
     f->scale = p->scale;
     f->causal = p->causal ? 1 : 0;
     f->elem = elem;
+
+    /* The row-concatenated layout: one (B*S, (H + 2 H_kv) d) matrix from the start of the
+     * q area; the q, k and v areas follow one another (each start rounded up to 256 bytes),
+     * so together they hold its B*S*(D + 2 kvd) elements. */
+    if (g_rowcat && elem == CF_ELEM_F16) {
+        cf_gemm_args_t rc = *g;
+        rc.out_kind = CF_GEMM_OUT_ROWCAT;
+        rc.out[0] = data + off_q;
+        rc.out[1] = rc.out[2] = NULL;
+        cf_flash_args_t fr = *f;
+        fr.q = data + off_q;
+        fr.k = fr.vt = NULL;
+        fr.qkv_ld = (int32_t)(D + 2 * kvd);
+        if (cf_gemm_rowcat_ok(&rc) && cf_flash_rowcat_ok(&fr)) {
+            *g = rc;
+            *f = fr;
+        }
+    }
 
     cf_gemm_args_t* o = &pl->wo;
     o->a = data + off_o;

@@ -82,6 +82,11 @@ int register_causal_mask_f32_cuda(void);
  * every CU), otherwise rounded to the kernel's quantum.  Process-wide; for tuning and
  * split-invariance tests. */
 void    mha_decode_set_split_chunk(int64_t chunk);
+/* Prefill (mha_fused_f16_cuda): 1 (default) writes the QKV projection as one row-major
+ * (B*S, (H + 2 H_kv) d) matrix that attention reads directly, where both kernels take it
+ * (fp16, d = 64, S % 8 == 0); 0 always scatters q, k, v^T head-major.  Process-wide; for
+ * tests and measurements. */
+void    mha_fused_set_rowcat(int on);
 /* The (chunk, n_split) the decode core would use for these params on this device. */
 int     mha_decode_plan(const mha_decode_params_t* p, int elem_f16, int64_t* chunk, int64_t* n_split);
 

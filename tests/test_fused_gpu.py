@@ -167,6 +167,31 @@ def test_flash_kernel_variants_agree(gpu, native, causal):
         assert max_abs(outs[0], o) <= 1e-2
 
 
+@pytest.mark.parametrize("B,S,H,H_kv,causal", [(16, 200, 8, 2, False), (16, 200, 8, 2, True), (1, 384, 6, 6, True),
+                                              (2, 512, 12, 12, False)])
+def test_prefill_row_concatenated_qkv(gpu, native, B, S, H, H_kv, causal):
+    """fp16 prefill with the QKV product written as one row-major (B*S, (H + 2 H_kv) d)
+    matrix that attention reads directly (K and V rows as they are, V transposed on its
+    way out of LDS), against the oracle and against the head-major q / k / v^T scatter:
+    GQA, a length that ends inside a 64-key block, causal and not, and both query widths
+    of the attention kernel."""
+    c = FusedCase(B, S, H, H_kv, 64, seed=S + H, f16=True, causal=causal, residual=True, bias_std=0.02)
+    want = c.oracle()
+    outs = []
+    try:
+        for rowcat, mode in ((1, 2), (1, 1), (0, 3)):
+            native.mha_fused_set_rowcat(rowcat)
+            native.cf_flash_set_mode(mode)
+            outs.append(run_fused_gpu(c))
+    finally:
+        native.mha_fused_set_rowcat(1)
+        native.cf_flash_set_mode(3)
+    for o in outs:
+        assert max_abs(want, o) <= TOL16
+    assert max_abs(outs[0], outs[1]) <= 1e-2
+    assert max_abs(outs[0], outs[2]) <= 1e-2
+
+
 WS_SHAPES = [(256, 192), (256, 144), (256, 128), (256, 96), (256, 64), (256, 48), (128, 192), (128, 128),
              (128, 96), (128, 64)]
 
