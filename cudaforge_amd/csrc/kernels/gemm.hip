@@ -993,6 +993,26 @@ void gemm_f16_ws(cf_gemm_args_t a, Tiling t) {
         // [wn + 16j + lr], for tiles whose every column goes to v^T (contiguous along s).
         auto run = [&](auto ct_c) {
             constexpr bool CT = decltype(ct_c)::value;
+            // The epilogue's bias values (CT: four columns of one segment per lane and j;
+            // v^T tiles: column n's value), loaded before the main loop so that their round
+            // trip is not paid after it (config-3 QKV product: ~1 us), except for the
+            // scatter epilogue, whose widest tile would then spill registers.
+            h4_t b4[NJ];
+            _Float16 bc[NJ];
+            auto load_bias = [&]() {
+#pragma unroll
+                for (int j = 0; j < NJ; j++) {
+                    if constexpr (CT) {
+                        int col;
+                        const int sg = ws_seg(a, start, n0 + wn + 16 * j + 4 * lq, col);
+                        const _Float16* bias = epi.bias(sg);
+                        b4[j] = bias ? *(const h4_t*)(bias + col) : h4_t{0, 0, 0, 0};
+                    } else {
+                        bc[j] = epi.bias2 ? epi.bias2[n0 + wn + 16 * j + lr - start[2]] : (_Float16)0;
+                    }
+                }
+            };
+            if constexpr (EPI != WS_EPI_QKV) load_bias();
             f4_t acc[4][NJ];
 #pragma unroll
             for (int i = 0; i < 4; i++)
@@ -1019,19 +1039,11 @@ void gemm_f16_ws(cf_gemm_args_t a, Tiling t) {
                 }
                 ring_barrier();
             });
+            if constexpr (EPI == WS_EPI_QKV) load_bias();
             if constexpr (CT) {
                 // Stage [BM][BN]: bias added in fp32; fp16 (one rounding) without a residual,
-                // fp32 with one.  A lane's four columns lie in one segment (n[s] % 8 == 0);
-                // every bias load is issued before the first is used.
+                // fp32 with one.  A lane's four columns lie in one segment (n[s] % 8 == 0).
                 constexpr bool f32s = EPI == WS_EPI_RESIDUAL;
-                h4_t b4[NJ];
-#pragma unroll
-                for (int j = 0; j < NJ; j++) {
-                    int col;
-                    const int sg = ws_seg(a, start, n0 + wn + 16 * j + 4 * lq, col);
-                    const _Float16* bias = epi.bias(sg);
-                    b4[j] = bias ? *(const h4_t*)(bias + col) : h4_t{0, 0, 0, 0};
-                }
 #pragma unroll
                 for (int j = 0; j < NJ; j++)
 #pragma unroll
@@ -1043,10 +1055,7 @@ void gemm_f16_ws(cf_gemm_args_t a, Tiling t) {
                         else *(uint2*)(smem + r * (BN + 8) + c) = pack4(v0, v1, v2, v3);
                     }
             } else {
-                // A v^T tile: stage [BN][BM] (column-major), bias of column n added in fp32.
-                _Float16 bc[NJ];
-#pragma unroll
-                for (int j = 0; j < NJ; j++) bc[j] = epi.bias2 ? epi.bias2[n0 + wn + 16 * j + lr - start[2]] : (_Float16)0;
+                // A v^T tile: stage [BM][BN] (column-major), bias of column n added in fp32.
 #pragma unroll
                 for (int j = 0; j < NJ; j++)
 #pragma unroll
