@@ -300,10 +300,11 @@ def bench_fused(cf, stream, steps, warmup, B, S, H, d, causal, seed, f16=True):
     p = cf.MhaFusedParams(B, S, D, H, H, d, float(1 / np.sqrt(d)), False, causal)
     name = "mha_fused_f16_cuda" if f16 else "mha_fused_f32_cuda"
     ms = time_op(cf, name, ins, [Y], p, stream, steps, warmup)
+    st = sorted(time_op(cf, name, ins, [Y], p, stream, steps, 1) for _ in range(STAT_REPS))
     kms = fused_kernel_times(cf, ins, [Y], p, stream, f16, steps, warmup)
     pairs = B * H * (S * (S + 1) // 2 if causal else S * S)
     kfl = [2 * B * S * D * 3 * D, 4 * pairs * d, 2 * B * S * D * D]
-    return ms, sum(kfl), kms, kfl
+    return ms, sum(kfl), kms, kfl, (st[len(st) // 2], st[0])
 
 
 def cpu_baseline_decode(budget_s: float):
@@ -468,8 +469,8 @@ def bench_prefill(cf, stream, steps, warmup, fp32=True) -> dict:
         legs["prefill_config3_bert_base_f32"] = (8, 512, 12, 64, False, 300, False)
     for key, (B, S, H, d, causal, seed, f16) in legs.items():
         log(key)
-        n = max(steps // 4, 10) if f16 else max(steps // 20, 5)
-        ms_p, fl, kms, kfl = bench_fused(cf, stream, n, max(warmup // 2, 3), B, S, H, d, causal, seed, f16)
+        n = max(steps, 10) if f16 else max(steps // 20, 5)
+        ms_p, fl, kms, kfl, (med, mn) = bench_fused(cf, stream, n, max(warmup // 2, 3), B, S, H, d, causal, seed, f16)
         peak = FP16_PEAK_TFLOPS if f16 else FP32_PEAK_TFLOPS
         tf = fl / (ms_p * 1e-3) / 1e12
         kernels = {}
@@ -477,12 +478,13 @@ def bench_prefill(cf, stream, steps, warmup, fp32=True) -> dict:
             ktf = kf / (kt * 1e-3) / 1e12
             kernels[kname] = {"us": round(kt * 1e3, 2), "alg_flop": kf, "TFLOP_s": round(ktf, 1),
                               "frac": round(ktf / peak, 4)}
-        out[key] = {"us_per_step": round(ms_p * 1e3, 2), "TFLOP_s": round(tf, 1), "alg_flop": fl,
+        out[key] = {"us_per_step": round(ms_p * 1e3, 2), "us_per_step_median": round(med * 1e3, 2),
+                    "us_per_step_min": round(mn * 1e3, 2), "TFLOP_s": round(tf, 1), "alg_flop": fl,
                     "mfma_frac": round(tf / peak, 4),
                     "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": peak, "unit": "TFLOP/s",
                                  "frac": round(tf / peak, 4), "dtype": "f16" if f16 else "f32",
                                  "kernel_sum_us": round(sum(kms) * 1e3, 2), "kernels": kernels}}
-        log(f"  {ms_p * 1e3:.1f} us/step {tf:.1f} TFLOP/s; kernels " +
+        log(f"  {ms_p * 1e3:.1f} us/step (median {med * 1e3:.1f}, min {mn * 1e3:.1f}) {tf:.1f} TFLOP/s; kernels " +
             ", ".join(f"{k} {v['us']} us ({v['frac']:.3f})" for k, v in kernels.items()))
     return out
 
