@@ -726,6 +726,31 @@ def test_split_chunks_longer_than_4096(gpu, native):
     assert max_abs(want, got) <= TOL16
 
 
+@pytest.mark.parametrize("f16,d", [(True, 128), (True, 64), (False, 128)])
+def test_merge_many_splits(gpu, native, f16, d):
+    """Uniform lengths cut into 32-position splits, 157 and 94 splits per row (the row
+    merge), against the oracle, and the row merge forced the same way."""
+    B, H_kv, G = 2, 2, 4
+    H = H_kv * G
+    r = O.round_f16 if f16 else (lambda a: a)
+    for T in (5000, 3000):
+        Q, K, V = (r(O.normal(s, 150 + i)) for i, s in enumerate([(B, H, d), (B, T, H_kv, d), (B, T, H_kv, d)]))
+        want = O.decode_attn(Q, K, V, np.full(B, T, np.int32), float(1 / np.sqrt(d)), H_kv)
+        outs = []
+        try:
+            native.mha_decode_set_split_chunk(32)
+            for rows in (0, 1):
+                native.cf_decode_attn_set_merge_rows(rows)
+                outs.append(run_decode_attn_gpu(Q, K, V, T - 1, H_kv, f16))
+        finally:
+            native.cf_decode_attn_set_merge_rows(0)
+            native.mha_decode_set_split_chunk(0)
+        tol = TOL16 if f16 else TOL32
+        for got in outs:
+            assert max_abs(want, got) <= tol
+        assert max_abs(outs[0], outs[1]) <= tol
+
+
 @pytest.mark.parametrize("f16,d,G", [(True, 128, 4), (True, 64, 2), (True, 64, 8), (True, 128, 1),
                                      (False, 64, 1), (False, 128, 8)])
 def test_merge_kernels_agree(gpu, native, f16, d, G):
