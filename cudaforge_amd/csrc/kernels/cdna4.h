@@ -17,6 +17,9 @@ typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 lds_h4_t;
 #define CF_LDS __attribute__((address_space(3)))
+// Global memory, for pointers the compiler cannot trace back to a kernel argument (it
+// would otherwise emit flat loads, which also count against lgkmcnt).
+#define CF_GLOBAL __attribute__((address_space(1)))
 
 // s_waitcnt vmcnt(N), expcnt/lgkmcnt left at their maxima (gfx9 encoding).  The empty
 // asm after it keeps the compiler from hoisting LDS reads above the wait.

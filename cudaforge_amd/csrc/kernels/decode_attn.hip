@@ -1024,19 +1024,20 @@ void merge_wave(cf_decode_attn_args_t a, int Gx, int units_per_b, int rows) {
     const int nsplit = sr.n;
     if (nsplit <= 1) return;                       // finished by the split kernel
     // Every load first (one round trip): lane s < nsplit holds split s's (m, l), and each
-    // lane the DPL accumulator values of every split for its dims.
-    float mv = -INFINITY, lv = 0.0f;
-    if (lane < nsplit) {
-        mv = sr.first[(size_t)lane * sr.step + g];
-        lv = sr.first[(size_t)lane * sr.step + Gx + g];
-    }
+    // lane the DPL accumulator values of every split for its dims.  The loads are
+    // unconditional, split indices clamped to the last split (weight 0 below), so that
+    // no branch splits them into several waits.
+    const int last = nsplit - 1;
+    const CF_GLOBAL float* first = (const CF_GLOBAL float*)sr.first;
+    const CF_GLOBAL float* ph = first + (size_t)min(lane, last) * sr.step + g;
+    const float mr = ph[0], lr = ph[Gx];
+    const float mv = lane < nsplit ? mr : -INFINITY, lv = lane < nsplit ? lr : 0.0f;
     float av[MAXS][DPL];
 #pragma unroll
     for (int j = 0; j < MAXS; j++) {
-        const bool ok = j < nsplit;
-        const float* ps = sr.first + (size_t)(ok ? j : 0) * sr.step + hdr + g * D + DPL * lane;
+        const CF_GLOBAL float* ps = first + (size_t)min(j, last) * sr.step + hdr + g * D + DPL * lane;
 #pragma unroll
-        for (int e = 0; e < DPL; e++) av[j][e] = ok ? ps[e] : 0.0f;
+        for (int e = 0; e < DPL; e++) av[j][e] = ps[e];
     }
     float M = mv;
 #pragma unroll

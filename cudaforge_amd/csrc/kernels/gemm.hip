@@ -794,21 +794,21 @@ constexpr unsigned ws_lds_bytes() { return (unsigned)S * WsShape<BM, BN>::ST * 2
 // reading them from the argument block after the main loop cost ~1 us per group of fields
 // (config-3 QKV product, 22.8 -> 19 us without those late reads).
 struct WsEpi {
-    _Float16* out0;
-    _Float16* out1;
-    _Float16* out2;
-    const _Float16* bias0;
-    const _Float16* bias1;
-    const _Float16* bias2;
-    const _Float16* res;
+    CF_GLOBAL _Float16* out0;
+    CF_GLOBAL _Float16* out1;
+    CF_GLOBAL _Float16* out2;
+    const CF_GLOBAL _Float16* bias0;
+    const CF_GLOBAL _Float16* bias1;
+    const CF_GLOBAL _Float16* bias2;
+    const CF_GLOBAL _Float16* res;
     int S, Hq, Hkv, d, n0w;
     // Per-segment pointers as the first one plus a selected distance: a select among the
     // pointers themselves is turned into an indexed load of the struct, which then lives
     // in scratch memory.
-    __device__ _Float16* out(int s) const {
+    __device__ CF_GLOBAL _Float16* out(int s) const {
         return out0 + (s == 1 ? out1 - out0 : (ptrdiff_t)0) + (s == 2 ? out2 - out0 : (ptrdiff_t)0);
     }
-    __device__ const _Float16* bias(int s) const {
+    __device__ const CF_GLOBAL _Float16* bias(int s) const {
         return bias0 + (s == 1 ? bias1 - bias0 : (ptrdiff_t)0) + (s == 2 ? bias2 - bias0 : (ptrdiff_t)0);
     }
 };
@@ -817,13 +817,13 @@ struct WsEpi {
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ WsEpi ws_epi(const cf_gemm_args_t& a) {
     WsEpi e;
-    e.out0 = (_Float16*)a.out[0];
-    e.out1 = (_Float16*)a.out[1];
-    e.out2 = (_Float16*)a.out[2];
-    e.bias0 = (const _Float16*)a.bias[0];
-    e.bias1 = (const _Float16*)a.bias[1];
-    e.bias2 = (const _Float16*)a.bias[2];
-    e.res = (const _Float16*)a.residual;
+    e.out0 = (CF_GLOBAL _Float16*)a.out[0];
+    e.out1 = (CF_GLOBAL _Float16*)a.out[1];
+    e.out2 = (CF_GLOBAL _Float16*)a.out[2];
+    e.bias0 = (const CF_GLOBAL _Float16*)a.bias[0];
+    e.bias1 = (const CF_GLOBAL _Float16*)a.bias[1];
+    e.bias2 = (const CF_GLOBAL _Float16*)a.bias[2];
+    e.res = (const CF_GLOBAL _Float16*)a.residual;
     e.S = a.S;
     e.Hq = a.H_q;
     e.Hkv = a.H_kv;
@@ -1005,8 +1005,8 @@ void gemm_f16_ws(cf_gemm_args_t a, Tiling t) {
                     if constexpr (CT) {
                         int col;
                         const int sg = ws_seg(a, start, n0 + wn + 16 * j + 4 * lq, col);
-                        const _Float16* bias = epi.bias(sg);
-                        b4[j] = bias ? *(const h4_t*)(bias + col) : h4_t{0, 0, 0, 0};
+                        const CF_GLOBAL _Float16* bias = epi.bias(sg);
+                        b4[j] = bias ? *(const CF_GLOBAL h4_t*)(bias + col) : h4_t{0, 0, 0, 0};
                     } else {
                         bc[j] = epi.bias2 ? epi.bias2[n0 + wn + 16 * j + lr - start[2]] : (_Float16)0;
                     }
@@ -1094,7 +1094,7 @@ __device__ __forceinline__ void ws_store(const WsEpi& e, const int (&start)[4], 
             const int id = tid + 512 * it;
             if (id < NCH) {
                 const int r = id / CPR, c8 = id - r * CPR;
-                *(h8_t*)(e.out0 + (size_t)(m0 + r) * e.n0w + n0 + 8 * c8) = *(const h8_t*)(smem + r * (BN + 8) + 8 * c8);
+                *(CF_GLOBAL h8_t*)(e.out0 + (size_t)(m0 + r) * e.n0w + n0 + 8 * c8) = *(const h8_t*)(smem + r * (BN + 8) + 8 * c8);
             }
         }
         return;
@@ -1112,11 +1112,11 @@ __device__ __forceinline__ void ws_store(const WsEpi& e, const int (&start)[4], 
         }
 #pragma unroll
         for (int it = 0; it < ITV; it++)
-            if (tid + 512 * it < NV) *(h8_t*)(e.out2 + off[it]) = v[it];
+            if (tid + 512 * it < NV) *(CF_GLOBAL h8_t*)(e.out2 + off[it]) = v[it];
         return;
     }
     if constexpr (EPI == WS_EPI_RESIDUAL) {
-        const _Float16* __restrict__ res = e.res;
+        const CF_GLOBAL _Float16* __restrict__ res = e.res;
         f4_t lo[IT], hi[IT];
         h8_t rv[IT];
         size_t off[IT];
@@ -1127,7 +1127,7 @@ __device__ __forceinline__ void ws_store(const WsEpi& e, const int (&start)[4], 
             off[it] = (size_t)(m0 + r) * e.n0w + n0 + 8 * c8;
             lo[it] = *(const f4_t*)sp;
             hi[it] = *(const f4_t*)(sp + 4);
-            rv[it] = *(const h8_t*)(res + off[it]);
+            rv[it] = *(const CF_GLOBAL h8_t*)(res + off[it]);
         }
 #pragma unroll
         for (int it = 0; it < IT; it++) {
@@ -1136,7 +1136,7 @@ __device__ __forceinline__ void ws_store(const WsEpi& e, const int (&start)[4], 
             h8_t v;
 #pragma unroll
             for (int e = 0; e < 8; e++) v[e] = (_Float16)(f[e] + (float)rv[it][e]);
-            *(h8_t*)(e.out0 + off[it]) = v;
+            *(CF_GLOBAL h8_t*)(e.out0 + off[it]) = v;
         }
         return;
     }
@@ -1155,7 +1155,7 @@ __device__ __forceinline__ void ws_store(const WsEpi& e, const int (&start)[4], 
 #pragma unroll
         for (int it = 0; it < IT; it++) {
             if (tid + 512 * it >= NCH || (qkv && sg[it] == 2)) continue;   // v^T: below
-            *(h8_t*)(e.out(sg[it]) + off[it]) = v[it];
+            *(CF_GLOBAL h8_t*)(e.out(sg[it]) + off[it]) = v[it];
         }
     }
     if (qkv && n0 + BN > start[2]) {
