@@ -947,17 +947,20 @@ void merge_rows(cf_decode_attn_args_t a, int Gx, int units_per_b, int ds) {
     f4_t num = {0.f, 0.f, 0.f, 0.f};
     if (sg < SG) {
         constexpr int NB = 8;
+        // Unconditional loads (split index clamped to the last split, weight 0 below)
+        // through a global pointer: one batch of loads per round, no branch between them.
+        const CF_GLOBAL float* first = (const CF_GLOBAL float*)sr.first;
         for (int s0 = sg; s0 < nsplit; s0 += SG * NB) {
             float mv[NB], lv[NB];
             f4_t av[NB];
 #pragma unroll
             for (int j = 0; j < NB; j++) {
                 const int sp = s0 + j * SG;
-                const bool ok = sp < nsplit;
-                const float* ps = sr.first + (size_t)(ok ? sp : 0) * sr.step;
-                mv[j] = ok ? ps[g] : -INFINITY;
-                lv[j] = ok ? ps[Gx + g] : 0.0f;
-                av[j] = ok ? *(const f4_t*)(ps + hdr + g * D + 4 * col) : f4_t{0.f, 0.f, 0.f, 0.f};
+                const CF_GLOBAL float* ps = first + (size_t)min(sp, nsplit - 1) * sr.step;
+                const float mr = ps[g], lr = ps[Gx + g];
+                mv[j] = sp < nsplit ? mr : -INFINITY;
+                lv[j] = sp < nsplit ? lr : 0.0f;
+                av[j] = *(const CF_GLOBAL f4_t*)(ps + hdr + g * D + 4 * col);
             }
             float mc = mv[0];
 #pragma unroll
