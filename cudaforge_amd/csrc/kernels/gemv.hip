@@ -397,62 +397,77 @@ int dma_bn(const cf_gemv_args_t* a) {
     return bn;
 }
 
-// Partial reduce (tile widths are multiples of 64, so 4 adjacent columns share a tile):
-// a thread owns 4 adjacent columns of one row and issues all of its K-chunk loads
-// (16-byte) before summing, so the whole reduction is one round trip to memory.
-// One-wave workgroups spread the partials over every CU (16 rows x 6144 columns is
-// 384 of them).
+// Partial reduce.  A wave owns rows of one column tile (t.bn = 64, 128 or 256 columns):
+// bn / 4 lanes per row, each with 4 adjacent columns, so the tile, its segment and the
+// segment's pointers are uniform per wave (scalar loads of the argument block).  Every
+// load that does not need the partials is issued around them: the row's position and
+// the bias before, the RoPE angles (which need the position) right after, so the whole
+// reduction is about one round trip to memory.  A thread issues all of its K-chunk
+// loads (16-byte) before summing: KS >= k_split loads, unconditional, the chunk index
+// clamped to the last chunk and the surplus left out of the sum (a load under a branch
+// was waited for right there).  One-wave workgroups spread the partials over the CUs
+// (16 rows x 6144 columns is 384 of them).
 constexpr int kReduceThreads = 64;
 constexpr int kMaxKSplit = 32;    // K chunks the reduce keeps in flight
-template <typename T>
+template <typename T, int KS>
 __global__ __launch_bounds__(kReduceThreads)
 void gemv_reduce4(cf_gemv_args_t a, Tiles t) {
-    constexpr int MAXKS = kMaxKSplit;
-    const int ncols = t.start[a.nseg] * t.bn;
+    static_assert(KS <= kMaxKSplit, "K chunks");
+    const int ntiles = t.start[a.nseg], bn = t.bn;
+    const int lpr = bn / 4, rpw = kReduceThreads / lpr;   // lanes per row, rows per wave
+    const int ncols = ntiles * bn;
     const size_t plane = (size_t)a.M * ncols;
-    const size_t total = (size_t)a.M * (ncols / 4);
     advance_lengths(a);
-    const size_t idx = (size_t)blockIdx.x * kReduceThreads + threadIdx.x;
-    if (idx >= total) return;
-    const int m = (int)(idx / (ncols / 4));
-    const int col = (int)(idx - (size_t)m * (ncols / 4)) * 4;
-    const float* p = a.partials + (size_t)m * ncols + col;
-    f4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-    for (int kb = 0; kb < a.k_split; kb += MAXKS) {   // one pass: k_split <= MAXKS
-        const int nk = min(MAXKS, a.k_split - kb);
-        f4_t v[MAXKS];
-#pragma unroll
-        for (int k = 0; k < MAXKS; k++)
-            if (k < nk) v[k] = *(const f4_t*)(p + (size_t)(kb + k) * plane);
-#pragma unroll
-        for (int k = 0; k < MAXKS; k += 2) {
-            if (k < nk) s0 += v[k];
-            if (k + 1 < nk) s1 += v[k + 1];
-        }
-    }
-    s0 += s1;
-    const int tile = col / t.bn;
+    const int tile = (int)(blockIdx.x % (unsigned)ntiles), rb = (int)(blockIdx.x / (unsigned)ntiles);
+    const int m = rb * rpw + (int)threadIdx.x / lpr;
+    if (m >= a.M) return;
+    const int lc = 4 * ((int)threadIdx.x % lpr);
     const int seg = seg_of(a, t, tile);
     const cf_gemv_seg_t& sg = a.seg[seg];
-    const int n = (tile - t.start[seg]) * t.bn + (col - tile * t.bn);
+    const int n = (tile - t.start[seg]) * bn + lc;        // segment-local column
+    // Optional operands are read through a stand-in (the partials, always valid) and the
+    // value selected afterwards: a load under a branch makes the compiler wait for it at
+    // the branch's end, one round trip each.
+    const float* const dummy = a.partials;
+    const int32_t* const pl = a.pos_lens ? a.pos_lens : (const int32_t*)dummy;
+    const int32_t pl_m = pl[m];
     const T* __restrict__ bias = (const T*)sg.bias;
-    float v[4];
+    const T* const bp = bias ? bias : (const T*)dummy;
+    float bv[4];
 #pragma unroll
-    for (int e = 0; e < 4; e++) v[e] = bias && n + e < sg.n ? s0[e] + to_f(bias[n + e]) : s0[e];
-    if (a.rope_table && ((a.rope_segs >> seg) & 1)) {
-        // n is a multiple of 4 and rope_d is even, so (n, n+1) and (n+2, n+3) are pairs.
-        const int64_t pos = a.pos_lens ? (int64_t)a.pos_lens[m] : a.pos_uniform;
-        if (pos >= 0 && pos < a.rope_rows) {
-            const int half = a.rope_d >> 1;
-            const float2* tb = (const float2*)a.rope_table + pos * half;
+    for (int e = 0; e < 4; e++) bv[e] = to_f(bp[min(n + e, (int)sg.n - 1)]);
+    const float* p = a.partials + (size_t)m * ncols + (size_t)tile * bn + lc;
+    const int nk = min(KS, a.k_split);                    // the launcher picks KS >= k_split
+    f4_t v[KS];
 #pragma unroll
-            for (int e = 0; e < 4; e += 2)
-                if (n + e + 1 < sg.n) rotate_pair(v[e], v[e + 1], tb[((n + e) % a.rope_d) >> 1]);
-        }
+    for (int k = 0; k < KS; k++) v[k] = *(const f4_t*)(p + (size_t)min(k, nk - 1) * plane);
+    const int64_t pos = a.pos_lens ? (int64_t)pl_m : a.pos_uniform;
+    const bool rotate = a.rope_table && ((a.rope_segs >> seg) & 1) && pos >= 0 && pos < a.rope_rows;
+    // n is a multiple of 4 and rope_d is even, so (n, n+1) and (n+2, n+3) are pairs.
+    const int rd = a.rope_table ? a.rope_d : 2;
+    const float2* tb = a.rope_table ? (const float2*)a.rope_table + (rotate ? pos : 0) * (rd >> 1)
+                                    : (const float2*)dummy;
+    const float2 c0 = tb[(n % rd) >> 1], c1 = tb[((n + 2) % rd) >> 1];
+    const float2 cs[2] = {rotate ? c0 : float2{1.f, 0.f}, rotate ? c1 : float2{1.f, 0.f}};
+    f4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < KS; k += 2) {
+        if (k < nk) s0 += v[k];
+        if (k + 1 < nk) s1 += v[k + 1];
     }
+    s0 += s1;
+    float o[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) o[e] = n + e < sg.n && bias ? s0[e] + bv[e] : s0[e];
+    if (rotate)
+#pragma unroll
+        for (int e = 0; e < 4; e += 2)
+            if (n + e + 1 < sg.n) rotate_pair(o[e], o[e + 1], cs[e >> 1]);
+    if (!pos_ok(a, sg, pos)) return;
+    T* out = (T*)sg.out + (size_t)m * sg.ld_m + (size_t)(sg.ld_pos ? pos : 0) * sg.ld_pos + n;
 #pragma unroll
     for (int e = 0; e < 4; e++)
-        if (n + e < sg.n) store_val<T>(a, sg, m, n + e, v[e]);
+        if (n + e < sg.n) out[e] = from_f<T>(o[e]);
 }
 
 // ---- small projections (a few batch rows, weights of a few MB, e.g. GPT-2-small
@@ -716,11 +731,19 @@ extern "C" int cf_launch_gemv(const cf_gemv_args_t* a, void* stream) {
         hipLaunchKernelGGL(gemv_kernel<float>, grid, dim3(kThreads), 0, s, args, t);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || t.ks == 1) return (int)e;
-    const size_t total4 = (size_t)a->M * t.start[a->nseg] * t.bn / 4;
-    const dim3 rgrid((unsigned)((total4 + kReduceThreads - 1) / kReduceThreads));
-    if (a->elem == CF_ELEM_F16)
-        hipLaunchKernelGGL(gemv_reduce4<_Float16>, rgrid, dim3(kReduceThreads), 0, s, args, t);
-    else
-        hipLaunchKernelGGL(gemv_reduce4<float>, rgrid, dim3(kReduceThreads), 0, s, args, t);
+    // A wave per (column tile, kReduceThreads / (bn / 4) rows).
+    const int rpw = kReduceThreads / (t.bn / 4);
+    const dim3 rgrid((unsigned)(t.start[a->nseg] * ((a->M + rpw - 1) / rpw)));
+    auto reduce = [&](auto ks_c) {
+        constexpr int KS = decltype(ks_c)::value;
+        if (a->elem == CF_ELEM_F16)
+            hipLaunchKernelGGL((gemv_reduce4<_Float16, KS>), rgrid, dim3(kReduceThreads), 0, s, args, t);
+        else
+            hipLaunchKernelGGL((gemv_reduce4<float, KS>), rgrid, dim3(kReduceThreads), 0, s, args, t);
+    };
+    if (t.ks <= 4) reduce(std::integral_constant<int, 4>{});
+    else if (t.ks <= 8) reduce(std::integral_constant<int, 8>{});
+    else if (t.ks <= 16) reduce(std::integral_constant<int, 16>{});
+    else reduce(std::integral_constant<int, kMaxKSplit>{});
     return (int)hipGetLastError();
 }

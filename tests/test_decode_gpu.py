@@ -666,6 +666,22 @@ def test_projection_tile_widths(gpu, native, bn):
         assert max_abs(w, g) <= TOL16
 
 
+@pytest.mark.parametrize("ks", [2, 3, 8, 13, 32])
+def test_projection_k_splits(gpu, native, ks):
+    """The fp16 projections with K split into 2..32 chunks, which the partial reduce sums
+    with each of its chunk bounds (4, 8, 16, 32; the surplus loads clamped to the last
+    chunk), give the decode result within tolerance of the oracle."""
+    c = DecodeCase(5, 8, 2, 128, 300, cache_len=299, seed=70 + ks, f16=True)
+    want = c.oracle()
+    try:
+        native.cf_gemv_set_dma_ksplit(ks)
+        got = run_decode_gpu(c)
+    finally:
+        native.cf_gemv_set_dma_ksplit(0)
+    for w, g in zip(want, got):
+        assert max_abs(w, g) <= TOL16
+
+
 @pytest.mark.parametrize("stages", [2, 3, 4])
 def test_split_ring_depths(gpu, native, stages):
     """The fp16 split kernel at each LDS ring depth (2/3/4 stages), with ragged lengths that
