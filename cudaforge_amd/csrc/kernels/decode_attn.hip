@@ -672,19 +672,25 @@ void split_f32(cf_decode_attn_args_t a) {
     for (int g = 0; g < G; g++) qv[g] = *(const f4_t*)((const float*)a.q + ((size_t)b * a.H_q + h0 + g) * D + c * 4);
     const float qk_scale = a.scale * kLog2e;
 
+    // Rows are loaded unconditionally, clamped to the split's last row (a load under a
+    // branch is waited for at the branch's end), and the first block's V rows go out with
+    // its K rows, so a split of one block (config 1: 64 positions) reads K and V in one
+    // round trip.
+    auto load_rows = [&](const float* __restrict__ src, int base, f4_t (&dst)[kF32Unroll]) {
+#pragma unroll
+        for (int u = 0; u < kF32Unroll; u++)
+            dst[u] = *(const f4_t*)(src + (size_t)min(base + u * ROWS + wave * RPW + r, t1 - 1) * row_stride);
+    };
+    f4_t kv[kF32Unroll], v0[kF32Unroll];
+    load_rows(kb, t0, kv);
+    load_rows(vb, t0, v0);
     float mloc[G];
 #pragma unroll
     for (int g = 0; g < G; g++) mloc[g] = -INFINITY;
-    for (int base = t0; base < t1; base += PIT) {
-        f4_t kv[kF32Unroll];
-        int pos[kF32Unroll];
+    auto score_block = [&](int base) {
 #pragma unroll
         for (int u = 0; u < kF32Unroll; u++) {
-            pos[u] = base + u * ROWS + wave * RPW + r;
-            kv[u] = pos[u] < t1 ? *(const f4_t*)(kb + (size_t)pos[u] * row_stride) : f4_t{};
-        }
-#pragma unroll
-        for (int u = 0; u < kF32Unroll; u++)
+            const int pos = base + u * ROWS + wave * RPW + r;
 #pragma unroll
             for (int g = 0; g < G; g++) {
                 float s = qv[g][0] * kv[u][0];
@@ -694,11 +700,17 @@ void split_f32(cf_decode_attn_args_t a) {
 #pragma unroll
                 for (int m = 1; m < LPR; m <<= 1) s += __shfl_xor(s, m);
                 s *= qk_scale;
-                if (pos[u] < t1) {
-                    if (c == g) sc[(pos[u] - t0) * G + g] = s;
+                if (pos < t1) {
+                    if (c == g) sc[(pos - t0) * G + g] = s;
                     mloc[g] = fmaxf(mloc[g], s);
                 }
             }
+        }
+    };
+    score_block(t0);
+    for (int base = t0 + PIT; base < t1; base += PIT) {
+        load_rows(kb, base, kv);
+        score_block(base);
     }
 #pragma unroll
     for (int g = 0; g < G; g++) {
@@ -745,24 +757,25 @@ void split_f32(cf_decode_attn_args_t a) {
     for (int g = 0; g < G; g++)
 #pragma unroll
         for (int e = 0; e < 4; e++) acc[g][e] = 0.0f;
-    for (int base = t0; base < t1; base += PIT) {
-        f4_t vv[kF32Unroll];
-        int pos[kF32Unroll];
+    auto acc_block = [&](int base, const f4_t (&vv)[kF32Unroll]) {
 #pragma unroll
         for (int u = 0; u < kF32Unroll; u++) {
-            pos[u] = base + u * ROWS + wave * RPW + r;
-            vv[u] = pos[u] < t1 ? *(const f4_t*)(vb + (size_t)pos[u] * row_stride) : f4_t{};
-        }
-#pragma unroll
-        for (int u = 0; u < kF32Unroll; u++)
-            if (pos[u] < t1) {
+            const int pos = base + u * ROWS + wave * RPW + r;
+            if (pos < t1) {
 #pragma unroll
                 for (int g = 0; g < G; g++) {
-                    const float p = sc[(pos[u] - t0) * G + g];
+                    const float p = sc[(pos - t0) * G + g];
 #pragma unroll
                     for (int e = 0; e < 4; e++) acc[g][e] = __builtin_fmaf(p, vv[u][e], acc[g][e]);
                 }
             }
+        }
+    };
+    acc_block(t0, v0);
+    for (int base = t0 + PIT; base < t1; base += PIT) {
+        f4_t vv[kF32Unroll];
+        load_rows(vb, base, vv);
+        acc_block(base, vv);
     }
 #pragma unroll
     for (int g = 0; g < G; g++)

@@ -504,6 +504,17 @@ void gemv_small(cf_gemv_args_t a, Tiles t) {
     const int M = a.M, K = a.K;
     const int kq = (K + kWaves * RPI - 1) / (kWaves * RPI) * RPI;   // rows per wave
     const int k_lo = wave * kq, k_hi = min(K, k_lo + kq);
+    // The storing threads' position, bias and RoPE angles are loaded with the first W
+    // batch and X, not after the sums, where they would cost another round trip.  Each
+    // load is unconditional (an optional operand is read through a stand-in, W, and the
+    // value selected afterwards; non-storing threads read row M - 1): a load under a
+    // branch is waited for at the branch's end.  The position goes first, so the RoPE
+    // angles that need it wait only for it.
+    const int store_m = tid / (kSmallCols / 4), n = nb + 4 * (tid % (kSmallCols / 4));
+    const bool storer = tid < M * (kSmallCols / 4);
+    const T* const stand_in = (const T*)sg.w;
+    const int32_t* const pl = a.pos_lens ? a.pos_lens : (const int32_t*)stand_in;
+    const int32_t pl_m = pl[min(store_m, M - 1)];
     V w[NB];
     auto load_batch = [&](int r0) {
 #pragma unroll
@@ -513,41 +524,30 @@ void gemv_small(cf_gemv_args_t a, Tiles t) {
         }
     };
     if (k_lo < k_hi) load_batch(k_lo);
-    // The storing threads' bias, position and RoPE angles are loaded now as well, not
-    // after the sums, where they would cost another round trip.
-    const int store_m = tid / (kSmallCols / 4), n = nb + 4 * (tid % (kSmallCols / 4));
-    const bool storer = tid < M * (kSmallCols / 4);
     const T* __restrict__ bias = (const T*)sg.bias;
-    float bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    int64_t pos = a.pos_uniform;
-    float2 rot[2] = {{1.0f, 0.0f}, {1.0f, 0.0f}};
-    bool rotate = false;
-    if (storer) {
-        if (bias)
+    const T* const bp = bias ? bias : stand_in;
+    float bv[4];
 #pragma unroll
-            for (int e = 0; e < 4; e++) bv[e] = to_f(bias[n + e]);
-        if (a.pos_lens) pos = a.pos_lens[store_m];
-        if (a.rope_table && ((a.rope_segs >> seg) & 1) && pos >= 0 && pos < a.rope_rows) {
-            // n is a multiple of 4 and rope_d is even, so (n, n+1) and (n+2, n+3) are pairs.
-            const float2* tb = (const float2*)a.rope_table + pos * (a.rope_d >> 1);
-            rot[0] = tb[(n % a.rope_d) >> 1];
-            rot[1] = tb[((n + 2) % a.rope_d) >> 1];
-            rotate = true;
-        }
-    }
-    {
-        // Every X load is issued before the first LDS store, so they share the W loads'
-        // round trip.
-        constexpr int XPT = kSmallMaxX / kThreads;
-        const T* __restrict__ xg = (const T*)a.x;
-        const int nx = M * K;
-        T xv[XPT];
+    for (int e = 0; e < 4; e++) bv[e] = to_f(bp[n + e]);   // n + 3 < N: segments are whole tiles
+    // Every X load is issued before the first LDS store, so they share the W loads'
+    // round trip.
+    constexpr int XPT = kSmallMaxX / kThreads;
+    const T* __restrict__ xg = (const T*)a.x;
+    const int nx = M * K;
+    T xv[XPT];
 #pragma unroll
-        for (int j = 0; j < XPT; j++) xv[j] = xg[min(tid + j * kThreads, nx - 1)];
+    for (int j = 0; j < XPT; j++) xv[j] = xg[min(tid + j * kThreads, nx - 1)];
+    const int64_t pos = a.pos_lens ? (int64_t)pl_m : a.pos_uniform;
+    const bool rotate = a.rope_table && ((a.rope_segs >> seg) & 1) && pos >= 0 && pos < a.rope_rows;
+    // n is a multiple of 4 and rope_d is even, so (n, n+1) and (n+2, n+3) are pairs.
+    const int rd = a.rope_table ? a.rope_d : 2;
+    const float2* tb = a.rope_table ? (const float2*)a.rope_table + (rotate ? pos : 0) * (rd >> 1)
+                                    : (const float2*)stand_in;
+    const float2 c0 = tb[(n % rd) >> 1], c1 = tb[((n + 2) % rd) >> 1];
+    const float2 rot[2] = {rotate ? c0 : float2{1.f, 0.f}, rotate ? c1 : float2{1.f, 0.f}};
 #pragma unroll
-        for (int j = 0; j < XPT; j++)
-            if (tid + j * kThreads < nx) xs[tid + j * kThreads] = to_f(xv[j]);
-    }
+    for (int j = 0; j < XPT; j++)
+        if (tid + j * kThreads < nx) xs[tid + j * kThreads] = to_f(xv[j]);
     __syncthreads();
     float acc[kSmallMaxM][VEC];
 #pragma unroll
