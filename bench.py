@@ -298,7 +298,7 @@ def bench_fused(cf, stream, steps, warmup, B, S, H, d, causal, seed, f16=True):
            mk((D, D), 4, 0.02), zero(D), mk((D, D), 5, 0.02), zero(D)]
     Y = cf.DeviceBuffer.empty((B, S, D), dt)
     p = cf.MhaFusedParams(B, S, D, H, H, d, float(1 / np.sqrt(d)), False, causal)
-    name = "mha_fused_f16_cuda" if f16 else "mha_fused_f32_cuda"
+    name = "mha_fused_f16io_cuda" if f16 else "mha_fused_f32_cuda"
     ms = time_op(cf, name, ins, [Y], p, stream, steps, warmup)
     st = sorted(time_op(cf, name, ins, [Y], p, stream, steps, 1) for _ in range(STAT_REPS))
     kms = fused_kernel_times(cf, ins, [Y], p, stream, f16, steps, warmup)
@@ -458,7 +458,7 @@ def vendor_comparison(reps: int = 50) -> dict:
 
 
 def bench_prefill(cf, stream, steps, warmup, fp32=True) -> dict:
-    """Configs 3 and 5 through mha_fused_f16_cuda, and config 3's shape through the FP32
+    """Configs 3 and 5 through mha_fused_f16io_cuda (fp16 buffers), and config 3's shape through the FP32
     entry (mha_fused_f32_cuda, fp32 MFMA): TFLOP/s over the algorithmic FLOPs, with a
     roofline block per config (the whole op and each of its three kernels, timed in this
     run) against the dense MFMA peak of the arithmetic type."""

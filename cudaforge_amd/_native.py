@@ -171,7 +171,7 @@ def _proto(lib):
         fn.restype = res
         fn.argtypes = args
     for name in ("mha_decode_f32_cuda", "mha_decode_f16_cuda", "mha_decode_attn_f32_cuda",
-                 "mha_decode_attn_f16_cuda", "mha_fused_f32_cuda", "mha_fused_f16_cuda",
+                 "mha_decode_attn_f16_cuda", "mha_fused_f32_cuda", "mha_fused_f16_cuda", "mha_fused_f16io_cuda",
                  "causal_mask_f32_cuda", "rope_f32_cuda", "rope_f16_cuda", "mha_decode_rope_f32_cuda",
                  "mha_decode_rope_f16_cuda", "mha_decode_attn_f16_noalloc"):
         fn = getattr(lib, name)

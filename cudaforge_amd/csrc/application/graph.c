@@ -363,6 +363,9 @@ static const operator_registry_t* resolve_node(const inference_graph_t* g, const
         char b16[64];
         if (bl > 3 && strcmp(base + bl - 3, "f32") == 0) snprintf(b16, sizeof(b16), "%.*sf16", (int)(bl - 3), base);
         else snprintf(b16, sizeof(b16), "%s", base);
+        /* mha_fused_f16_cuda keeps the reference's FP32 buffers; F16 tensors take the
+         * fp16-I/O op. */
+        if (n->type == OP_MHA_FUSED && use_cuda) snprintf(b16, sizeof(b16), "mha_fused_f16io");
         snprintf(buf, buf_len, use_cuda ? "%s_cuda" : "%s", b16);
         op = operator_find(buf);
     }

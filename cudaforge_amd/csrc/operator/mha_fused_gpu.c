@@ -33,26 +33,51 @@ typedef struct {
 static int g_rowcat = 1;
 void mha_fused_set_rowcat(int on) { g_rowcat = on != 0; }
 
-static int fused_plan(int elem, const void* inputs[], void* outputs[], const operator_params_t* params,
-                      void* st, fused_plan_t* pl) {
-    if (!inputs || !inputs[0] || !outputs || !outputs[0] || !params) return -1;
-    if (!inputs[2] || !inputs[4] || !inputs[6] || !inputs[8]) return -1;
+/* The shape of a call, checked as the plan needs it. */
+typedef struct { int64_t B, S, D, H, d, H_kv, kvd; } fused_shape_t;
+
+static int fused_shape(const operator_params_t* params, fused_shape_t* sh) {
+    if (!params) return -1;
     const mha_fused_params_t* p = (const mha_fused_params_t*)params;
     const int64_t B = p->batch_size, S = p->seq_len, D = p->hidden_size;
     const int64_t H = p->num_heads, d = p->head_dim;
     const int64_t H_kv = p->num_kv_heads > 0 ? p->num_kv_heads : H;
     if (B <= 0 || S <= 0 || D <= 0 || H <= 0 || d <= 0 || H % H_kv != 0 || H * d != D) return -1;
     if (B > 65535 || H > 65535 || B * S > (1LL << 31) - 1 || D > (1 << 20)) return -1;
-    const size_t esz = elem == CF_ELEM_F16 ? 2 : 4;
-    const int64_t kvd = H_kv * d;
+    *sh = (fused_shape_t){B, S, D, H, d, H_kv, H_kv * d};
+    return 0;
+}
 
-    size_t cur = 0;
-    const size_t off_q = cf_ws_take(&cur, (size_t)(B * S * D) * esz);
-    const size_t off_k = cf_ws_take(&cur, (size_t)(B * S * kvd) * esz);
-    const size_t off_v = cf_ws_take(&cur, (size_t)(B * S * kvd) * esz);
-    const size_t off_o = cf_ws_take(&cur, (size_t)(B * S * D) * esz);
+/* Workspace areas of the intermediates (q, k, v, attention output), carved from *cur on. */
+static void fused_carve(const fused_shape_t* sh, size_t esz, size_t* cur, size_t off[4]) {
+    off[0] = cf_ws_take(cur, (size_t)(sh->B * sh->S * sh->D) * esz);
+    off[1] = cf_ws_take(cur, (size_t)(sh->B * sh->S * sh->kvd) * esz);
+    off[2] = cf_ws_take(cur, (size_t)(sh->B * sh->S * sh->kvd) * esz);
+    off[3] = cf_ws_take(cur, (size_t)(sh->B * sh->S * sh->D) * esz);
+}
+
+static void fused_fill(int elem, const void* inputs[], void* outputs[], const operator_params_t* params,
+                       const fused_shape_t* sh, char* data, const size_t off[4], fused_plan_t* pl);
+
+static int fused_plan(int elem, const void* inputs[], void* outputs[], const operator_params_t* params,
+                      void* st, fused_plan_t* pl) {
+    if (!inputs || !inputs[0] || !outputs || !outputs[0] || !params) return -1;
+    if (!inputs[2] || !inputs[4] || !inputs[6] || !inputs[8]) return -1;
+    fused_shape_t sh;
+    if (fused_shape(params, &sh) != 0) return -1;
+    size_t cur = 0, off[4];
+    fused_carve(&sh, elem == CF_ELEM_F16 ? 2 : 4, &cur, off);
     char* data = (char*)gpu_workspace_get_stream(st, cur);
     if (!data) return -1;
+    fused_fill(elem, inputs, outputs, params, &sh, data, off, pl);
+    return 0;
+}
+
+static void fused_fill(int elem, const void* inputs[], void* outputs[], const operator_params_t* params,
+                       const fused_shape_t* sh, char* data, const size_t off[4], fused_plan_t* pl) {
+    const mha_fused_params_t* p = (const mha_fused_params_t*)params;
+    const int64_t B = sh->B, S = sh->S, D = sh->D, H = sh->H, d = sh->d, H_kv = sh->H_kv, kvd = sh->kvd;
+    const size_t off_q = off[0], off_k = off[1], off_v = off[2], off_o = off[3];
 
     memset(pl, 0, sizeof(*pl));
     cf_gemm_args_t* g = &pl->qkv;
@@ -108,7 +133,6 @@ static int fused_plan(int elem, const void* inputs[], void* outputs[], const ope
     o->out[0] = outputs[0];
     o->residual = (p->has_residual && inputs[1]) ? inputs[1] : NULL;
     o->elem = elem;
-    return 0;
 }
 
 static int fused_launch(const fused_plan_t* pl, int which, void* st) {
@@ -161,9 +185,47 @@ int mha_fused_f32_cuda(const void* inputs[], void* outputs[],
     return fused_op(CF_ELEM_F32, inputs, outputs, params, stream);
 }
 
+int mha_fused_f16io_cuda(const void* inputs[], void* outputs[],
+                         const operator_params_t* params, stream_t* stream) {
+    return fused_op(CF_ELEM_F16, inputs, outputs, params, stream);
+}
+
+/* The reference's contract for mha_fused_f16_cuda (mha_fused_f16_cuda.cu:209-244): FP32
+ * buffers in and out, FP16 arithmetic inside.  X, R, the weights and biases are rounded
+ * to fp16 (nearest even) into the stream's workspace, the fp16 path runs on them, and Y
+ * is widened back to fp32.  Any S (the reference's kernel held a sequence in shared
+ * memory, S <= 64). */
 int mha_fused_f16_cuda(const void* inputs[], void* outputs[],
                        const operator_params_t* params, stream_t* stream) {
-    return fused_op(CF_ELEM_F16, inputs, outputs, params, stream);
+    if (!inputs || !inputs[0] || !outputs || !outputs[0] || !params) return -1;
+    if (!inputs[2] || !inputs[4] || !inputs[6] || !inputs[8]) return -1;
+    fused_shape_t sh;
+    if (fused_shape(params, &sh) != 0) return -1;
+    const mha_fused_params_t* p = (const mha_fused_params_t*)params;
+    const int64_t BSD = sh.B * sh.S * sh.D, D = sh.D, kvd = sh.kvd;
+    /* Elements of inputs 0..9 (X, R, WQ, bQ, WK, bK, WV, bV, WO, bO); R only when it is used. */
+    const int64_t n_in[10] = {BSD, (p->has_residual && inputs[1]) ? BSD : 0, D * D, D, D * kvd, kvd,
+                              D * kvd, kvd, D * D, D};
+    size_t cur = 0, off_in[10], off_y, off[4];
+    for (int i = 0; i < 10; i++) off_in[i] = cf_ws_take(&cur, (size_t)n_in[i] * 2);
+    off_y = cf_ws_take(&cur, (size_t)BSD * 2);
+    fused_carve(&sh, 2, &cur, off);
+    void* st = cf_stream_of(stream);
+    char* data = (char*)gpu_workspace_get_stream(st, cur);
+    if (!data) return -1;
+    const void* in16[10];
+    for (int i = 0; i < 10; i++) {
+        in16[i] = NULL;
+        if (!inputs[i] || n_in[i] == 0) continue;
+        if (cf_launch_cast(inputs[i], data + off_in[i], n_in[i], CF_CAST_F32_F16, st) != 0) return -1;
+        in16[i] = data + off_in[i];
+    }
+    void* out16[1] = {data + off_y};
+    fused_plan_t pl;
+    fused_fill(CF_ELEM_F16, in16, out16, params, &sh, data, off, &pl);
+    for (int k = 0; k < 3; k++)
+        if (fused_launch(&pl, k, st) != 0) return -1;
+    return cf_launch_cast(data + off_y, outputs[0], BSD, CF_CAST_F16_F32, st);
 }
 
 int causal_mask_f32_cuda(const void* inputs[], void* outputs[],
@@ -176,14 +238,20 @@ int causal_mask_f32_cuda(const void* inputs[], void* outputs[],
 }
 
 /* Registrations (mha_fused_cuda.cu:1191-1197, mha_fused_f16_cuda.cu:246-252,
- * causal_mask_cuda.cu).  mha_fused_f16_cuda now declares "f16" I/O. */
+ * causal_mask_cuda.cu).  mha_fused_f16_cuda declares "f32" I/O as the reference does;
+ * the fp16-I/O op, which graphs of F16 tensors dispatch to, is mha_fused_f16io_cuda. */
 int register_mha_fused_f32_cuda(void) {
     static const operator_registry_t reg = {"mha_fused_f32_cuda", "f32", mha_fused_f32_cuda, 6, OP_FLAG_NONE};
     return operator_register(&reg);
 }
 
 int register_mha_fused_f16_cuda(void) {
-    static const operator_registry_t reg = {"mha_fused_f16_cuda", "f16", mha_fused_f16_cuda, 2, OP_FLAG_NONE};
+    static const operator_registry_t reg = {"mha_fused_f16_cuda", "f32", mha_fused_f16_cuda, 2, OP_FLAG_NONE};
+    return operator_register(&reg);
+}
+
+int register_mha_fused_f16io_cuda(void) {
+    static const operator_registry_t reg = {"mha_fused_f16io_cuda", "f16", mha_fused_f16io_cuda, 1, OP_FLAG_NONE};
     return operator_register(&reg);
 }
 

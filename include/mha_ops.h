@@ -60,11 +60,18 @@ int mha_decode_attn_f16_noalloc(const void* inputs[], void* outputs[],
  * outputs [Y(B,S,D)]; honours causal and num_kv_heads (the reference CPU op ignores both). */
 int mha_fused_f32_cuda(const void* inputs[], void* outputs[],
                        const operator_params_t* params, stream_t* stream);
-/* MHA_Fused with FP16 I/O and fp32 accumulation.  Replaces mha_fused_f16_cuda
- * (src/operator/nn/mha_fused_f16_cuda.cu:209-244), which took FP32 buffers and S <= 64;
- * this one takes F16 buffers like every other _f16 op and any S. */
+/* MHA_Fused with FP16 arithmetic behind FP32 buffers: replaces mha_fused_f16_cuda
+ * (src/operator/nn/mha_fused_f16_cuda.cu:209-244, registered "f32"), same slots and
+ * buffer types.  Inputs are rounded to fp16, the fp16 path runs, Y is widened to fp32;
+ * any S (the reference took S <= 64). */
 int mha_fused_f16_cuda(const void* inputs[], void* outputs[],
                        const operator_params_t* params, stream_t* stream);
+/* MHA_Fused with FP16 buffers and fp32 accumulation (registered "f16"): the op graphs of
+ * F16 tensors dispatch MHA_Fused nodes to (the reference's graph named
+ * mha_fused_f16_cuda there, graph.c:841-865, which read those buffers as floats).  Same
+ * slots; every activation, weight and bias _Float16. */
+int mha_fused_f16io_cuda(const void* inputs[], void* outputs[],
+                         const operator_params_t* params, stream_t* stream);
 
 /* CausalMask (src/operator/nn/causal_mask_cuda.cu:6-29): outputs [mask(S,S) f32]. */
 int causal_mask_f32_cuda(const void* inputs[], void* outputs[],
@@ -76,13 +83,14 @@ int register_mha_decode_attn_f32_cuda(void);
 int register_mha_decode_attn_f16_cuda(void);
 int register_mha_fused_f32_cuda(void);
 int register_mha_fused_f16_cuda(void);
+int register_mha_fused_f16io_cuda(void);
 int register_causal_mask_f32_cuda(void);
 
 /* Decode split planning.  Positions per split for the next calls: 0 = automatic (fill
  * every CU), otherwise rounded to the kernel's quantum.  Process-wide; for tuning and
  * split-invariance tests. */
 void    mha_decode_set_split_chunk(int64_t chunk);
-/* Prefill (mha_fused_f16_cuda): 1 (default) writes the QKV projection as one row-major
+/* Prefill (mha_fused_f16io_cuda and mha_fused_f16_cuda): 1 (default) writes the QKV projection as one row-major
  * (B*S, (H + 2 H_kv) d) matrix that attention reads directly, where both kernels take it
  * (fp16, d = 64, S % 8 == 0); 0 always scatters q, k, v^T head-major.  Process-wide; for
  * tests and measurements. */

@@ -159,7 +159,7 @@ def run_fused_gpu(case: FusedCase, stream=None):
     dt = np.float16 if case.f16 else np.float32
     Y = cf.DeviceBuffer.empty((case.B, case.S, case.D), dt)
     p = case.params(cf.MhaFusedParams)
-    name = "mha_fused_f16_cuda" if case.f16 else "mha_fused_f32_cuda"
+    name = "mha_fused_f16io_cuda" if case.f16 else "mha_fused_f32_cuda"
     rc = cf.call_op(name, bufs, [Y], p, stream)
     assert rc == 0, f"{name} returned {rc}"
     return Y.download(stream).astype(np.float32)

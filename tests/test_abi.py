@@ -81,13 +81,15 @@ def test_struct_layouts(native):
 def test_registry_names(native):
     names = {native.operator_at(i).contents.name.decode() for i in range(native.operator_count())}
     hip = {"mha_decode_f32_cuda", "mha_decode_f16_cuda", "mha_decode_attn_f32_cuda", "mha_decode_attn_f16_cuda",
-           "mha_fused_f32_cuda", "mha_fused_f16_cuda", "causal_mask_f32_cuda"}
+           "mha_fused_f32_cuda", "mha_fused_f16_cuda", "mha_fused_f16io_cuda", "causal_mask_f32_cuda"}
     assert hip <= names
     assert native.operator_init_all() == 0              # idempotent
     assert native.operator_count() == len(names)
     assert not native.operator_find(b"mha_fused_f32_nonexistent")
-    e = native.operator_find(b"mha_fused_f16_cuda").contents
-    assert e.data_type == b"f16"
+    # The reference registers mha_fused_f16_cuda as "f32" (FP32 buffers, fp16 math); the
+    # fp16-I/O op that F16 graphs dispatch to is mha_fused_f16io_cuda.
+    assert native.operator_find(b"mha_fused_f16_cuda").contents.data_type == b"f32"
+    assert native.operator_find(b"mha_fused_f16io_cuda").contents.data_type == b"f16"
 
 
 def _slots(vals):
@@ -151,6 +153,11 @@ def test_fused_argument_validation(native):
     p.hidden_size, p.num_kv_heads = 16, 3
     assert native.mha_fused_f32_cuda(ctypes.cast(_slots(good), POINTER(c_void_p)), outs, ctypes.addressof(p),
                                      None) == -1
+    assert native.mha_fused_f16io_cuda(ctypes.cast(_slots(good), POINTER(c_void_p)), outs, ctypes.addressof(p),
+                                       None) == -1
+    p.num_kv_heads = 2
+    bad[0], bad[8] = DP, None     # WO missing
+    assert f(ctypes.cast(_slots(bad), POINTER(c_void_p)), outs, ctypes.addressof(p), None) == -1
 
 
 # ----------------------------------------------------------------------- graph ---
@@ -205,7 +212,7 @@ def test_graph_name_resolution(cpu_ops):
     assert lib.graph_resolve_op(g.g, nid, False, buf, 64) and buf.value == b"mha_fused_f32"
     g.destroy()
     g, nid, _, _ = build_fused_graph(lib, c, f16_out=True)
-    assert lib.graph_resolve_op(g.g, nid, True, buf, 64) and buf.value == b"mha_fused_f16_cuda"
+    assert lib.graph_resolve_op(g.g, nid, True, buf, 64) and buf.value == b"mha_fused_f16io_cuda"
     g.destroy()
 
 

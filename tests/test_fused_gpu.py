@@ -13,7 +13,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from helpers import FusedCase, max_abs, run_fused_gpu
+from helpers import FusedCase, dev, max_abs, run_fused_gpu
 
 pytestmark = pytest.mark.gpu
 
@@ -59,6 +59,26 @@ def test_fused_vs_oracle(gpu, f16, B, S, H, H_kv, d, causal):
     want = c.oracle()
     got = run_fused_gpu(c)
     assert max_abs(want, got) <= (TOL16 if f16 else TOL32)
+
+
+@pytest.mark.parametrize("B,S,H,H_kv,d,causal,residual", [(2, 64, 4, 4, 64, False, True), (1, 130, 8, 2, 64, True, False),
+                                                         (2, 33, 3, 3, 16, False, True), (8, 512, 12, 12, 64, False, False)])
+def test_fused_f16_entry_takes_float_buffers(gpu, B, S, H, H_kv, d, causal, residual):
+    """mha_fused_f16_cuda keeps the reference's contract (mha_fused_f16_cuda.cu:209-244,
+    registered "f32", called with float buffers by tests/bench_bert_mha.c:233-266): FP32
+    inputs and output, fp16 arithmetic inside.  Its result is bit for bit the fp16-I/O
+    op's (mha_fused_f16io_cuda) on the inputs rounded to fp16, widened to fp32, and within
+    the fp16 tolerance of the oracle on those rounded inputs."""
+    import cudaforge_amd as cf
+    c32 = FusedCase(B, S, H, H_kv, d, seed=40 + S, f16=False, causal=causal, residual=residual, bias_std=0.02)
+    c16 = FusedCase(B, S, H, H_kv, d, seed=40 + S, f16=True, causal=causal, residual=residual, bias_std=0.02)
+    bufs = [None if a is None else dev(a, False) for a in c32.arrays()]
+    Y = cf.DeviceBuffer.empty((B, S, H * d), np.float32)
+    assert cf.call_op("mha_fused_f16_cuda", bufs, [Y], c32.params(cf.MhaFusedParams)) == 0
+    got = Y.download()
+    assert got.dtype == np.float32
+    assert np.array_equal(got, run_fused_gpu(c16))
+    assert max_abs(c16.oracle(), got) <= TOL16
 
 
 def test_config3_bert_base_full_size(gpu):
@@ -120,7 +140,7 @@ def test_residual_flag_with_null_residual(gpu):
 def test_graph_fused_on_gpu(gpu, native, f16):
     """graph_execute(use_cuda) over one OP_MHA_FUSED node (the reference's GPU graph test,
     tests/test_bert_mha.c:167-306): F32 tensors resolve to mha_fused_f32_cuda, F16 tensors
-    to mha_fused_f16_cuda."""
+    to the fp16-I/O mha_fused_f16io_cuda."""
     from helpers import DT_F16, DT_F32, OP_INPUT, OP_MHA_FUSED, OP_OUTPUT, Graph
     import oracle as O
     c = FusedCase(2, 48, 4, 2, 32, seed=17, f16=f16, residual=True, causal=True, bias_std=0.02)
@@ -139,7 +159,7 @@ def test_graph_fused_on_gpu(gpu, native, f16):
         assert native.graph_build(g.g) == 0
         buf = ctypes.create_string_buffer(64)
         assert native.graph_resolve_op(g.g, nid, True, buf, 64)
-        assert buf.value == (b"mha_fused_f16_cuda" if f16 else b"mha_fused_f32_cuda")
+        assert buf.value == (b"mha_fused_f16io_cuda" if f16 else b"mha_fused_f32_cuda")
         ins, outs = (ctypes.c_void_p * 1)(tX), (ctypes.c_void_p * 1)(tY)
         assert native.graph_execute(g.g, ins, outs, True) == 0
         got = g.read(tY, c.X.shape, npdt)
