@@ -66,17 +66,22 @@ __device__ __forceinline__ float* partial_at(const cf_decode_attn_args_t& a, int
     return a.partials + ((size_t)unit * a.n_split + split) * (size_t)part_stride(Gx, D);
 }
 
-// Balanced ragged split (a.balanced, grouped fp16 kernel): the attended positions of all
-// sequences laid end to end (W in all) are cut into n_split equal ranges of R positions
-// (a multiple of 16), one per workgroup.  Sequence b (starting at P_b) spans ranges
-// P_b / R .. (P_b + T_b - 1) / R, one split each; its partial records are numbered
-// after those of sequences 0 .. b-1, record (piece, kv head) at piece * H_kv + kv head.
+// Balanced ragged split (a.balanced, grouped fp16 kernel): every workgroup takes one
+// contiguous range of one sequence, and the ranges are about equal across the batch.
+// With W = sum of the attended lengths T_b and L = ceil(W / (n_split - B)), sequence b
+// gets ns_b = ceil(T_b / L) workgroups of C_b = ceil(T_b / ns_b) positions (ns_b then
+// recounted as ceil(T_b / C_b), so no range is empty): sum ns_b <= W / L + B <= n_split,
+// and no workgroup holds more than L positions.  (Ranges that straddled two sequences
+// paid a second ring fill and drain, and those workgroups set the kernel's end.)
+// Sequence b's workgroups are first_b .. first_b + ns_b - 1; workgroup w writes record
+// (w, kv head) at w * H_kv + kv head, so b's records are contiguous from first_b.
 // Every lane of the calling wave gets the geometry (B <= 64: lane b holds sequence b's
-// figures), from one load per lane and two wave prefix sums.
+// figures), from one load per lane, a wave sum and a wave prefix sum.
 struct BalancedGeom {
-    int W, R;          // total attended positions, positions per workgroup
-    int T, P, pieces;  // lane b: T_b, its first position P_b, records before its own
-    int ns;            // lane b: splits (pieces) of sequence b
+    int W;             // total attended positions
+    int used;          // workgroups with a range (sum of ns_b)
+    int T, ns, C;      // lane b: T_b, its workgroups, positions per workgroup
+    int first;         // lane b: its first workgroup (= its first record piece)
 };
 __device__ __forceinline__ int wave_excl_sum(int v, int lane) {
     int x = v;
@@ -91,12 +96,29 @@ __device__ __forceinline__ BalancedGeom balanced_geom(const cf_decode_attn_args_
     const int lane = threadIdx.x & 63;
     BalancedGeom g;
     g.T = lane < a.B ? attended(a, lane) : 0;
-    g.P = wave_excl_sum(g.T, lane);
-    g.W = __builtin_amdgcn_readlane(g.P + g.T, 63);
-    g.R = ((g.W + a.n_split - 1) / a.n_split + 15) / 16 * 16;
-    g.ns = lane < a.B ? (g.P + g.T - 1) / g.R - g.P / g.R + 1 : 0;
-    g.pieces = wave_excl_sum(g.ns, lane);
+    const int P = wave_excl_sum(g.T, lane);
+    g.W = __builtin_amdgcn_readlane(P + g.T, 63);
+    const int avail = max(a.n_split - a.B, 1);           // the launcher keeps n_split >= 2B
+    const int L = max((g.W + avail - 1) / avail, 1);
+    int ns = (g.T + L - 1) / L;
+    g.C = ns > 0 ? (g.T + ns - 1) / ns : 0;
+    g.ns = g.C > 0 ? (g.T + g.C - 1) / g.C : 0;
+    g.first = wave_excl_sum(g.ns, lane);
+    g.used = __builtin_amdgcn_readlane(g.first + g.ns, 63);
     return g;
+}
+
+// The range of workgroup w (< geo.used) in the balanced split: its sequence b and
+// positions [t0, t1) of it, and the number of workgroups b has.
+struct BalancedRange { int b, t0, t1, ns; };
+__device__ __forceinline__ BalancedRange balanced_range(const cf_decode_attn_args_t& a, const BalancedGeom& geo, int w) {
+    const int lane = threadIdx.x & 63;
+    // b = the last sequence whose first workgroup is at or before w (sequences have ns >= 1).
+    const unsigned long long m = __ballot(lane < a.B && geo.first <= w);
+    const int b = 63 - __builtin_clzll(m);
+    const int first = __builtin_amdgcn_readlane(geo.first, b), C = __builtin_amdgcn_readlane(geo.C, b);
+    const int T = __builtin_amdgcn_readlane(geo.T, b), t0 = (w - first) * C;
+    return {b, t0, min(t0 + C, T), __builtin_amdgcn_readlane(geo.ns, b)};
 }
 
 // The splits of (b, unit): their count and where split s's record is (first + s * step
@@ -109,8 +131,8 @@ __device__ __forceinline__ SplitRecords split_records(const cf_decode_attn_args_
         return {(T_b + a.chunk - 1) / a.chunk, a.partials + (size_t)unit * a.n_split * stride, (size_t)stride};
     }
     const BalancedGeom geo = balanced_geom(a);
-    const int ns = __builtin_amdgcn_readlane(geo.ns, b), pieces = __builtin_amdgcn_readlane(geo.pieces, b);
-    return {ns, a.partials + ((size_t)pieces * a.H_kv + unit % units_per_b) * stride, (size_t)a.H_kv * stride};
+    const int ns = __builtin_amdgcn_readlane(geo.ns, b), first = __builtin_amdgcn_readlane(geo.first, b);
+    return {ns, a.partials + ((size_t)first * a.H_kv + unit % units_per_b) * stride, (size_t)a.H_kv * stride};
 }
 
 // ------------------------------------------------------------------ fp16 split ---
@@ -569,21 +591,13 @@ void split_f16(cf_decode_attn_args_t a) {
     _Float16* ring = ring_all + (WIDE ? kvh * WAVE_LDS : 0);
     if constexpr (WIDE) {
         if (a.balanced) {
-            // Ragged lengths: workgroup g takes positions [gR, gR + R) of the batch's
-            // attended positions laid end to end, one piece per sequence it overlaps.
+            // Ragged lengths: one range of one sequence per workgroup (balanced_geom).
             const BalancedGeom geo = balanced_geom(a);
-            const int lo = (int)blockIdx.x * geo.R, hi = min(lo + geo.R, geo.W);
-            for (int b = 0; b < a.B; b++) {
-                const int P = __builtin_amdgcn_readlane(geo.P, b), T = __builtin_amdgcn_readlane(geo.T, b);
-                if (P >= hi) break;
-                if (P + T <= lo) continue;
-                const int first = P / geo.R, ns = __builtin_amdgcn_readlane(geo.ns, b);
-                float* part = ns == 1 ? nullptr
-                                      : a.partials + ((size_t)(__builtin_amdgcn_readlane(geo.pieces, b) +
-                                                               (int)blockIdx.x - first) * a.H_kv + kvh) *
-                                                         part_stride(G, D);
-                split_range<D, G, NS, WIDE>(a, ring, b, kvh, max(lo - P, 0), min(hi - P, T), part);
-            }
+            if ((int)blockIdx.x >= geo.used) return;
+            const BalancedRange r = balanced_range(a, geo, (int)blockIdx.x);
+            float* part = r.ns == 1 ? nullptr
+                                    : a.partials + ((size_t)blockIdx.x * a.H_kv + kvh) * part_stride(G, D);
+            split_range<D, G, NS, WIDE>(a, ring, r.b, kvh, r.t0, r.t1, part);
             return;
         }
     }
@@ -613,18 +627,10 @@ void split_f16_kv(cf_decode_attn_args_t a) {
     _Float16* ring = ring_all + kvh * WAVE_LDS;
     if (a.balanced) {
         const BalancedGeom geo = balanced_geom(a);
-        const int lo = (int)blockIdx.x * geo.R, hi = min(lo + geo.R, geo.W);
-        for (int b = 0; b < a.B; b++) {
-            const int P = __builtin_amdgcn_readlane(geo.P, b), T = __builtin_amdgcn_readlane(geo.T, b);
-            if (P >= hi) break;
-            if (P + T <= lo) continue;
-            const int first = P / geo.R, ns = __builtin_amdgcn_readlane(geo.ns, b);
-            float* part = ns == 1 ? nullptr
-                                  : a.partials + ((size_t)(__builtin_amdgcn_readlane(geo.pieces, b) +
-                                                           (int)blockIdx.x - first) * a.H_kv + kvh) *
-                                                     part_stride(G, D);
-            split_range_kv<D, G, NSV, NSETS>(a, ring, b, kvh, max(lo - P, 0), min(hi - P, T), part);
-        }
+        if ((int)blockIdx.x >= geo.used) return;
+        const BalancedRange r = balanced_range(a, geo, (int)blockIdx.x);
+        float* part = r.ns == 1 ? nullptr : a.partials + ((size_t)blockIdx.x * a.H_kv + kvh) * part_stride(G, D);
+        split_range_kv<D, G, NSV, NSETS>(a, ring, r.b, kvh, r.t0, r.t1, part);
         return;
     }
     const int split = blockIdx.x, b = blockIdx.y;
@@ -1222,8 +1228,10 @@ extern "C" int32_t cf_decode_attn_wide_wgs_per_cu(int32_t elem, int32_t d, int32
 }
 
 extern "C" int32_t cf_decode_attn_balanced_ok(int32_t elem, int32_t d, int32_t group, int32_t h_kv, int32_t B) {
-    // Every workgroup and the merge walk the B lengths to find their ranges.
-    return cf_decode_attn_wide_wgs_per_cu(elem, d, group, h_kv) > 0 && B <= 64 ? 1 : 0;
+    // Every workgroup and the merge derive their ranges from the B lengths (one per lane),
+    // and the partition needs n_split = CUs x workgroups per CU >= 2B.
+    const int per_cu = cf_decode_attn_wide_wgs_per_cu(elem, d, group, h_kv);
+    return per_cu > 0 && B <= 64 && (long long)cu_count() * per_cu >= 2LL * B ? 1 : 0;
 }
 
 extern "C" int32_t cf_decode_attn_wgs_per_cu(int32_t elem, int32_t d, int32_t group) {

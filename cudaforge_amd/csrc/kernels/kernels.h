@@ -35,8 +35,9 @@ typedef struct {
     const int32_t* seq_lens;   /* device, NULL = uniform cache_len */
     int32_t        lens_uniform; /* seq_lens all hold one value (a device-held uniform length) */
     int32_t        balanced;   /* ragged seq_lens on the grouped fp16 kernel: n_split workgroups
-                                  share the batch's attended positions equally (chunk unused);
-                                  partial records: (n_split + B) x H_kv */
+                                  (>= 2B) share the batch's attended positions about equally,
+                                  each one range of one sequence (chunk unused); partial
+                                  records: at most n_split x H_kv */
     float*         partials;   /* workspace */
     int32_t        B, H_q, H_kv, d;
     int32_t        max_seq, cache_len;

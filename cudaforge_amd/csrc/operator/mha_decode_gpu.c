@@ -134,7 +134,7 @@ static size_t attn_args(int elem, const decode_shape_t* s, const int32_t* lens, 
     a->chunk = (int32_t)chunk;
     a->n_split = (int32_t)n_split;
     a->elem = elem;
-    if (a->balanced)   /* records per (piece, kv head); at most n_split + B pieces */
+    if (a->balanced)   /* records per (workgroup, kv head); at most n_split (n_split + B kept as headroom) */
         return (size_t)(a->n_split + a->B) * (size_t)a->H_q * (size_t)(a->d + 4) * sizeof(float);
     return cf_decode_attn_partials_floats(a->B, a->H_q, a->H_kv, a->d, a->n_split, elem) * sizeof(float);
 }

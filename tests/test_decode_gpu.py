@@ -306,10 +306,11 @@ def test_config4_ragged_full_size(gpu):
                                   [16, 4080, 16, 4080], [257, 4095, 1000, 3]])
 def test_balanced_ragged_partition(gpu, native, lens):
     """Ragged fp16 lengths on the grouped kernel split the batch's attended positions
-    evenly over one round of workgroups: ranges that cut sequences anywhere (inside a
-    16-position block too), many short sequences in one range, length-1 sequences and
-    totals smaller than one position per workgroup.  Every row against float64, and
-    against the one-wave kernel (chunked splits over the capacity)."""
+    about evenly over one round of workgroups, each one range of one sequence: ranges
+    that start anywhere (inside a 16-position block too), one workgroup for each of many
+    short sequences, length-1 sequences and totals smaller than one position per
+    workgroup.  Every row against float64, and against the one-wave kernel (chunked
+    splits over the capacity)."""
     from helpers import attn_ref64_all
     B, H_kv, G, d, cap = len(lens), 2, 4, 128, 4096
     H = H_kv * G
