@@ -126,6 +126,7 @@ def _proto(lib):
         "cf_gemm_set_ws": (None, [c_int32]),
         "cf_gemm_set_ws_shape": (None, [c_int32, c_int32]),
         "cf_flash_set_mode": (None, [c_int32]),
+        "cf_flash_set_causal_pairs": (None, [c_int32]),
         "mha_decode_plan": (c_int, [c_void_p, c_int, POINTER(c_int64), POINTER(c_int64)]),
         "cf_decode_attn_scratch_bytes": (c_size_t, []),
         # host platform / tensors

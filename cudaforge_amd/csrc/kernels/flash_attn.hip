@@ -19,8 +19,8 @@
 // registers a lane already holds are exactly its B operand (the V^T reads follow the
 // same permutation).  No score or probability goes through LDS.  Masks are evaluated
 // only on blocks that cross the sequence end or the causal diagonal.  Causal workgroups
-// of this kernel are issued heaviest-first; the DMA kernel below pairs each causal query
-// block with its mirror so every workgroup has the same work.
+// of this kernel and of the DMA kernel below are issued heaviest-first (the DMA kernel
+// can also pair each causal query block with its mirror, equal work per workgroup).
 //
 // fp32 path (d = 64 or 128): the same structure on v_mfma_f32_16x16x4_f32, see flash_f32.
 // Generic path (other head sizes): one thread per query, online softmax in fp32 with Q
@@ -261,7 +261,7 @@ __device__ __forceinline__ int trswz(int row) { return 2 * ((row >> 1) & 3); }
 // build (taken with at least two workgroups per CU) at three would spill registers.
 template <int NJ, bool RC = false>
 __global__ __launch_bounds__(kThreads, NJ == 1 ? 3 : 2)
-void flash_f16_dma64(cf_flash_args_t a) {
+void flash_f16_dma64(cf_flash_args_t a, int pairs) {
     constexpr int D = 64;
     constexpr int QW = 16 * NJ;                   // queries per wave
     constexpr int QB = 4 * QW;                    // queries per workgroup
@@ -272,14 +272,19 @@ void flash_f16_dma64(cf_flash_args_t a) {
     static_assert(NS == 3, "the prologue issues two blocks");
     __shared__ __attribute__((aligned(16))) _Float16 ring[NS * 2 * TILE];
 
-    // Causal: workgroup slot qi runs query block nqb-1-qi and then its mirror qi, so
-    // every workgroup does nqb+1 key blocks whatever the order the CUs receive them in
-    // (one block per slot when the two meet).
+    // Causal (pairs == 0, the default): one query block per workgroup, every head's
+    // heaviest blocks first (slot-major order), so later, lighter blocks fill the CUs
+    // that finish early.  With pairs, workgroup slot qi runs query block nqb-1-qi and
+    // then its mirror qi, so every workgroup does nqb+1 key blocks (one block per slot
+    // when the two meet).
     const int nqb = (a.S + QB - 1) / QB;
-    const int nslot = a.causal ? (nqb + 1) / 2 : nqb;
     const int HB = a.B * a.H_q;
+    const int paired = a.causal && pairs;
+    const int nslot = paired ? (nqb + 1) / 2 : nqb;
     const int w = blockIdx.x, r8 = w & 7, rest = w >> 3;
-    const int qi = rest % nslot, grp = rest / nslot;
+    const int ngrp = (HB + 7) / 8;
+    const int qi = a.causal && !pairs ? rest / ngrp : rest % nslot;
+    const int grp = a.causal && !pairs ? rest % ngrp : rest / nslot;
     const int hb = grp * 8 + r8;
     if (hb >= HB) return;                          // padding of the last group of 8
     const int h = hb % a.H_q, b = hb / a.H_q;
@@ -540,6 +545,10 @@ void flash_f16_dma64(cf_flash_args_t a) {
         return;
     }
     const int heavy = nqb - 1 - qi;
+    if (!pairs) {
+        run(heavy);
+        return;
+    }
     run(heavy);
     if (qi < heavy) {
         wait_vm<0>();                              // the first block's output stores
@@ -800,10 +809,13 @@ void flash_generic(cf_flash_args_t a) {
 // Tuning/test switch for fp16 d = 64: 0 register-staged kernel, 1 DMA kernel with 32
 // queries per wave, 2 DMA kernel with 16 per wave, 3 (default) DMA kernel, chosen by size.
 int g_flash_mode = 3;
+int g_flash_pairs = 0;   // causal DMA kernel: 1 pairs each query block with its mirror; 0 (default)
+                         // one block per workgroup, heaviest first
 
 }  // namespace
 
 extern "C" void cf_flash_set_mode(int32_t mode) { g_flash_mode = mode >= 0 && mode <= 3 ? mode : 3; }
+extern "C" void cf_flash_set_causal_pairs(int32_t on) { g_flash_pairs = on > 0 ? 1 : 0; }
 
 extern "C" int32_t cf_flash_rowcat_ok(const cf_flash_args_t* a) {
     return a->elem == CF_ELEM_F16 && a->d == 64 && a->S > 0 && a->S % 8 == 0 && a->S <= (1 << 24) &&
@@ -828,17 +840,24 @@ extern "C" int cf_launch_flash_attn(const cf_flash_args_t* a, void* stream) {
             // them the waves per SIMD that hide each block's latency chain; 32 per wave
             // halves the LDS traffic per query (every wave reads the whole K/V^T block),
             // better once there are two 128-query workgroups per CU.
-            auto slots = [&](int nj) {                 // causal pairs query blocks
-                const long long n = (a->S + 64 * nj - 1) / (64 * nj);
-                return a->causal ? (n + 1) / 2 : n;
-            };
-            const int nj = g_flash_mode == 1 ? 2 : g_flash_mode == 2 ? 1 : (groups * slots(2) * 8 < 2LL * cu_count() ? 1 : 2);
-            dim3 grid2((unsigned)(groups * slots(nj) * 8));
+            // Causal: one query block per workgroup, the heaviest blocks of every head
+            // first, so the CUs that finish early take the light ones.  Pairing each block
+            // with its mirror (equal work per workgroup, half as many) measured slower at
+            // 16-query waves: S = 512, 96 heads 12.3 against 9.35 us; S = 1024, 64 heads
+            // 18.5 against 17.3 us; S = 2048, 32 heads 30.6 against 26.7 us.  The query
+            // width is still chosen as if paired (32-query waves only with two paired
+            // workgroups per CU), which keeps config 5 on 16-query waves.
+            auto nblocks = [&](int nj) { return (a->S + 64LL * nj - 1) / (64LL * nj); };
+            auto pair_slots = [&](int nj) { return a->causal ? (nblocks(nj) + 1) / 2 : nblocks(nj); };
+            const int nj = g_flash_mode == 1 ? 2 : g_flash_mode == 2 ? 1
+                         : (groups * pair_slots(2) * 8 < 2LL * cu_count() ? 1 : 2);
+            const int pairs = a->causal && g_flash_pairs ? 1 : 0;
+            dim3 grid2((unsigned)(groups * (pairs ? pair_slots(nj) : nblocks(nj)) * 8));
             if (a->qkv_ld) {
-                if (nj == 1) hipLaunchKernelGGL((flash_f16_dma64<1, true>), grid2, dim3(kThreads), 0, s, *a);
-                else hipLaunchKernelGGL((flash_f16_dma64<2, true>), grid2, dim3(kThreads), 0, s, *a);
-            } else if (nj == 1) hipLaunchKernelGGL(flash_f16_dma64<1>, grid2, dim3(kThreads), 0, s, *a);
-            else hipLaunchKernelGGL(flash_f16_dma64<2>, grid2, dim3(kThreads), 0, s, *a);
+                if (nj == 1) hipLaunchKernelGGL((flash_f16_dma64<1, true>), grid2, dim3(kThreads), 0, s, *a, pairs);
+                else hipLaunchKernelGGL((flash_f16_dma64<2, true>), grid2, dim3(kThreads), 0, s, *a, pairs);
+            } else if (nj == 1) hipLaunchKernelGGL(flash_f16_dma64<1>, grid2, dim3(kThreads), 0, s, *a, pairs);
+            else hipLaunchKernelGGL(flash_f16_dma64<2>, grid2, dim3(kThreads), 0, s, *a, pairs);
         } else if (a->d == 64) hipLaunchKernelGGL(flash_f16<64>, grid, dim3(kThreads), 0, s, *a);
         else hipLaunchKernelGGL(flash_f16<128>, grid, dim3(kThreads), 0, s, *a);
         return (int)hipGetLastError();

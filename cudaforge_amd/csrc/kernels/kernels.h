@@ -237,6 +237,9 @@ int32_t cf_flash_rowcat_ok(const cf_flash_args_t* a);
  * staged kernel, 1 / 2 the DMA-ring kernel with 32 / 16 queries per wave, 3 (default)
  * the DMA-ring kernel where it applies (S % 8 == 0) with the width chosen by size. */
 void cf_flash_set_mode(int32_t mode);
+/* Causal fp16 DMA attention: 1 runs each query block and its mirror in one workgroup;
+ * 0 (default) one block per workgroup, heaviest first (tests and measurements). */
+void cf_flash_set_causal_pairs(int32_t on);
 
 /* CausalMask (S, S) float on the device. */
 int cf_launch_causal_mask(float* mask, int64_t S, void* stream);

@@ -187,6 +187,26 @@ def test_flash_kernel_variants_agree(gpu, native, causal):
         assert max_abs(outs[0], o) <= 1e-2
 
 
+@pytest.mark.parametrize("B,S,H,H_kv,mode", [(2, 264, 8, 2, 2), (2, 264, 8, 2, 1), (1, 1024, 16, 16, 2), (3, 72, 4, 4, 2)])
+def test_causal_attention_schedules_bit_identical(gpu, native, B, S, H, H_kv, mode):
+    """Causal DMA attention with each query block paired with its mirror in one
+    workgroup (cf_flash_set_causal_pairs(1)) and with one block per workgroup, heaviest
+    first (0, the default): the same per-block arithmetic, so the same bits, at 16- and
+    32-query waves, an odd block count and a length inside a block."""
+    c = FusedCase(B, S, H, H_kv, 64, seed=S + 5, f16=True, causal=True, residual=False, bias_std=0.02)
+    outs = []
+    try:
+        native.cf_flash_set_mode(mode)
+        for pairs in (1, 0):
+            native.cf_flash_set_causal_pairs(pairs)
+            outs.append(run_fused_gpu(c))
+    finally:
+        native.cf_flash_set_causal_pairs(0)
+        native.cf_flash_set_mode(3)
+    assert max_abs(c.oracle(), outs[0]) <= TOL16
+    assert np.array_equal(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("B,S,H,H_kv,causal", [(16, 200, 8, 2, False), (16, 200, 8, 2, True), (1, 384, 6, 6, True),
                                               (2, 512, 12, 12, False)])
 def test_prefill_row_concatenated_qkv(gpu, native, B, S, H, H_kv, causal):
