@@ -21,6 +21,26 @@ typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 lds_h4_t;
 // would otherwise emit flat loads, which also count against lgkmcnt).
 #define CF_GLOBAL __attribute__((address_space(1)))
 
+// Quotient of 0 <= n < 2^31 by a divisor d >= 1 fixed at launch, without the ~25
+// instructions of a runtime division: q = (n * mul) >> shift in 64 bits, with
+// shift = 31 + ceil(log2 d) and mul = ceil(2^shift / d) < 2^32, computed once on the host.
+// Exact: mul * d = 2^shift + e with 0 <= e < d, so n * mul / 2^shift = n / d + n e / (d 2^shift),
+// and n e < n d < 2^31 * 2^ceil(log2 d) = 2^shift keeps the second term below 1/d.
+// Wave-uniform operands compile to scalar multiplies.
+struct FastDiv {
+    uint32_t mul;
+    uint32_t shift;
+};
+__host__ inline FastDiv fastdiv_make(int d) {
+    uint32_t l = 0;
+    while ((1u << l) < (uint32_t)d) l++;
+    const uint32_t shift = 31 + l;
+    return FastDiv{(uint32_t)(((1ull << shift) + (uint64_t)d - 1) / (uint64_t)d), shift};
+}
+__device__ __forceinline__ int fastdiv(int n, FastDiv f) {
+    return (int)(((uint64_t)(uint32_t)n * f.mul) >> f.shift);
+}
+
 // s_waitcnt vmcnt(N), expcnt/lgkmcnt left at their maxima (gfx9 encoding).  The empty
 // asm after it keeps the compiler from hoisting LDS reads above the wait.
 template <int N>

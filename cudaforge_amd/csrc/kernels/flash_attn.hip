@@ -261,7 +261,7 @@ __device__ __forceinline__ int trswz(int row) { return 2 * ((row >> 1) & 3); }
 // build (taken with at least two workgroups per CU) at three would spill registers.
 template <int NJ, bool RC = false>
 __global__ __launch_bounds__(kThreads, NJ == 1 ? 3 : 2)
-void flash_f16_dma64(cf_flash_args_t a, int pairs) {
+void flash_f16_dma64(cf_flash_args_t a, int pairs, FastDiv div_slot, FastDiv div_hq, FastDiv div_g) {
     constexpr int D = 64;
     constexpr int QW = 16 * NJ;                   // queries per wave
     constexpr int QB = 4 * QW;                    // queries per workgroup
@@ -281,15 +281,18 @@ void flash_f16_dma64(cf_flash_args_t a, int pairs) {
     const int HB = a.B * a.H_q;
     const int paired = a.causal && pairs;
     const int nslot = paired ? (nqb + 1) / 2 : nqb;
+    // The launcher's divisors (FastDiv): div_slot by ngrp (causal, one block per
+    // workgroup) or nslot, div_hq by H_q, div_g by H_q / H_kv.
     const int w = blockIdx.x, r8 = w & 7, rest = w >> 3;
     const int ngrp = (HB + 7) / 8;
-    const int qi = a.causal && !pairs ? rest / ngrp : rest % nslot;
-    const int grp = a.causal && !pairs ? rest % ngrp : rest / nslot;
+    const int rq = fastdiv(rest, div_slot), rr = rest - rq * (a.causal && !pairs ? ngrp : nslot);
+    const int qi = a.causal && !pairs ? rq : rr;
+    const int grp = a.causal && !pairs ? rr : rq;
     const int hb = grp * 8 + r8;
     if (hb >= HB) return;                          // padding of the last group of 8
-    const int h = hb % a.H_q, b = hb / a.H_q;
+    const int b = fastdiv(hb, div_hq), h = hb - b * a.H_q;
     const int S = a.S;
-    const int kvh = h / (a.H_q / a.H_kv);
+    const int kvh = fastdiv(h, div_g);
   auto run = [&](int qb) {
     const int q0 = qb * QB;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -852,12 +855,17 @@ extern "C" int cf_launch_flash_attn(const cf_flash_args_t* a, void* stream) {
             const int nj = g_flash_mode == 1 ? 2 : g_flash_mode == 2 ? 1
                          : (groups * pair_slots(2) * 8 < 2LL * cu_count() ? 1 : 2);
             const int pairs = a->causal && g_flash_pairs ? 1 : 0;
-            dim3 grid2((unsigned)(groups * (pairs ? pair_slots(nj) : nblocks(nj)) * 8));
+            const long long nslot = pairs ? pair_slots(nj) : nblocks(nj);
+            dim3 grid2((unsigned)(groups * nslot * 8));
+            // The kernel's grid decomposition divides by these (measured: ~0.45 us of
+            // config 5's attention as runtime divisions in every workgroup's prologue).
+            const FastDiv dslot = fastdiv_make((int)(a->causal && !pairs ? groups : nslot));
+            const FastDiv dhq = fastdiv_make(a->H_q), dg = fastdiv_make(a->H_q / a->H_kv);
             if (a->qkv_ld) {
-                if (nj == 1) hipLaunchKernelGGL((flash_f16_dma64<1, true>), grid2, dim3(kThreads), 0, s, *a, pairs);
-                else hipLaunchKernelGGL((flash_f16_dma64<2, true>), grid2, dim3(kThreads), 0, s, *a, pairs);
-            } else if (nj == 1) hipLaunchKernelGGL(flash_f16_dma64<1>, grid2, dim3(kThreads), 0, s, *a, pairs);
-            else hipLaunchKernelGGL(flash_f16_dma64<2>, grid2, dim3(kThreads), 0, s, *a, pairs);
+                if (nj == 1) hipLaunchKernelGGL((flash_f16_dma64<1, true>), grid2, dim3(kThreads), 0, s, *a, pairs, dslot, dhq, dg);
+                else hipLaunchKernelGGL((flash_f16_dma64<2, true>), grid2, dim3(kThreads), 0, s, *a, pairs, dslot, dhq, dg);
+            } else if (nj == 1) hipLaunchKernelGGL(flash_f16_dma64<1>, grid2, dim3(kThreads), 0, s, *a, pairs, dslot, dhq, dg);
+            else hipLaunchKernelGGL(flash_f16_dma64<2>, grid2, dim3(kThreads), 0, s, *a, pairs, dslot, dhq, dg);
         } else if (a->d == 64) hipLaunchKernelGGL(flash_f16<64>, grid, dim3(kThreads), 0, s, *a);
         else hipLaunchKernelGGL(flash_f16<128>, grid, dim3(kThreads), 0, s, *a);
         return (int)hipGetLastError();

@@ -45,7 +45,24 @@ struct Tiling {
     int w_vec[3];       // W rows of segment s may be read with vector loads
     int epi_vec;        // fp16 epilogue may use 8-element stores (alignment and shape)
     int group_m;        // tile rows per group of the XCD-aware tile order
+    int n_tiles_n;      // column tiles (set_order)
+    // Divisors of the tile order, fixed per launch (set_order): group_m * n_tiles_n,
+    // group_m, and the last group's height n_tiles_m - (groups - 1) * group_m.
+    FastDiv div_group, div_gm, div_gm_last;
 };
+
+// Fills the tile order's divisors; every launch of a kernel that calls tile_of_block
+// sets them first (as runtime divisions they were ~75 scalar instructions of every
+// workgroup's prologue).
+inline void set_order(Tiling& t, int tiles_n) {
+    t.n_tiles_n = tiles_n;
+    const int gm = t.group_m > 0 ? t.group_m : 1;
+    const int groups = (t.n_tiles_m + gm - 1) / gm;
+    t.div_group = fastdiv_make(gm * tiles_n > 0 ? gm * tiles_n : 1);
+    t.div_gm = fastdiv_make(gm);
+    const int last = t.n_tiles_m - (groups - 1) * gm;
+    t.div_gm_last = fastdiv_make(last > 0 ? last : 1);
+}
 
 __device__ __forceinline__ float to_f(float x) { return x; }
 __device__ __forceinline__ float to_f(_Float16 x) { return (float)x; }
@@ -59,18 +76,20 @@ template <typename T> __device__ __forceinline__ T from_f(float x) { return (T)x
 constexpr int kXcds = 8;
 constexpr int kGroupM = 4;
 
-__device__ __forceinline__ void tile_of_block(int blk, int tiles_m, int tiles_n, int group_m, int& tm, int& tn) {
+__device__ __forceinline__ void tile_of_block(int blk, const Tiling& tl, int& tm, int& tn) {
+    const int tiles_m = tl.n_tiles_m, tiles_n = tl.n_tiles_n, group_m = tl.group_m;
     const int T = tiles_m * tiles_n;
     const int x = blk % kXcds, j = blk / kXcds;
     const int base = T / kXcds, rem = T % kXcds;
     const int t = x * base + min(x, rem) + j;      // position in the tile order
     const int per_group = group_m * tiles_n;
-    const int g = t / per_group;
+    const int g = fastdiv(t, tl.div_group);
     const int first_m = g * group_m;
     const int gm = min(tiles_m - first_m, group_m);
     const int r = t - g * per_group;
-    tm = first_m + r % gm;
-    tn = r / gm;
+    const int q = gm == group_m ? fastdiv(r, tl.div_gm) : fastdiv(r, tl.div_gm_last);
+    tm = first_m + (r - q * gm);
+    tn = q;
 }
 
 __device__ __forceinline__ int find_seg(const cf_gemm_args_t& a, const Tiling& t, int tile_n) {
@@ -216,7 +235,7 @@ void gemm_f16(cf_gemm_args_t a, Tiling t) {
     __shared__ __attribute__((aligned(16))) _Float16 smem[2 * (A_STAGE + W_STAGE)];
 
     int tile_m, tile_n;
-    tile_of_block(blockIdx.x, t.n_tiles_m, t.seg_start[3], t.group_m, tile_m, tile_n);
+    tile_of_block(blockIdx.x, t, tile_m, tile_n);
     const int seg = find_seg(a, t, tile_n);
     const int N = a.n[seg];
     const int m0 = tile_m * BM;
@@ -482,7 +501,7 @@ void gemm_f16_async(cf_gemm_args_t a, Tiling t) {
     _Float16* const smem = (KSPLIT == 1 ? smem_s : smem_dyn) + kg * STAGES * ST;
 
     int tile_m, tile_n;
-    tile_of_block(blockIdx.x, t.n_tiles_m, t.seg_start[3], t.group_m, tile_m, tile_n);
+    tile_of_block(blockIdx.x, t, tile_m, tile_n);
     const int seg = find_seg(a, t, tile_n);
     const int N = a.n[seg];
     const int K = a.K;
@@ -649,7 +668,7 @@ void gemm_f32(cf_gemm_args_t a, Tiling t) {
     __shared__ float Bs[2][BK32 * LDN];     // [k][n]
 
     int tile_m, tile_n;
-    tile_of_block(blockIdx.x, t.n_tiles_m, t.seg_start[3], t.group_m, tile_m, tile_n);
+    tile_of_block(blockIdx.x, t, tile_m, tile_n);
     const int seg = find_seg(a, t, tile_n);
     const int N = a.n[seg];
     const int m0 = tile_m * BM;
@@ -902,7 +921,7 @@ void gemm_f16_ws(cf_gemm_args_t a, Tiling t) {
     start[2] = a.n[0] + (a.nseg > 1 ? a.n[1] : 0);
     start[3] = start[2] + (a.nseg > 2 ? a.n[2] : 0);
     int tile_m, tile_n;
-    tile_of_block(blockIdx.x, t.n_tiles_m, start[3] / BN, t.group_m, tile_m, tile_n);
+    tile_of_block(blockIdx.x, t, tile_m, tile_n);
     const int m0 = tile_m * BM, n0 = tile_n * BN;
     const int K = a.K, nk = K / WS_BK;
     // Every column of the tile goes to v^T: accumulate C and stage it column-major.
@@ -1371,6 +1390,7 @@ extern "C" int cf_launch_gemm(const cf_gemm_args_t* a, void* stream) {
         t.n_tiles_m = a->M / c->bm;
         const long long blocks = (long long)t.n_tiles_m * (ntot / c->bn);
         if (blocks <= 0 || blocks > 0x7fffffffLL) return (int)hipErrorInvalidValue;
+        set_order(t, (int)(ntot / c->bn));
         const hipError_t e = c->launch(dim3((unsigned)blocks), (hipStream_t)stream, *a, t);
         if (e != hipSuccess) return (int)e;
         return (int)hipGetLastError();
@@ -1420,6 +1440,7 @@ extern "C" int cf_launch_gemm(const cf_gemm_args_t* a, void* stream) {
     for (int s = a->nseg; s < 4; s++) t.seg_start[s] = acc;
     const long long blocks = (long long)acc * t.n_tiles_m;
     if (blocks <= 0 || blocks > 0x7fffffffLL) return (int)hipErrorInvalidValue;
+    set_order(t, acc);
     dim3 grid((unsigned)blocks);
     hipStream_t st = (hipStream_t)stream;
     if (full) {
