@@ -118,6 +118,53 @@ __device__ __forceinline__ float max_xor32(float x) { float a = x, b = x; swap_x
 __device__ __forceinline__ float add_xor16(float x) { float a = x, b = x; swap_xor16(a, b); return a + b; }
 __device__ __forceinline__ float add_xor32(float x) { float a = x, b = x; swap_xor32(a, b); return a + b; }
 
+// DPP moves inside 16-lane rows (gfx9 dpp_ctrl encodings), VALU operands with no LDS
+// round trip (a ds_bpermute or ds_swizzle exchange waits on the LDS pipe): quad_perm
+// [1,0,3,2] reads lane ^ 1, quad_perm [2,3,0,1] lane ^ 2, row_half_mirror lane ^ 7 within
+// 8 lanes, row_mirror lane ^ 15 within 16, row_shr:n lane - n within the row (bound_ctrl:
+// 0 where that leaves the row).
+enum : int { kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140, kDppShr = 0x110 };
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int x) { return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, true); }
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) { return __int_as_float(dpp_i<CTRL>(__float_as_int(x))); }
+
+// The wave's maximum and sum in every lane.  After the two quad steps every lane of a
+// quad holds the quad's value, so the half-row mirror pairs quads and the row mirror
+// pairs 8-lane halves; the row swaps finish across rows.  Each step combines two equal
+// pairs of operands (a + b on one lane, b + a on its partner), so all lanes get the
+// same bits.
+__device__ __forceinline__ float wave_max(float x) {
+    x = fmaxf(x, dpp_f<kDppXor1>(x));
+    x = fmaxf(x, dpp_f<kDppXor2>(x));
+    x = fmaxf(x, dpp_f<kDppHalfMirror>(x));
+    x = fmaxf(x, dpp_f<kDppMirror>(x));
+    return max_xor32(max_xor16(x));
+}
+__device__ __forceinline__ float wave_sum(float x) {
+    x += dpp_f<kDppXor1>(x);
+    x += dpp_f<kDppXor2>(x);
+    x += dpp_f<kDppHalfMirror>(x);
+    x += dpp_f<kDppMirror>(x);
+    return add_xor32(add_xor16(x));
+}
+
+// Exclusive prefix sum of v over lanes 0 .. lane - 1: an inclusive scan inside each
+// 16-lane row (row_shr 1, 2, 4, 8), then every row adds the totals of the rows before it
+// (read from lanes 15, 31, 47).
+__device__ __forceinline__ int wave_excl_sum(int v, int lane) {
+    int x = v;
+    x += dpp_i<kDppShr + 1>(x);
+    x += dpp_i<kDppShr + 2>(x);
+    x += dpp_i<kDppShr + 4>(x);
+    x += dpp_i<kDppShr + 8>(x);
+    const int r0 = __builtin_amdgcn_readlane(x, 15), r1 = __builtin_amdgcn_readlane(x, 31);
+    const int r2 = __builtin_amdgcn_readlane(x, 47);
+    const int row = lane >> 4;
+    x += (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
+    return x - v;
+}
+
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
     return (uint32_t)(uintptr_t)(const CF_LDS void*)p;
 }

@@ -83,15 +83,6 @@ struct BalancedGeom {
     int T, ns, C;      // lane b: T_b, its workgroups, positions per workgroup
     int first;         // lane b: its first workgroup (= its first record piece)
 };
-__device__ __forceinline__ int wave_excl_sum(int v, int lane) {
-    int x = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(x, o, 64);
-        if (lane >= o) x += y;
-    }
-    return x - v;
-}
 __device__ __forceinline__ BalancedGeom balanced_geom(const cf_decode_attn_args_t& a) {
     const int lane = threadIdx.x & 63;
     BalancedGeom g;
@@ -124,15 +115,18 @@ __device__ __forceinline__ BalancedRange balanced_range(const cf_decode_attn_arg
 // The splits of (b, unit): their count and where split s's record is (first + s * step
 // records of `stride` floats).
 struct SplitRecords { int n; const float* first; size_t step; };
+// The merge launches' divisors (FastDiv): the row's group size Gx, the units per batch
+// row, and the split length.
+struct MergeDivs { FastDiv gx, ub, chunk; };
 __device__ __forceinline__ SplitRecords split_records(const cf_decode_attn_args_t& a, int b, int unit,
-                                                      int units_per_b, int stride) {
+                                                      int units_per_b, int stride, const MergeDivs& md) {
     if (!a.balanced) {
         const int T_b = attended(a, b);
-        return {(T_b + a.chunk - 1) / a.chunk, a.partials + (size_t)unit * a.n_split * stride, (size_t)stride};
+        return {fastdiv(T_b + a.chunk - 1, md.chunk), a.partials + (size_t)unit * a.n_split * stride, (size_t)stride};
     }
     const BalancedGeom geo = balanced_geom(a);
     const int ns = __builtin_amdgcn_readlane(geo.ns, b), first = __builtin_amdgcn_readlane(geo.first, b);
-    return {ns, a.partials + ((size_t)first * a.H_kv + unit % units_per_b) * stride, (size_t)a.H_kv * stride};
+    return {ns, a.partials + ((size_t)first * a.H_kv + (unit - b * units_per_b)) * stride, (size_t)a.H_kv * stride};
 }
 
 // ------------------------------------------------------------------ fp16 split ---
@@ -897,7 +891,7 @@ void split_generic(cf_decode_attn_args_t a) {
 // (M, num, den) with the log-sum-exp rescale, so there is no LDS and no barrier.
 template <typename T>
 __global__ __launch_bounds__(kMergeThreads)
-void merge_kernel(cf_decode_attn_args_t a, int Gx, int units_per_b) {
+void merge_kernel(cf_decode_attn_args_t a, int Gx, int units_per_b, MergeDivs md) {
     const int D = a.d;
     const size_t idx = (size_t)blockIdx.x * kMergeThreads + threadIdx.x;
     const size_t total = (size_t)a.B * units_per_b * Gx * D;
@@ -908,7 +902,7 @@ void merge_kernel(cf_decode_attn_args_t a, int Gx, int units_per_b) {
     const int unit = (int)(ug / Gx);
     const int b = unit / units_per_b;
     const int stride = part_stride(Gx, D), hdr = part_hdr(Gx);
-    const SplitRecords sr = split_records(a, b, unit, units_per_b, stride);
+    const SplitRecords sr = split_records(a, b, unit, units_per_b, stride, md);
     const int nsplit = sr.n;
     if (nsplit <= 1) return;                       // finished by the split kernel
     constexpr int NB = 16;
@@ -951,12 +945,12 @@ void merge_kernel(cf_decode_attn_args_t a, int Gx, int units_per_b) {
 // of splits; 256 threads measured faster than 1024 per row).
 template <typename T, int NT = kMergeThreads>
 __global__ __launch_bounds__(NT)
-void merge_rows(cf_decode_attn_args_t a, int Gx, int units_per_b, int ds) {
+void merge_rows(cf_decode_attn_args_t a, int Gx, int units_per_b, int ds, MergeDivs md) {
     const int D = a.d, DV = D / (4 * ds), SG = NT / DV;
     const int row = blockIdx.x / ds, part = blockIdx.x - row * ds;
-    const int g = row % Gx, unit = row / Gx, b = unit / units_per_b;
+    const int unit = fastdiv(row, md.gx), g = row - unit * Gx, b = fastdiv(unit, md.ub);
     const int stride = part_stride(Gx, D), hdr = part_hdr(Gx);
-    const SplitRecords sr = split_records(a, b, unit, units_per_b, stride);
+    const SplitRecords sr = split_records(a, b, unit, units_per_b, stride, md);
     const int nsplit = sr.n;
     if (nsplit <= 1) return;                       // finished by the split kernel
     const int tid = threadIdx.x, col = part * DV + tid % DV, sg = tid / DV;
@@ -1034,15 +1028,15 @@ void merge_rows(cf_decode_attn_args_t a, int Gx, int units_per_b, int ds) {
 // s % 64), eight in flight.
 template <typename T, int DPL>
 __global__ __launch_bounds__(256)
-void merge_wave(cf_decode_attn_args_t a, int Gx, int units_per_b, int rows) {
+void merge_wave(cf_decode_attn_args_t a, int Gx, int units_per_b, int rows, MergeDivs md) {
     constexpr int D = 64 * DPL;
     constexpr int MAXS = kMergeWaveSplits;
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int row = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     if (row >= rows) return;
-    const int g = row % Gx, unit = row / Gx, b = unit / units_per_b;
+    const int unit = fastdiv(row, md.gx), g = row - unit * Gx, b = fastdiv(unit, md.ub);
     const int stride = part_stride(Gx, D), hdr = part_hdr(Gx);
-    const SplitRecords sr = split_records(a, b, unit, units_per_b, stride);
+    const SplitRecords sr = split_records(a, b, unit, units_per_b, stride, md);
     const int nsplit = sr.n;
     if (nsplit <= 1) return;                       // finished by the split kernel
     // Every load first (one round trip): lane s < nsplit holds split s's (m, l), and each
@@ -1061,19 +1055,17 @@ void merge_wave(cf_decode_attn_args_t a, int Gx, int units_per_b, int rows) {
 #pragma unroll
         for (int e = 0; e < DPL; e++) av[j][e] = ps[e];
     }
-    float M = mv;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    // Reductions on DPP and the row swaps, weights broadcast by v_readlane: no LDS round
+    // trip after the loads.
+    const float M = wave_max(mv);
     const float w = lane < nsplit ? exp2f(mv - M) : 0.0f;
-    float den = w * lv;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) den += __shfl_xor(den, off, 64);
+    const float den = wave_sum(w * lv);
     float num[DPL];
 #pragma unroll
     for (int e = 0; e < DPL; e++) num[e] = 0.0f;
 #pragma unroll
     for (int j = 0; j < MAXS; j++) {
-        const float wj = __shfl(w, j, 64);        // 0 for j >= nsplit
+        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));   // 0 for j >= nsplit
 #pragma unroll
         for (int e = 0; e < DPL; e++) num[e] = __builtin_fmaf(wj, av[j][e], num[e]);
     }
@@ -1279,17 +1271,18 @@ extern "C" int cf_launch_decode_attn_merge(const cf_decode_attn_args_t* a, void*
     const int Gx = fast ? a->H_q / a->H_kv : 1;
     const int units_per_b = fast ? a->H_kv : a->H_q;
     const int rows = a->B * units_per_b * Gx;
+    const MergeDivs md{fastdiv_make(Gx), fastdiv_make(units_per_b), fastdiv_make(a->chunk > 0 ? a->chunk : 1)};
     // One wave per row while the splits fit a few rounds of eight loads; with many
     // splits (long or ragged caches) a whole workgroup per row keeps more in flight.
     if ((a->d == 64 || a->d == 128) && a->n_split <= kMergeWaveSplits && !g_merge_rows) {
         const int per = g_merge_wave_wg;
         const dim3 grid((unsigned)((rows + per - 1) / per)), blk(64 * per);
         if (a->elem == CF_ELEM_F16) {
-            if (a->d == 64) hipLaunchKernelGGL((merge_wave<_Float16, 1>), grid, blk, 0, s, *a, Gx, units_per_b, rows);
-            else hipLaunchKernelGGL((merge_wave<_Float16, 2>), grid, blk, 0, s, *a, Gx, units_per_b, rows);
+            if (a->d == 64) hipLaunchKernelGGL((merge_wave<_Float16, 1>), grid, blk, 0, s, *a, Gx, units_per_b, rows, md);
+            else hipLaunchKernelGGL((merge_wave<_Float16, 2>), grid, blk, 0, s, *a, Gx, units_per_b, rows, md);
         } else {
-            if (a->d == 64) hipLaunchKernelGGL((merge_wave<float, 1>), grid, blk, 0, s, *a, Gx, units_per_b, rows);
-            else hipLaunchKernelGGL((merge_wave<float, 2>), grid, blk, 0, s, *a, Gx, units_per_b, rows);
+            if (a->d == 64) hipLaunchKernelGGL((merge_wave<float, 1>), grid, blk, 0, s, *a, Gx, units_per_b, rows, md);
+            else hipLaunchKernelGGL((merge_wave<float, 2>), grid, blk, 0, s, *a, Gx, units_per_b, rows, md);
         }
         return (int)hipGetLastError();
     }
@@ -1297,17 +1290,17 @@ extern "C" int cf_launch_decode_attn_merge(const cf_decode_attn_args_t* a, void*
         const int ds = merge_rows_dsplit(a->d);
         dim3 grid((unsigned)((size_t)a->B * units_per_b * Gx * ds));
         if (a->elem == CF_ELEM_F16)
-            hipLaunchKernelGGL((merge_rows<_Float16>), grid, dim3(kMergeThreads), 0, s, *a, Gx, units_per_b, ds);
+            hipLaunchKernelGGL((merge_rows<_Float16>), grid, dim3(kMergeThreads), 0, s, *a, Gx, units_per_b, ds, md);
         else
-            hipLaunchKernelGGL((merge_rows<float>), grid, dim3(kMergeThreads), 0, s, *a, Gx, units_per_b, ds);
+            hipLaunchKernelGGL((merge_rows<float>), grid, dim3(kMergeThreads), 0, s, *a, Gx, units_per_b, ds, md);
         return (int)hipGetLastError();
     }
     const size_t total = (size_t)a->B * units_per_b * Gx * a->d;
     dim3 grid((unsigned)((total + kMergeThreads - 1) / kMergeThreads));
     if (a->elem == CF_ELEM_F16)
-        hipLaunchKernelGGL(merge_kernel<_Float16>, grid, dim3(kMergeThreads), 0, s, *a, Gx, units_per_b);
+        hipLaunchKernelGGL(merge_kernel<_Float16>, grid, dim3(kMergeThreads), 0, s, *a, Gx, units_per_b, md);
     else
-        hipLaunchKernelGGL(merge_kernel<float>, grid, dim3(kMergeThreads), 0, s, *a, Gx, units_per_b);
+        hipLaunchKernelGGL(merge_kernel<float>, grid, dim3(kMergeThreads), 0, s, *a, Gx, units_per_b, md);
     return (int)hipGetLastError();
 }
 
