@@ -122,8 +122,9 @@ __device__ __forceinline__ float add_xor32(float x) { float a = x, b = x; swap_x
 // round trip (a ds_bpermute or ds_swizzle exchange waits on the LDS pipe): quad_perm
 // [1,0,3,2] reads lane ^ 1, quad_perm [2,3,0,1] lane ^ 2, row_half_mirror lane ^ 7 within
 // 8 lanes, row_mirror lane ^ 15 within 16, row_shr:n lane - n within the row (bound_ctrl:
-// 0 where that leaves the row).
-enum : int { kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140, kDppShr = 0x110 };
+// 0 where that leaves the row), row_ror:n lane - n mod 16 within the row.
+enum : int { kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140, kDppShr = 0x110,
+             kDppRor = 0x120 };
 template <int CTRL>
 __device__ __forceinline__ int dpp_i(int x) { return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, true); }
 template <int CTRL>
@@ -147,6 +148,28 @@ __device__ __forceinline__ float wave_sum(float x) {
     x += dpp_f<kDppHalfMirror>(x);
     x += dpp_f<kDppMirror>(x);
     return add_xor32(add_xor16(x));
+}
+
+// Sum over each 16-lane row, in every lane of it (the first four steps of wave_sum).
+__device__ __forceinline__ float row_sum16(float x) {
+    x += dpp_f<kDppXor1>(x);
+    x += dpp_f<kDppXor2>(x);
+    x += dpp_f<kDppHalfMirror>(x);
+    return x + dpp_f<kDppMirror>(x);
+}
+
+// Sum over the lanes with the same lane % S (S = 1, 2, 4, 8, 16 or 32): rotations inside
+// each 16-lane row by S, 2S, .. 8, then the row swaps.  Lanes of one class can end with
+// different roundings (each adds its own pairs first); callers read one lane per class.
+template <int S>
+__device__ __forceinline__ float sum_stride(float x) {
+    static_assert(S == 1 || S == 2 || S == 4 || S == 8 || S == 16 || S == 32, "stride");
+    if constexpr (S == 1) return wave_sum(x);
+    if constexpr (S <= 2) x += dpp_f<kDppRor + 2>(x);
+    if constexpr (S <= 4) x += dpp_f<kDppRor + 4>(x);
+    if constexpr (S <= 8) x += dpp_f<kDppRor + 8>(x);
+    if constexpr (S <= 16) x = add_xor16(x);
+    return add_xor32(x);
 }
 
 // Exclusive prefix sum of v over lanes 0 .. lane - 1: an inclusive scan inside each

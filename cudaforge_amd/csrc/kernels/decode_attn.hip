@@ -646,6 +646,7 @@ void split_f32(cf_decode_attn_args_t a) {
     constexpr int ROWS = NW * RPW;
     constexpr int PIT = ROWS * kF32Unroll;
     static_assert(G <= LPR, "one writer lane per head");
+    static_assert(LPR == 16 || LPR == 32, "row reductions on DPP and the row swaps");
     extern __shared__ float smem[];
 
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
@@ -697,8 +698,8 @@ void split_f32(cf_decode_attn_args_t a) {
                 s = __builtin_fmaf(qv[g][1], kv[u][1], s);
                 s = __builtin_fmaf(qv[g][2], kv[u][2], s);
                 s = __builtin_fmaf(qv[g][3], kv[u][3], s);
-#pragma unroll
-                for (int m = 1; m < LPR; m <<= 1) s += __shfl_xor(s, m);
+                s = row_sum16(s);                  // the row's LPR lanes (DPP, no LDS trip)
+                if constexpr (LPR == 32) s = add_xor16(s);
                 s *= qk_scale;
                 if (pos < t1) {
                     if (c == g) sc[(pos - t0) * G + g] = s;
@@ -715,8 +716,8 @@ void split_f32(cf_decode_attn_args_t a) {
 #pragma unroll
     for (int g = 0; g < G; g++) {
         float m = mloc[g];
-#pragma unroll
-        for (int off = LPR; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+        if constexpr (LPR == 16) m = max_xor16(m);
+        m = max_xor32(m);
         if (lane == 0) red[wave * G + g] = m;
     }
     __syncthreads();
@@ -740,8 +741,7 @@ void split_f32(cf_decode_attn_args_t a) {
             lsum += p;
         }
     }
-#pragma unroll
-    for (int off = G; off < 64; off <<= 1) lsum += __shfl_xor(lsum, off);
+    lsum = sum_stride<G>(lsum);
     if (lane < G) red[NW * G + wave * G + lane] = lsum;
     __syncthreads();
     float L[G];
@@ -782,9 +782,8 @@ void split_f32(cf_decode_attn_args_t a) {
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             float v = acc[g][e];
-#pragma unroll
-            for (int off = LPR; off < 64; off <<= 1) v += __shfl_xor(v, off);
-            acc[g][e] = v;
+            if constexpr (LPR == 16) v = add_xor16(v);
+            acc[g][e] = add_xor32(v);
         }
     __syncthreads();
     float* accbuf = smem;                      // [NW][G][D]

@@ -61,6 +61,9 @@ struct Tiles {
     int ks;                           // K chunks (workgroups along K)
     int dma;                          // fp16 DMA path: its tile width (64/128/256), else 0
     int small;                        // one-pass kernel for small projections (gemv_small)
+    // The K-chunk sum's divisors, set by the launcher: column tiles, lanes per row
+    // (bn / 4), and the RoPE head size (2 without RoPE).
+    FastDiv div_tiles, div_lpr, div_rd;
 };
 
 __device__ __forceinline__ float to_f(float x) { return x; }
@@ -414,14 +417,15 @@ __global__ __launch_bounds__(kReduceThreads)
 void gemv_reduce4(cf_gemv_args_t a, Tiles t) {
     static_assert(KS <= kMaxKSplit, "K chunks");
     const int ntiles = t.start[a.nseg], bn = t.bn;
-    const int lpr = bn / 4, rpw = kReduceThreads / lpr;   // lanes per row, rows per wave
+    const int lpr = bn / 4, rpw = fastdiv(kReduceThreads, t.div_lpr);   // lanes per row, rows per wave
     const int ncols = ntiles * bn;
     const size_t plane = (size_t)a.M * ncols;
     advance_lengths(a);
-    const int tile = (int)(blockIdx.x % (unsigned)ntiles), rb = (int)(blockIdx.x / (unsigned)ntiles);
-    const int m = rb * rpw + (int)threadIdx.x / lpr;
+    const int rb = fastdiv((int)blockIdx.x, t.div_tiles), tile = (int)blockIdx.x - rb * ntiles;
+    const int tq = fastdiv((int)threadIdx.x, t.div_lpr);
+    const int m = rb * rpw + tq;
     if (m >= a.M) return;
-    const int lc = 4 * ((int)threadIdx.x % lpr);
+    const int lc = 4 * ((int)threadIdx.x - tq * lpr);
     const int seg = seg_of(a, t, tile);
     const cf_gemv_seg_t& sg = a.seg[seg];
     const int n = (tile - t.start[seg]) * bn + lc;        // segment-local column
@@ -447,7 +451,7 @@ void gemv_reduce4(cf_gemv_args_t a, Tiles t) {
     const int rd = a.rope_table ? a.rope_d : 2;
     const float2* tb = a.rope_table ? (const float2*)a.rope_table + (rotate ? pos : 0) * (rd >> 1)
                                     : (const float2*)dummy;
-    const float2 c0 = tb[(n % rd) >> 1], c1 = tb[((n + 2) % rd) >> 1];
+    const float2 c0 = tb[(n - fastdiv(n, t.div_rd) * rd) >> 1], c1 = tb[(n + 2 - fastdiv(n + 2, t.div_rd) * rd) >> 1];
     const float2 cs[2] = {rotate ? c0 : float2{1.f, 0.f}, rotate ? c1 : float2{1.f, 0.f}};
     f4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -543,7 +547,7 @@ void gemv_small(cf_gemv_args_t a, Tiles t) {
     const int rd = a.rope_table ? a.rope_d : 2;
     const float2* tb = a.rope_table ? (const float2*)a.rope_table + (rotate ? pos : 0) * (rd >> 1)
                                     : (const float2*)stand_in;
-    const float2 c0 = tb[(n % rd) >> 1], c1 = tb[((n + 2) % rd) >> 1];
+    const float2 c0 = tb[(n - fastdiv(n, t.div_rd) * rd) >> 1], c1 = tb[(n + 2 - fastdiv(n + 2, t.div_rd) * rd) >> 1];
     const float2 rot[2] = {rotate ? c0 : float2{1.f, 0.f}, rotate ? c1 : float2{1.f, 0.f}};
 #pragma unroll
     for (int j = 0; j < XPT; j++)
@@ -570,16 +574,22 @@ void gemv_small(cf_gemv_args_t a, Tiles t) {
             }
         }
     }
-    // Sum over the rows of the wave (lanes with the same column group c), then store the
-    // wave's 16 column sums per batch row.
+    // Sum over the rows of the wave (lanes with the same column group c = lane % LPR):
+    // inside each 16-lane row by DPP rotations of LPR, 2 LPR, .. 8 lanes, then across rows
+    // with the row swaps (no LDS round trip); lanes lr == 0 store the wave's 16 column
+    // sums per batch row.
+    static_assert(LPR == 2 || LPR == 4, "column groups");
 #pragma unroll
     for (int m = 0; m < kSmallMaxM; m++) {
         if (m >= M) break;
 #pragma unroll
         for (int v = 0; v < VEC; v++) {
-#pragma unroll
-            for (int off = LPR; off < 64; off <<= 1) acc[m][v] += __shfl_xor(acc[m][v], off, 64);
-            if (lr == 0) wsum[wave][m][c * VEC + v] = acc[m][v];
+            float x = acc[m][v];
+            if constexpr (LPR == 2) x += dpp_f<kDppRor + 2>(x);
+            x += dpp_f<kDppRor + 4>(x);
+            x += dpp_f<kDppRor + 8>(x);
+            x = add_xor32(add_xor16(x));
+            if (lr == 0) wsum[wave][m][c * VEC + v] = x;
         }
     }
     __syncthreads();
@@ -711,10 +721,12 @@ extern "C" int cf_launch_gemv(const cf_gemv_args_t* a, void* stream) {
     args.k_split = t.ks;
     hipStream_t s = (hipStream_t)stream;
     if (t.small) {
+        Tiles ts = t;
+        ts.div_rd = fastdiv_make(a->rope_table ? (int)a->rope_d : 2);
         if (a->elem == CF_ELEM_F16)
-            hipLaunchKernelGGL(gemv_small<_Float16>, dim3((unsigned)t.start[a->nseg]), dim3(kThreads), 0, s, args, t);
+            hipLaunchKernelGGL(gemv_small<_Float16>, dim3((unsigned)t.start[a->nseg]), dim3(kThreads), 0, s, args, ts);
         else
-            hipLaunchKernelGGL(gemv_small<float>, dim3((unsigned)t.start[a->nseg]), dim3(kThreads), 0, s, args, t);
+            hipLaunchKernelGGL(gemv_small<float>, dim3((unsigned)t.start[a->nseg]), dim3(kThreads), 0, s, args, ts);
         return (int)hipGetLastError();
     }
     const int m_tiles = (a->M + kMTile - 1) / kMTile;
@@ -734,12 +746,16 @@ extern "C" int cf_launch_gemv(const cf_gemv_args_t* a, void* stream) {
     // A wave per (column tile, kReduceThreads / (bn / 4) rows).
     const int rpw = kReduceThreads / (t.bn / 4);
     const dim3 rgrid((unsigned)(t.start[a->nseg] * ((a->M + rpw - 1) / rpw)));
+    Tiles tr = t;
+    tr.div_tiles = fastdiv_make(t.start[a->nseg]);
+    tr.div_lpr = fastdiv_make(t.bn / 4);
+    tr.div_rd = fastdiv_make(a->rope_table ? (int)a->rope_d : 2);
     auto reduce = [&](auto ks_c) {
         constexpr int KS = decltype(ks_c)::value;
         if (a->elem == CF_ELEM_F16)
-            hipLaunchKernelGGL((gemv_reduce4<_Float16, KS>), rgrid, dim3(kReduceThreads), 0, s, args, t);
+            hipLaunchKernelGGL((gemv_reduce4<_Float16, KS>), rgrid, dim3(kReduceThreads), 0, s, args, tr);
         else
-            hipLaunchKernelGGL((gemv_reduce4<float, KS>), rgrid, dim3(kReduceThreads), 0, s, args, t);
+            hipLaunchKernelGGL((gemv_reduce4<float, KS>), rgrid, dim3(kReduceThreads), 0, s, args, tr);
     };
     if (t.ks <= 4) reduce(std::integral_constant<int, 4>{});
     else if (t.ks <= 8) reduce(std::integral_constant<int, 8>{});
