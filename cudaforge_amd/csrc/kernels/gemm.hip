@@ -28,6 +28,8 @@
 
 #include <atomic>
 
+#include <climits>
+
 #include "kernels.h"
 #include "cdna4.h"
 
@@ -946,22 +948,66 @@ void gemm_f16_ws(cf_gemm_args_t a, Tiling t) {
         const _Float16* w_ptr[W_PW];
         uint32_t w_step[W_PW];
         int nw = 0;
+        // A chunk's segment, base, width and first column.  A tile inside one segment
+        // takes them wave-uniform; a tile over two segments picks one of two uniform sets
+        // per chunk by one compare against the boundary; only a tile over three (segments
+        // narrower than a tile) makes the three-way choice per chunk, whose selects and
+        // 64-bit arithmetic, done for every tile, had delayed every product's first W
+        // loads.  Pointers are selected, never indexed per lane: a per-lane index into the
+        // argument block would move it to scratch memory.
+        const _Float16* const wb0 = (const _Float16*)a.w[0];
+        const _Float16* const wb1 = a.nseg > 1 ? (const _Float16*)a.w[1] : wb0;
+        const _Float16* const wb2 = a.nseg > 2 ? (const _Float16*)a.w[2] : wb1;
+        const int ns0 = a.n[0], ns1 = a.nseg > 1 ? a.n[1] : ns0, ns2 = a.nseg > 2 ? a.n[2] : ns1;
+        const int st1 = a.nseg > 1 ? start[1] : INT_MAX, st2 = a.nseg > 2 ? start[2] : INT_MAX;
+        const int last = n0 + BN - 8;
+        const int s_lo = n0 >= st2 ? 2 : n0 >= st1 ? 1 : 0, s_hi = last >= st2 ? 2 : last >= st1 ? 1 : 0;
+        if (s_hi == s_lo) {
+            // One segment (every tile of a one-segment product, most of a Q|K|V one):
+            // wave-uniform base, width and start.
+            const _Float16* const wb = s_lo == 2 ? wb2 : s_lo == 1 ? wb1 : wb0;
+            const int ns = s_lo == 2 ? ns2 : s_lo == 1 ? ns1 : ns0;
+            const int st = s_lo == 2 ? st2 : s_lo == 1 ? st1 : 0;
 #pragma unroll
-        for (int v = 0; v < W_PW; v++) {
-            const int u = cw + 4 * v;
-            nw += u < W_INSTR ? 1 : 0;
-            const int q = min(64 * u + lane, W_CH - 1);
-            const int r = q / WCPR, c = min(q % WCPR, BN / 8 - 1);
-            int col;
-            const int s = ws_seg(a, start, n0 + 8 * c, col);
-            // Offsets from segment 0, not a.w[s] / a.n[s]: a per-lane index into the
-            // argument block would copy it to scratch memory.
-            const _Float16* w0 = (const _Float16*)a.w[0];
-            const _Float16* wbase = w0 + (s == 1 ? (const _Float16*)a.w[1] - w0 : (ptrdiff_t)0) +
-                                    (s == 2 ? (const _Float16*)a.w[2] - w0 : (ptrdiff_t)0);
-            const int ns = a.n[0] + (s == 1 ? a.n[1] - a.n[0] : 0) + (s == 2 ? a.n[2] - a.n[0] : 0);
-            w_ptr[v] = wbase + (size_t)r * ns + col;
-            w_step[v] = (uint32_t)(WS_BK * ns);
+            for (int v = 0; v < W_PW; v++) {
+                const int u = cw + 4 * v;
+                nw += u < W_INSTR ? 1 : 0;
+                const int q = min(64 * u + lane, W_CH - 1);
+                const int r = q / WCPR, c = min(q - r * WCPR, BN / 8 - 1);
+                w_ptr[v] = wb + ((size_t)r * ns + (n0 + 8 * c - st));
+                w_step[v] = (uint32_t)(WS_BK * ns);
+            }
+        } else if (s_hi - s_lo == 1) {
+            const _Float16* const wlo = s_lo == 2 ? wb2 : s_lo == 1 ? wb1 : wb0;
+            const _Float16* const whi = s_hi == 2 ? wb2 : s_hi == 1 ? wb1 : wb0;
+            const int nlo = s_lo == 2 ? ns2 : s_lo == 1 ? ns1 : ns0, nhi = s_hi == 2 ? ns2 : s_hi == 1 ? ns1 : ns0;
+            const int slo = s_lo == 2 ? st2 : s_lo == 1 ? st1 : 0;
+            const int shi = s_hi == s_lo ? INT_MAX : s_hi == 2 ? st2 : st1;   // the boundary, if any
+#pragma unroll
+            for (int v = 0; v < W_PW; v++) {
+                const int u = cw + 4 * v;
+                nw += u < W_INSTR ? 1 : 0;
+                const int q = min(64 * u + lane, W_CH - 1);
+                const int r = q / WCPR, c = min(q - r * WCPR, BN / 8 - 1);
+                const int gc = n0 + 8 * c;
+                const bool hi = gc >= shi;
+                const int ns = hi ? nhi : nlo;
+                w_ptr[v] = (hi ? whi : wlo) + ((size_t)r * ns + (gc - (hi ? shi : slo)));
+                w_step[v] = (uint32_t)(WS_BK * ns);
+            }
+        } else {
+#pragma unroll
+            for (int v = 0; v < W_PW; v++) {
+                const int u = cw + 4 * v;
+                nw += u < W_INSTR ? 1 : 0;
+                const int q = min(64 * u + lane, W_CH - 1);
+                const int r = q / WCPR, c = min(q - r * WCPR, BN / 8 - 1);
+                const int gc = n0 + 8 * c;
+                const bool in1 = gc >= st1, in2 = gc >= st2;     // start[2] >= start[1]: in2 implies in1
+                const int ns = in2 ? ns2 : in1 ? ns1 : ns0;
+                w_ptr[v] = (in2 ? wb2 : in1 ? wb1 : wb0) + ((size_t)r * ns + (gc - (in2 ? st2 : in1 ? st1 : 0)));
+                w_step[v] = (uint32_t)(WS_BK * ns);
+            }
         }
         const uint32_t lds0 = lds_offset(smem);
         const uint32_t a_lds = __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)(A_PW * cw) * 1024u);

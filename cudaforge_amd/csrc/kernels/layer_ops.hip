@@ -9,14 +9,11 @@
 #include <stdint.h>
 
 #include "kernels.h"
+#include "cdna4.h"
 
 namespace {
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
+using cdna4::wave_sum;   // DPP and row swaps: no LDS round trip per reduction step
 
 template <typename T> struct Vec4;
 template <> struct Vec4<float> { typedef float type __attribute__((ext_vector_type(4))); };
