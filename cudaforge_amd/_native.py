@@ -118,6 +118,7 @@ def _proto(lib):
         "cf_decode_attn_set_wide": (None, [c_int32]),
         "cf_decode_attn_set_kreg": (None, [c_int32]),
         "cf_decode_attn_kreg_ok": (c_int32, [c_int32]),
+        "cf_fastdiv_quotient": (c_int32, [c_int32, c_int32]),
         "cf_gemm_set_stages": (None, [c_int32]),
         "cf_gemm_set_group_m": (None, [c_int32]),
         "cf_gemm_set_bn": (None, [c_int32]),

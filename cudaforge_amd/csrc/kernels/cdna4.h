@@ -37,7 +37,7 @@ __host__ inline FastDiv fastdiv_make(int d) {
     const uint32_t shift = 31 + l;
     return FastDiv{(uint32_t)(((1ull << shift) + (uint64_t)d - 1) / (uint64_t)d), shift};
 }
-__device__ __forceinline__ int fastdiv(int n, FastDiv f) {
+__host__ __device__ __forceinline__ int fastdiv(int n, FastDiv f) {
     return (int)(((uint64_t)(uint32_t)n * f.mul) >> f.shift);
 }
 

@@ -47,6 +47,9 @@ typedef struct {
 } cf_decode_attn_args_t;
 
 /* Positions one workgroup pass covers (chunk must be a multiple); 0 = generic kernel. */
+/* n / d (0 <= n < 2^31, d >= 1) by the multiply-and-shift divisor the kernels take at
+ * launch, computed on the host (checks of that arithmetic). */
+int32_t cf_fastdiv_quotient(int32_t n, int32_t d);
 int32_t cf_decode_attn_chunk_quantum(int32_t elem, int32_t d, int32_t group);
 int32_t cf_decode_attn_chunk_max(int32_t elem, int32_t d, int32_t group);
 /* Workgroups of the fp16 split kernel that fit one CU (its LDS ring bounds it), or 0

@@ -4,6 +4,7 @@
 #include <stdint.h>
 
 #include "kernels.h"
+#include "cdna4.h"
 
 namespace {
 
@@ -82,6 +83,12 @@ extern "C" int cf_launch_fill_normal(void* out, size_t n, int elem, uint64_t see
         hipLaunchKernelGGL(fill_normal_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
                            (float*)out, n, seed, mean, stddev);
     return (int)hipGetLastError();
+}
+
+// The kernels' launch-time divisor (cdna4::FastDiv), run on the host for checking:
+// n / d through the same multiplier and shift the kernels use.
+extern "C" int32_t cf_fastdiv_quotient(int32_t n, int32_t d) {
+    return cdna4::fastdiv(n, cdna4::fastdiv_make(d));
 }
 
 extern "C" int cf_launch_copy_bytes(void* dst, const void* src, size_t bytes, void* stream) {

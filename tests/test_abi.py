@@ -383,3 +383,27 @@ def test_graph_decode_length_past_capacity_cpu(cpu_ops):
     lib.graph_update_cache_len(g.g, 8)
     assert lib.graph_execute(g.g, ins, outs, False) == -1
     g.destroy()
+
+
+def test_launch_time_divisor_is_exact(native):
+    """The kernels divide grid and row indices by launch-time values through a multiplier
+    and shift (cdna4.h FastDiv), exact for 0 <= n < 2^31.  The same source runs on the
+    host here: every n below 70 000 for divisors 1..300, the largest n, powers of two and
+    their neighbours, and random pairs across the range, against integer division."""
+    q = native.cf_fastdiv_quotient
+    rng = np.random.default_rng(2026)
+    top = 2**31 - 1
+    for d in range(1, 301):
+        ns = np.arange(0, 70000, 7 if d > 40 else 1)
+        assert all(q(int(n), d) == n // d for n in ns), d
+        for n in (top, top - 1, top - d, 2**30, 2**30 - 1, d * (top // d), d * (top // d) - 1):
+            assert q(n, d) == n // d, (n, d)
+    for k in range(31):
+        for d in (2**k - 1, 2**k, 2**k + 1):
+            if d >= 1:
+                for n in (0, 1, d - 1, d, d + 1, top, top - 1):
+                    assert q(n, d) == n // d, (n, d)
+    for n, d in zip(rng.integers(0, top, 20000), rng.integers(1, top, 20000)):
+        assert q(int(n), int(d)) == int(n) // int(d), (n, d)
+    for n, d in zip(rng.integers(0, top, 20000), rng.integers(1, 5000, 20000)):
+        assert q(int(n), int(d)) == int(n) // int(d), (n, d)
