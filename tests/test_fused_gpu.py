@@ -236,12 +236,14 @@ WS_SHAPES = [(256, 192), (256, 144), (256, 128), (256, 96), (256, 64), (256, 48)
              (128, 96), (128, 64)]
 
 
-@pytest.mark.parametrize("H,H_kv", [(6, 6), (6, 2)])
+@pytest.mark.parametrize("H,H_kv", [(6, 6), (6, 2), (7, 1)])
 def test_gemm_wave_specialised_shapes_agree(gpu, native, H, H_kv):
     """The wave-specialised fp16 projection GEMM at each of its tiles (a tile that does not
     fit a product leaves that product to the cost model's choice).  D = 384, M = 256: the
     QKV product's 144-column tiles straddle the Q|K and K|V boundaries; WO carries a bias
-    and a residual (fp32 staging); H_kv = 2 gives K and V segments narrower than Q.  Every
+    and a residual (fp32 staging); H_kv = 2 gives K and V segments narrower than Q, and
+    H = 7, H_kv = 1 a 192-column tile over the end of Q and all of K and V (the loaders'
+    three-way segment choice; the other tiles take the one- and two-segment ones).  Every
     run within the FP16 bound of the oracle and bit-identical to the others (each output
     element sums the same 32-k MFMA steps in the same order), and within a few fp16 ulps
     of the kernels it replaces and of the default choice (the QKV product keeps the
