@@ -388,7 +388,10 @@ void flash_f16_dma64(cf_flash_args_t a, int pairs, FastDiv div_slot, FastDiv div
             }
 
     const float c = a.scale * kLog2e;
-    const h8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
+    h8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
+    // Held in VGPRs for the whole loop: kept as a scalar constant, it was moved into
+    // VGPRs before the row-sum MFMAs of every block (two VALU moves per block).
+    asm volatile("" : "+v"(ones));
     float m_run[NJ];
     f4_t acc[NJ][UT], lsum[NJ];                    // lsum: every element is the query's sum of p
 #pragma unroll
